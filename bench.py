@@ -1,0 +1,156 @@
+"""Benchmark: batch-1 greedy decode of the 8B-shaped Q2_0 model at 2k context.
+
+Workload (the north-star config): d_model 4096, 36
+layers, 32 q / 8 kv heads x 128, SwiGLU 12288, vocab 151936; Q2_0 layer weights
+and Q8_0 embedding/head synthesized on the device from a seed; f32 KV cache
+pre-filled at positions 0..2047 with seeded N(0,1) values rounded to fp16; then
+greedy decode (repetition penalty 1.1, the reference default) from position 2048.
+A "step" is one decode forward (one token).  Timed region: K steps on the device
+stream, bracketed by synchronize + hipEvents inside the library.
+
+Also reported: per-stage device times (hipEvents) for layer 0, the roofline of
+the dominant kernel (the fused gate/up Q2_0 GEMV), and the CPU baseline — the
+oracle's restatement of Hearth's CPU path (AVX2 LUT Q2_0 arm, pool.rs row
+partitioning) timed on the host's cores on a bounded sample of the same work.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "decode tok/s @bs1, 8B Q2_0 2k ctx; Q1/Q2 GEMV HBM GB/s vs peak"
+
+
+def step_bytes(cfg, seq_len: int) -> dict:
+    """Algorithmic HBM bytes of one decode step at attention length seq_len."""
+    from hearth_amd import row_bytes
+    d, L, hd = cfg.d_model, cfg.n_layers, cfg.head_dim
+    nq, nkv = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    rb = lambda k: row_bytes(cfg.wtype, k)
+    w_layer = (nq + 2 * nkv) * rb(d) + d * rb(nq) + 2 * cfg.d_ffn * rb(d) + d * rb(cfg.d_ffn)
+    head = cfg.vocab * row_bytes(cfg.head_type, d)
+    kv_read = L * 2 * cfg.n_kv_heads * seq_len * hd * 4
+    kv_write = L * 2 * nkv * 4
+    norms = L * (2 * d + 2 * hd) * 4 + d * 4
+    small = row_bytes(cfg.head_type, d) + cfg.vocab * 4
+    return {"weights": L * w_layer, "head": head, "kv": kv_read + kv_write, "other": norms + small,
+            "total": L * w_layer + head + kv_read + kv_write + norms + small,
+            "gate_up": 2 * cfg.d_ffn * rb(d) + d * 4 * 2 + cfg.d_ffn + cfg.d_ffn // 32 * 8}
+
+
+def cpu_baseline(model, cfg, seed, kv_seed, tok0, budget_s: float):
+    """The oracle's restatement of Hearth's CPU decode, same weights (downloaded),
+    T = host cores, AVX2 arm; decode steps until ~budget_s of CPU work."""
+    from oracle import oracle as orc
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(threads, 16))
+    o = orc.OracleModel(cfg, seed=None, threads=threads, arm=1)
+    for name, t, ne0, ne1, nb in model.tensors():
+        o.tensor(name)[:] = model.download(name, nb)
+    o.prefill_kv_synthetic(kv_seed, 2048)
+    tok, pos, n = tok0, 2048, 0
+    t0 = time.perf_counter()
+    while True:
+        lg = o.forward(tok, pos)
+        tok = int(np.argmax(lg))
+        pos += 1
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= 64:
+            break
+    o.close()
+    avx2 = bool(orc.load().ho_have_avx2())
+    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps of the 8B Q2_0 config from pos 2048 (f32 KV), "
+                      f"{'AVX2 LUT' if avx2 else 'scalar'} Q2_0 arm, {threads} threads, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--layers", type=int, default=0, help="override layer count (debug only)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs one GPU per process: bench.py measures --gpus 1 only; "
+                                   "see DESIGN.md for how the decode path would shard"}))
+        sys.exit(2)
+
+    from hearth_amd import Ctx, Model, CONFIGS
+    cfg = CONFIGS["8b-q2"]
+    if args.layers:
+        cfg = cfg.replace(n_layers=args.layers)
+    seed, kv_seed = 2026, 77
+    K, W = args.steps, args.warmup
+    cfg = cfg.replace(max_seq=max(cfg.max_seq, 2048 + max(K, W) + 8))
+    ctx = Ctx(0)
+    m = Model(ctx, cfg)
+    m.synthesize(seed)
+    m.prefill_kv_synthetic(kv_seed, 2048)
+    from_seed = np.random.default_rng(seed)
+    tok0 = int(from_seed.integers(0, cfg.vocab))
+    print(f"[bench] model ready: 8B Q2_0, {cfg.n_layers} layers; warmup {W}, steps {K}", file=sys.stderr, flush=True)
+    if W:
+        m.generate([tok0], W + 1, start_pos=2048, repeat_pen=1.1)
+    ctx.sync()
+    t0 = time.perf_counter()
+    toks, _ = m.generate([tok0], K + 1, start_pos=2048, repeat_pen=1.1)
+    wall = time.perf_counter() - t0
+    dev_ms = m.last_decode_ms()
+    ms_per_step = dev_ms / K
+    tps = 1000.0 / ms_per_step
+    print(f"[bench] {K} steps: device {dev_ms:.2f} ms ({ms_per_step:.4f} ms/step), wall {wall*1e3:.1f} ms",
+          file=sys.stderr, flush=True)
+    mean_seq = 2048 + 1 + (K - 1) / 2.0 + 1
+    b = step_bytes(cfg, int(round(mean_seq)))
+    stage = m.time_stages(layer=0, iters=50)
+    print(f"[bench] stage ms (layer 0): {json.dumps(stage)}", file=sys.stderr, flush=True)
+    gu_ms = stage["gate_up"]
+    gu_gbs = b["gate_up"] / (gu_ms * 1e-3) / 1e9
+    step_gbs = b["total"] * tps / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded device-generated Q2_0/Q8_0 weights, seeded fp16-valued KV prefill)",
+        "config": {"workload": "8B-shaped Q2_0 dense decoder, batch 1, KV prefilled to 2048, greedy decode",
+                   "d_model": cfg.d_model, "layers": cfg.n_layers, "heads": f"{cfg.n_heads}q/{cfg.n_kv_heads}kv x {cfg.head_dim}",
+                   "d_ffn": cfg.d_ffn, "vocab": cfg.vocab, "kv_dtype": "f32", "repeat_pen": 1.1,
+                   "bytes_per_step": b["total"], "parallelism": "single GPU"},
+        "step_hbm": {"achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(step_gbs / PEAK_HBM_GBS, 4)},
+        "roofline": {"bound": "hbm", "kernel": "k_gemv<Q2,RMSNORM,SILU> (fused gate+up, layer 0)",
+                     "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": b["gate_up"]},
+        "stage_ms": {k: round(v, 5) for k, v in stage.items()},
+        "first_tokens": [int(t) for t in toks[:8]],
+    }
+    if not args.no_cpu:
+        try:
+            out["cpu_baseline"] = cpu_baseline(m, cfg, seed, kv_seed, tok0, args.cpu_budget)
+        except Exception as e:  # the GPU number stands on its own
+            out["cpu_baseline"] = {"error": repr(e)}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

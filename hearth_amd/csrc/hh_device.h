@@ -1,0 +1,116 @@
+// hh_device.h — device-side helpers shared by the gfx950 kernels.
+//
+// Formats (crates/hearth-gguf/src/ggml.rs:49-53, :105-171):
+//   Q8_0 : 32 el / 34 B  [f16 d][32 x i8]                    (q8_0.rs:4-51)
+//   Q1_0 : 128 el / 18 B [f16 d][16 B sign bits, LSB first]  (q1_0g128.rs:75-98)
+//   Q2_0 : 128 el / 34 B [f16 d][32 B 2-bit codes, LSB first, w = code-1] (q2_0.rs:66-84)
+//
+// Weights stay in that native layout in HBM.  A GEMV lane works on a "unit" of
+// whole blocks whose byte size is a multiple of 4 (so one dword-aligned 68- or
+// 36-byte load feeds it): Q2_0 2 blocks (256 el, 68 B), Q1_0 2 blocks (256 el,
+// 36 B), Q8_0 2 blocks (64 el, 68 B).  Rows are contiguous, so a matrix is a flat
+// array of units and consecutive lanes read consecutive units.
+//
+// Activations enter the GEMV as a "packed" Q8_0 vector: the same int8 values and
+// f16 scales as Q8_0 (bit-exact with q8_0.rs:20-51), stored as
+//   q[K] int8, permuted within 16/32-element chunks to match the weight format's
+//        bit-extraction order (so one AND + one v_dot4 handles 4 elements),
+//   d[K/32] f32 (the f16 scale widened), s[K/32] int32 (sum of q per block; lets
+//        the unsigned 2-bit codes stand in for code-1 and bits for +-1).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define HH_DEV __device__ __forceinline__
+
+enum : int { FMT_Q8 = 0, FMT_Q1 = 1, FMT_Q2 = 2 };
+
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+template <int FMT> struct UnitT;
+template <> struct UnitT<FMT_Q2> { static constexpr int EL = 256, DW = 17, BYTES = 68, SUBS = 8; };
+template <> struct UnitT<FMT_Q1> { static constexpr int EL = 256, DW = 9, BYTES = 36, SUBS = 8; };
+template <> struct UnitT<FMT_Q8> { static constexpr int EL = 64, DW = 17, BYTES = 68, SUBS = 2; };
+
+// LDS stride of one unit's int8 activations (16 B pad spreads units over banks).
+template <int FMT> HH_DEV constexpr int qstride() { return UnitT<FMT>::EL + 16; }
+
+HH_DEV float h2f(uint32_t h16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(h16 & 0xffffu)); }
+HH_DEV uint32_t f2h(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// Position of element e (within the vector) in the permuted int8 array.
+//   Q2: chunk of 16; element 4i+k -> k*4+i     (matches (D >> 2k) & 0x03030303)
+//   Q1: chunk of 32; element 8i+j -> j*4+i     (matches (D >> j)  & 0x01010101)
+HH_DEV int perm_pos(int fmt, int e) {
+  if (fmt == FMT_Q2) { int r = e & 15; return (e & ~15) | ((r & 3) << 2) | (r >> 2); }
+  if (fmt == FMT_Q1) { int r = e & 31; return (e & ~31) | ((r & 7) << 2) | (r >> 3); }
+  return e;
+}
+// Same, with the per-unit LDS padding applied.
+HH_DEV int lds_qpos(int fmt, int e) {
+  int p = perm_pos(fmt, e);
+  if (fmt == FMT_Q8) return (p >> 6) * 80 + (p & 63);
+  return (p >> 8) * 272 + (p & 255);
+}
+
+// Q8_0 quantization of one value given the block's f32 scale (q8_0.rs:44):
+// (x / scale).round().clamp(-128, 127) as i8 ; NaN -> 0 as Rust's `as` does.
+HH_DEV int q8_round(float x, float scale) {
+  float v = roundf(x / scale);
+  v = fminf(fmaxf(v, -128.0f), 127.0f);
+  return (v != v) ? 0 : (int)v;
+}
+// q8_0.rs:35: scale = max_abs == 0 ? 1 : max_abs / 127.
+HH_DEV float q8_scale(float amax) { return amax == 0.0f ? 1.0f : amax / 127.0f; }
+
+// ---- wave helpers (wave64) ----
+HH_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+HH_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// Reductions over aligned groups of W lanes (W power of two <= 64).
+template <int W> HH_DEV float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+template <int W> HH_DEV int group_sum_i(int v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ---- counter-based seeded generator (shared definition with the CPU checker) ----
+HH_DEV uint64_t mix64(uint64_t x) {
+  x ^= x >> 30;
+  x *= 0xbf58476d1ce4e5b9ull;
+  x ^= x >> 27;
+  x *= 0x94d049bb133111ebull;
+  x ^= x >> 31;
+  return x;
+}
+HH_DEV int32_t synth_int(uint64_t key, uint64_t idx) {
+  uint64_t h = mix64(key + idx * 0x9e3779b97f4a7c15ull);
+  int32_t s = (int32_t)(h & 0xffff) + (int32_t)((h >> 16) & 0xffff) + (int32_t)((h >> 32) & 0xffff) +
+              (int32_t)(h >> 48);
+  return s - 131070;
+}
+
+// Device-side step state: the token loop runs without host round trips.
+struct StepState {
+  int pos;        // position of the token being fed
+  int step;       // steps executed in this session
+  int token;      // token being fed
+  int n_prompt;   // prompt length (steps < n_prompt-1 take the next prompt token)
+  int update;     // 1: record argmax + repetition counts (generate), 0: forward only
+  int argmax;     // last greedy choice
+  int cancel;     // host-set cancel flag
+  float pen;      // repetition penalty for the dense greedy rule
+};

@@ -1,0 +1,186 @@
+// hh_gdn.hip — Gated-DeltaNet decode step for the qwen35 hybrids (gfx950).
+//
+// Restates qwen35.rs:1239-1492 (gdn_layer, no Hadamard fold):
+//   conv window prepare/push + depthwise conv (k taps) + silu   :1294-1303, :1820-1829, :264-315
+//   per-head L2 norm of q and k, 1/sqrt(sum x^2 + eps)          :1332-1347
+//   g = softplus(alpha + dt_bias) * ssm_a ; beta = sigmoid(b)    :1359-1363, :1809-1815
+//   alpha/beta = dense f32 [n_v x d] matvec of the normed input  :1285-1291, :1015-1025
+//   per v-head h, k-group h % n_k:                               :1371-1404
+//     dot_j = sum_i S[i][j] k[i]  (state before decay)
+//     S[i][j] = S[i][j]*exp(g) + k[i] * beta*(v_j - dot_j)
+//     o_j = sum_i S[i][j] q[i] / sqrt(hd)
+//   gated RMSNorm: rms_norm(o_h, ssm_norm) * silu(z)             :1427-1439
+// The fp32 state [n_v][hd][hd] stays resident in HBM; it is read and written
+// once per token.
+//
+// Kernel 1 (prep): workgroups [0, conv_dim/256) do conv + silu (+ L2 norm for
+//   the q/k channels, 2 heads of 128 per workgroup); the remaining workgroups
+//   compute alpha/beta for 4 v-heads each from rms_norm(hidden, attn_norm).
+// Kernel 2 (recurrence): workgroup (h, 32-column slice) updates its columns;
+//   the last of a head's workgroups applies the gated norm and writes the
+//   packed Q8_0 input of ssm_out.
+#include "hh_kernels.h"
+
+namespace {
+
+HH_DEV float softplus_f(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+
+__global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
+  const int n_conv_wg = conv_dim / 256;
+  __shared__ float red[8];
+  if ((int)blockIdx.x < n_conv_wg) {
+    const int ch = blockIdx.x * 256 + tid;
+    const int K = a.kernel;
+    float win[8];
+    float* cs = a.conv_state + (size_t)ch * (K - 1);
+    for (int t = 0; t < K - 1; ++t) win[t] = cs[t];
+    win[K - 1] = a.proj[ch];
+    for (int t = 0; t < K - 1; ++t) cs[t] = win[t + 1];
+    const float* w = a.conv_w + (size_t)ch * K;
+    float acc = 0.0f;
+    for (int t = 0; t < K; ++t) acc += w[t] * win[t];
+    float y = acc / (1.0f + expf(-acc));             // silu
+    if (ch < 2 * kdim) {
+      // L2 norm over the 128-channel head this lane belongs to (2 waves per head)
+      float ss = wave_sum(y * y);
+      if (lane == 0) red[wid] = ss;
+      __syncthreads();
+      int hw = wid & ~1;
+      float tot = red[hw] + red[hw + 1];
+      float inv = 1.0f / sqrtf(tot + a.eps);
+      a.qk[ch] = y * inv;
+    } else {
+      a.vconv[ch - 2 * kdim] = y;
+    }
+    return;
+  }
+  // alpha/beta for v-heads [4*j, 4*j+4)
+  extern __shared__ float xs[];   // d floats: rms_norm(hidden, attn_norm)
+  const int d = a.d;
+  float ss = 0.0f;
+  for (int i = tid; i < d; i += 256) ss += a.hidden[i] * a.hidden[i];
+  ss = wave_sum(ss);
+  if (lane == 0) red[wid] = ss;
+  __syncthreads();
+  float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  float inv = 1.0f / sqrtf(tot / (float)d + a.eps);
+  for (int i = tid; i < d; i += 256) xs[i] = a.hidden[i] * inv * a.attn_norm[i];
+  __syncthreads();
+  int h = ((int)blockIdx.x - n_conv_wg) * 4 + wid;
+  if (h >= a.n_v) return;
+  const float* wa = a.w_alpha + (size_t)h * d;
+  const float* wb = a.w_beta + (size_t)h * d;
+  float sa = 0.0f, sb = 0.0f;
+  for (int i = lane; i < d; i += 64) {
+    sa += wa[i] * xs[i];
+    sb += wb[i] * xs[i];
+  }
+  sa = wave_sum(sa);
+  sb = wave_sum(sb);
+  if (lane == 0) {
+    a.ab[h] = softplus_f(sa + a.dt_bias[h]) * a.ssm_a[h];
+    a.ab[a.n_v + h] = 1.0f / (1.0f + expf(-sb));
+  }
+}
+
+// workgroup (h, jb): columns j in [jb*32, jb*32+32), thread = (i-chunk ic, column jj)
+__global__ __launch_bounds__(256) void k_gdn_rec(GdnArgs a) {
+  const int tid = threadIdx.x;
+  const int hd = a.hd;                       // 128
+  const int h = blockIdx.x / (hd / 32), jb = blockIdx.x % (hd / 32);
+  const int jj = tid & 31, ic = tid >> 5;    // 8 chunks of 16 rows
+  const int j = jb * 32 + jj;
+  const int kg = h % a.n_k;
+  const int kdim = a.n_k * hd;
+  const float* qn = a.qk + (size_t)kg * hd;
+  const float* kn = a.qk + kdim + (size_t)kg * hd;
+  const float decay = expf(a.ab[h]);
+  const float b = a.ab[a.n_v + h];
+  float* S = a.state + (size_t)h * hd * hd;
+  __shared__ float part[8][33];
+  __shared__ float kv_s[2][128];
+  __shared__ int is_last;
+  if (tid < hd) { kv_s[0][tid] = kn[tid]; kv_s[1][tid] = qn[tid]; }
+  float sreg[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sreg[r] = S[(size_t)(ic * 16 + r) * hd + j];
+  __syncthreads();
+  float dp = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) dp += sreg[r] * kv_s[0][ic * 16 + r];
+  part[ic][jj] = dp;
+  __syncthreads();
+  float dot = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) dot += part[c][jj];
+  float bd = b * (a.vconv[(size_t)h * hd + j] - dot);
+  float op = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float sn = sreg[r] * decay + kv_s[0][ic * 16 + r] * bd;
+    S[(size_t)(ic * 16 + r) * hd + j] = sn;
+    op += sn * kv_s[1][ic * 16 + r];
+  }
+  __syncthreads();
+  part[ic][jj] = op;
+  __syncthreads();
+  if (ic == 0) {
+    float o = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) o += part[c][jj];
+    a.obuf[(size_t)h * hd + j] = o * (1.0f / sqrtf((float)hd));
+  }
+  // last column-slice of head h: gated RMSNorm + Q8_0 of the head's 128 outputs
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    is_last = atomicAdd(a.counter + h, 1) == hd / 32 - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  if (tid >= 64) return;
+  const int lane = tid;
+  float v0 = a.obuf[(size_t)h * hd + lane], v1 = a.obuf[(size_t)h * hd + 64 + lane];
+  float ss = wave_sum(v0 * v0 + v1 * v1);
+  float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+  float vals[2] = {v0, v1};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    int dd = k * 64 + lane;
+    float nv = vals[k] * inv * a.ssm_norm[dd];
+    float z = a.z[(size_t)h * hd + dd];
+    float o = nv * (z / (1.0f + expf(-z)));
+    if (a.out_f32) a.out_f32[(size_t)h * hd + dd] = o;
+    float am = group_max<32>(fabsf(o));
+    float sc = q8_scale(am);
+    int q = q8_round(o, sc);
+    int qs = group_sum_i<32>(q);
+    int e = h * hd + dd;
+    int Kv = a.n_v * hd;
+    a.act_out[perm_pos(a.act_fmt, e)] = (uint8_t)(int8_t)q;
+    if ((lane & 31) == 0) {
+      ((float*)(a.act_out + Kv))[e >> 5] = h2f(f2h(sc));
+      ((int*)(a.act_out + Kv + (Kv / 32) * 4))[e >> 5] = qs;
+    }
+  }
+  if (lane == 0) {
+    a.counter[h] = 0;
+    __threadfence();
+  }
+}
+
+}  // namespace
+
+int hh_gdn_launch(const GdnArgs& a, hipStream_t s) {
+  const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
+  if (conv_dim % 256 || a.hd != 128 || a.kernel > 8) return 1;
+  int n_conv_wg = conv_dim / 256;
+  int n_ab_wg = (a.n_v + 3) / 4;
+  hipLaunchKernelGGL(k_gdn_prep, dim3(n_conv_wg + n_ab_wg), dim3(256), sizeof(float) * a.d, s, a);
+  if (hipGetLastError() != hipSuccess) return 1;
+  hipLaunchKernelGGL(k_gdn_rec, dim3(a.n_v * (a.hd / 32)), dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}

@@ -1,0 +1,554 @@
+// hh_gemv.hip — quantized GEMV on packed Q8_0 activations for gfx950.
+//
+// Semantics: y[r] = dot_fn(w + r*row_bytes, x_q8, K), dot_fn one of
+//   dot_q2_0_q8_0_ptr   (q2_0.rs:537-574 scalar semantics, :308-392 shipped arm)
+//   dot_q1_0g128_q8_0_ptr (q1_0g128.rs:1113-1152)
+//   dot_q8_0_q8_0_ptr   (q8_0.rs:154-171)
+// over the rows par_dot_rows distributes across CPU workers (pool.rs:510-566).
+// Each 32-element sub-block dot is an exact int32; the fp32 combination
+// (sub-block * d_a, block * d_w) follows the scalar kernels, with the per-row
+// sum split over units and added in a fixed order (deterministic run to run).
+//
+// Mapping: a workgroup (256 lanes) owns a row range; its units (2 blocks each)
+// are taken by consecutive lanes, so each wave load instruction covers one
+// contiguous 4352-byte (Q2/Q8) or 2304-byte (Q1) stretch of HBM.  Weight loads
+// for the first batch are issued before the activation prologue and every
+// later batch is double-buffered in VGPRs, so the prologue (RMSNorm + Q8_0
+// quantization, or a copy) overlaps the first HBM round trip.
+//
+// Prologues:  PRO_PACKED  packed activation from global (written by a producer
+//             PRO_RMSNORM rms_norm(x, w) then Q8_0 (ops.rs:442-487 rms_norm_q8
+//                         semantics with ops.rs:8-35 operation order)
+//             PRO_STDQ8   standard Q8_0 blocks (the DotFn activation format)
+// Epilogues:  EPI_STORE   y[r] = sum
+//             EPI_ADD     y[r] += sum (the residual adds of mod.rs:718-720, :776-778)
+//             EPI_SILU    gate/up pair -> silu(g)*u -> packed Q8_0 (ops.rs:273-306)
+//             EPI_LOGITS  logits, repetition penalty, greedy argmax (sampler lib.rs:26-40,
+//                         :167-175; qwen35.rs:1735-1745), device step-state advance
+#include "hh_kernels.h"
+
+namespace {
+
+enum { PRO_PACKED = 0, PRO_RMSNORM = 1, PRO_STDQ8 = 2 };
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
+
+constexpr uint32_t M2 = 0x03030303u;
+constexpr uint32_t M1 = 0x01010101u;
+
+HH_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+
+// ---- unit dot products: w = unit dwords, aq/ad/as = the unit's activation ----
+HH_DEV float unit_q2(const uint32_t (&w)[17], const int8_t* aq, const float* ad, const int* as) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    uint32_t c[8];
+    float dw;
+    if (blk == 0) {
+      dw = h2f(w[0]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], 16);
+    } else {
+      dw = h2f(w[8] >> 16);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = w[9 + i];
+    }
+    float bacc = 0.0f;
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      const i32x4* A = (const i32x4*)(aq + blk * 128 + sub * 32);
+      i32x4 a0 = A[0], a1 = A[1];
+      uint32_t D0 = c[2 * sub], D1 = c[2 * sub + 1];
+      int s = 0;
+      s = sdot4(D0 & M2, a0.x, s);
+      s = sdot4((D0 >> 2) & M2, a0.y, s);
+      s = sdot4((D0 >> 4) & M2, a0.z, s);
+      s = sdot4((D0 >> 6) & M2, a0.w, s);
+      s = sdot4(D1 & M2, a1.x, s);
+      s = sdot4((D1 >> 2) & M2, a1.y, s);
+      s = sdot4((D1 >> 4) & M2, a1.z, s);
+      s = sdot4((D1 >> 6) & M2, a1.w, s);
+      s -= as[blk * 4 + sub];                 // sum (code-1)*a = sum code*a - sum a
+      bacc += (float)s * ad[blk * 4 + sub];   // block_acc += dot * a_scale
+    }
+    acc += bacc * dw;                         // sum += block_acc * w_scale
+  }
+  return acc;
+}
+
+HH_DEV float unit_q1(const uint32_t (&w)[9], const int8_t* aq, const float* ad, const int* as) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    uint32_t c[4];
+    float dw;
+    if (blk == 0) {
+      dw = h2f(w[0]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], 16);
+    } else {
+      dw = h2f(w[4] >> 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[i] = w[5 + i];
+    }
+    float bacc = 0.0f;
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      const i32x4* A = (const i32x4*)(aq + blk * 128 + sub * 32);
+      i32x4 a0 = A[0], a1 = A[1];
+      uint32_t D = c[sub];
+      int s = 0;
+      s = sdot4(D & M1, a0.x, s);
+      s = sdot4((D >> 1) & M1, a0.y, s);
+      s = sdot4((D >> 2) & M1, a0.z, s);
+      s = sdot4((D >> 3) & M1, a0.w, s);
+      s = sdot4((D >> 4) & M1, a1.x, s);
+      s = sdot4((D >> 5) & M1, a1.y, s);
+      s = sdot4((D >> 6) & M1, a1.z, s);
+      s = sdot4((D >> 7) & M1, a1.w, s);
+      s = 2 * s - as[blk * 4 + sub];          // sum (+-1)*a = 2*sum bit*a - sum a
+      bacc += (float)s * ad[blk * 4 + sub];
+    }
+    acc += bacc * dw;
+  }
+  return acc;
+}
+
+HH_DEV float unit_q8(const uint32_t (&w)[17], const int8_t* aq, const float* ad, const int* /*as*/) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    uint32_t c[8];
+    float dw;
+    if (blk == 0) {
+      dw = h2f(w[0]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], 16);
+    } else {
+      dw = h2f(w[8] >> 16);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = w[9 + i];
+    }
+    const i32x4* A = (const i32x4*)(aq + blk * 32);
+    i32x4 a0 = A[0], a1 = A[1];
+    int s = 0;
+    s = sdot4(c[0], a0.x, s); s = sdot4(c[1], a0.y, s); s = sdot4(c[2], a0.z, s); s = sdot4(c[3], a0.w, s);
+    s = sdot4(c[4], a1.x, s); s = sdot4(c[5], a1.y, s); s = sdot4(c[6], a1.z, s); s = sdot4(c[7], a1.w, s);
+    acc += (float)s * dw * ad[blk];           // sumf += sumi as f32 * d0 * d1
+  }
+  return acc;
+}
+
+template <int FMT> HH_DEV void load_unit(uint32_t (&w)[UnitT<FMT>::DW], const uint8_t* p) {
+  const u32x4_a4* v = (const u32x4_a4*)p;
+  if constexpr (FMT == FMT_Q1) {
+    u32x4_a4 a = __builtin_nontemporal_load(v), b = __builtin_nontemporal_load(v + 1);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    w[8] = __builtin_nontemporal_load((const uint32_t*)(p + 32));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4_a4 a = __builtin_nontemporal_load(v + i);
+      w[4 * i] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
+    }
+    w[16] = __builtin_nontemporal_load((const uint32_t*)(p + 64));
+  }
+}
+
+template <int FMT> HH_DEV float unit_dot(const uint32_t (&w)[UnitT<FMT>::DW], const int8_t* aq,
+                                         const float* ad, const int* as) {
+  if constexpr (FMT == FMT_Q2) return unit_q2(w, aq, ad, as);
+  else if constexpr (FMT == FMT_Q1) return unit_q1(w, aq, ad, as);
+  else return unit_q8(w, aq, ad, as);
+}
+
+// Packed activation into LDS from a dense f32 vector x (optionally RMS-normed).
+// 8 lanes per 32-element block, 4 consecutive elements per lane.
+template <int FMT>
+HH_DEV void prologue_quant(const float* __restrict__ x, const float* __restrict__ nw, float eps, int K,
+                           bool rmsnorm, int8_t* aq, float* ad, int* as, float* red) {
+  const int tid = threadIdx.x;
+  float inv = 1.0f;
+  if (rmsnorm) {
+    float ss = 0.0f;
+    for (int e = tid * 4; e < K; e += 1024) {
+      float4 v = *(const float4*)(x + e);
+      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    inv = 1.0f / sqrtf(tot / (float)K + eps);   // ops.rs:22-23
+  }
+  for (int e = tid * 4; e < K; e += 1024) {
+    float4 v = *(const float4*)(x + e);
+    float vv[4] = {v.x, v.y, v.z, v.w};
+    if (rmsnorm) {
+      float4 w4 = *(const float4*)(nw + e);
+      float ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vv[i] = vv[i] * inv * ww[i];   // ops.rs:29 (x * inv) * w
+    }
+    float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+    am = group_max<8>(am);
+    float sc = q8_scale(am);
+    int qs = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int q = q8_round(vv[i], sc);
+      qs += q;
+      aq[lds_qpos(FMT, e + i)] = (int8_t)q;
+    }
+    qs = group_sum_i<8>(qs);
+    if ((tid & 7) == 0) {
+      ad[e >> 5] = h2f(f2h(sc));
+      as[e >> 5] = qs;
+    }
+  }
+}
+
+// Standard Q8_0 blocks -> LDS packed layout.
+template <int FMT>
+HH_DEV void prologue_stdq8(const uint8_t* __restrict__ xq, int K, int8_t* aq, float* ad, int* as) {
+  const int tid = threadIdx.x;
+  for (int e = tid * 4; e < K; e += 1024) {
+    const uint8_t* blk = xq + (size_t)(e >> 5) * 34;
+    int off = e & 31;
+    int qs = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int q = (int8_t)blk[2 + off + i];
+      qs += q;
+      aq[lds_qpos(FMT, e + i)] = (int8_t)q;
+    }
+    qs = group_sum_i<8>(qs);
+    if ((tid & 7) == 0) {
+      ad[e >> 5] = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+      as[e >> 5] = qs;
+    }
+  }
+}
+
+// Packed activation in global memory -> LDS (adds the per-unit padding).
+template <int FMT>
+HH_DEV void prologue_packed(const uint8_t* __restrict__ act, int K, int8_t* aq, float* ad, int* as) {
+  const int tid = threadIdx.x;
+  constexpr int EL = UnitT<FMT>::EL;
+  for (int c = tid; c < K / 16; c += 256) {
+    int e = c * 16;
+    i32x4 v = *(const i32x4*)(act + e);
+    *(i32x4*)(aq + (e / EL) * qstride<FMT>() + (e % EL)) = v;
+  }
+  const float* gd = (const float*)(act + K);
+  const int* gs = (const int*)(act + K + (K / 32) * 4);
+  for (int b = tid; b < K / 32; b += 256) {
+    ad[b] = gd[b];
+    as[b] = gs[b];
+  }
+}
+
+template <int FMT, int PRO, int EPI>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
+  constexpr int DW = UnitT<FMT>::DW;
+  constexpr int UB = UnitT<FMT>::BYTES;
+  constexpr int SUBS = UnitT<FMT>::SUBS;
+  constexpr int DEPTH = (FMT == FMT_Q1) ? 4 : 2;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int K = p.K;
+  const int P = p.P;
+
+  if constexpr (EPI == EPI_LOGITS) {
+    StepState* st = p.state;
+    // Prompt tokens other than the last need no logits (forward_batch computes
+    // only the last token's, mod.rs:1201-1218): count in, advance, leave.
+    if (st->step + 1 < st->n_prompt) {
+      __syncthreads();
+      __shared__ int last_pf;
+      if (tid == 0) {
+        __threadfence();
+        last_pf = (atomicAdd(p.counter, 1) == (int)gridDim.x - 1);
+      }
+      __syncthreads();
+      if (last_pf && tid == 0) {
+        int s = st->step;
+        st->token = (int)p.prompt[s + 1];
+        st->pos = st->pos + 1;
+        st->step = s + 1;
+        *p.counter = 0;
+        __threadfence();
+      }
+      return;
+    }
+  }
+
+  // rows owned by this workgroup
+  int rows_total, r0, up_base = 0;
+  if constexpr (EPI == EPI_SILU) {
+    rows_total = 2 * p.rows_per_wg;             // gate rows then the matching up rows
+    r0 = blockIdx.x * p.rows_per_wg;
+    up_base = p.half_rows;
+  } else {
+    r0 = blockIdx.x * p.rows_per_wg;
+    rows_total = min(p.rows_per_wg, p.n_rows - r0);
+  }
+  const int U = rows_total * P;
+
+  // LDS carve-up
+  const int nunits_act = K / UnitT<FMT>::EL;
+  int8_t* aq = (int8_t*)smem;
+  float* ad = (float*)(smem + nunits_act * qstride<FMT>());
+  int* as = (int*)(ad + K / 32);
+  float* part = (float*)(as + K / 32);
+  float* red = part + U;
+  float* rowsum = red + 8;
+
+  auto unit_addr = [&](int lu) -> const uint8_t* {
+    int rl = lu / P, t = lu - rl * P;
+    int grow;
+    if constexpr (EPI == EPI_SILU) grow = (rl < p.rows_per_wg) ? r0 + rl : up_base + r0 + (rl - p.rows_per_wg);
+    else grow = r0 + rl;
+    return p.w + ((size_t)grow * P + t) * UB;
+  };
+
+  const int NI = (U + 255) / 256;
+  const int NB = (NI + DEPTH - 1) / DEPTH;
+  uint32_t wa[DEPTH][DW], wb[DEPTH][DW];
+
+  auto load_batch = [&](uint32_t (&wr)[DEPTH][DW], int b) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      int lu = (b * DEPTH + d) * 256 + tid;
+      if (lu < U) load_unit<FMT>(wr[d], unit_addr(lu));
+    }
+  };
+  auto comp_batch = [&](const uint32_t (&wr)[DEPTH][DW], int b) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      int lu = (b * DEPTH + d) * 256 + tid;
+      if (lu < U) {
+        int t = lu % P;
+        part[lu] = unit_dot<FMT>(wr[d], aq + t * qstride<FMT>(), ad + t * SUBS, as + t * SUBS);
+      }
+    }
+  };
+
+  if (NB > 0) load_batch(wa, 0);
+
+  if constexpr (PRO == PRO_PACKED) prologue_packed<FMT>(p.act, K, aq, ad, as);
+  else if constexpr (PRO == PRO_RMSNORM) prologue_quant<FMT>(p.x, p.norm_w, p.eps, K, true, aq, ad, as, red);
+  else prologue_stdq8<FMT>(p.act, K, aq, ad, as);
+  __syncthreads();
+
+  for (int b = 0; b < NB; b += 2) {
+    if (b + 1 < NB) load_batch(wb, b + 1);
+    comp_batch(wa, b);
+    if (b + 2 < NB) load_batch(wa, b + 2);
+    if (b + 1 < NB) comp_batch(wb, b + 1);
+  }
+  __syncthreads();
+
+  // per-row sums in unit order
+  for (int r = tid; r < rows_total; r += 256) {
+    const float* pr = part + r * P;
+    float s = 0.0f;
+    for (int t = 0; t < P; ++t) s += pr[t];
+    rowsum[r] = s;
+  }
+  __syncthreads();
+
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
+    for (int r = tid; r < rows_total; r += 256) {
+      if constexpr (EPI == EPI_STORE) p.y[r0 + r] = rowsum[r];
+      else p.y[r0 + r] = p.y[r0 + r] + rowsum[r];
+    }
+  } else if constexpr (EPI == EPI_SILU) {
+    // ops.rs:240-253 silu then mul_elem (mod.rs:758-763), then Q8_0 (q8_0.rs:20-51)
+    const int R2 = p.rows_per_wg;   // multiple of 32
+    for (int i0 = 0; i0 < R2; i0 += 256) {
+      int i = i0 + tid;
+      float h = 0.0f;
+      if (i < R2) {
+        float g = rowsum[i];
+        float sg = g / (1.0f + expf(-g));
+        h = sg * rowsum[R2 + i];
+      }
+      float am = group_max<32>(fabsf(h));
+      float sc = q8_scale(am);
+      int q = q8_round(h, sc);
+      int qs = group_sum_i<32>(q);
+      if (i < R2) {
+        int e = r0 + i;
+        p.act_out[perm_pos(p.act_out_fmt, e)] = (uint8_t)(int8_t)q;
+        if ((i & 31) == 0) {
+          float* od = (float*)(p.act_out + p.act_out_k);
+          int* os = (int*)(p.act_out + p.act_out_k + (p.act_out_k / 32) * 4);
+          od[e >> 5] = h2f(f2h(sc));
+          os[e >> 5] = qs;
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_LOGITS) {
+    StepState* st = p.state;
+    const int rule = p.rule;
+    const float pen = st->pen;
+    const bool do_pen = !(fabsf(pen - 1.0f) < 1e-6f);
+    float bv = -INFINITY;
+    int bi = (rule == 0) ? -1 : 0x7fffffff;
+    for (int r = tid; r < rows_total; r += 256) {
+      float v = rowsum[r];
+      int gr = r0 + r;
+      if (p.y) p.y[gr] = v;
+      if (rule == 0 && do_pen) {
+        int c = p.counts[gr];
+        for (int k = 0; k < c; ++k) v = (v > 0.0f) ? v / pen : v * pen;   // lib.rs:26-40
+      }
+      bool better = (rule == 0) ? (v > bv || (v == bv && gr > bi)) : (v > bv || (v == bv && gr < bi));
+      if (v != v) better = false;
+      if (better) { bv = v; bi = gr; }
+    }
+    // workgroup reduction
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    sv[tid] = bv;
+    si[tid] = bi;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+      if (tid < o) {
+        float v2 = sv[tid + o];
+        int i2 = si[tid + o];
+        float v1 = sv[tid];
+        int i1 = si[tid];
+        bool take = (rule == 0) ? (v2 > v1 || (v2 == v1 && i2 > i1)) : (v2 > v1 || (v2 == v1 && i2 < i1));
+        if (take) { sv[tid] = v2; si[tid] = i2; }
+      }
+      __syncthreads();
+    }
+    __shared__ int is_last;
+    if (tid == 0) {
+      p.part_val[blockIdx.x] = sv[0];
+      p.part_idx[blockIdx.x] = si[0];
+      __threadfence();
+      is_last = (atomicAdd(p.counter, 1) == (int)gridDim.x - 1);
+    }
+    __syncthreads();
+    if (is_last) {
+      __threadfence();
+      float v1 = -INFINITY;
+      int i1 = (rule == 0) ? -1 : 0x7fffffff;
+      for (int b = tid; b < (int)gridDim.x; b += 256) {
+        float v2 = __hip_atomic_load(p.part_val + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int i2 = __hip_atomic_load(p.part_idx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool take = (rule == 0) ? (v2 > v1 || (v2 == v1 && i2 > i1)) : (v2 > v1 || (v2 == v1 && i2 < i1));
+        if (take) { v1 = v2; i1 = i2; }
+      }
+      sv[tid] = v1;
+      si[tid] = i1;
+      __syncthreads();
+      for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) {
+          float v2 = sv[tid + o];
+          int i2 = si[tid + o];
+          float va = sv[tid];
+          int ia = si[tid];
+          bool take = (rule == 0) ? (v2 > va || (v2 == va && i2 > ia)) : (v2 > va || (v2 == va && i2 < ia));
+          if (take) { sv[tid] = v2; si[tid] = i2; }
+        }
+        __syncthreads();
+      }
+      if (tid == 0) {
+        int tok = si[0];
+        if (tok < 0 || tok >= p.n_rows) tok = 0;
+        st->argmax = tok;
+        if (st->update) {
+          int s = st->step;
+          int gen = s + 1 - st->n_prompt;           // index of this generated token
+          if (gen >= 0 && gen < p.max_out) p.out_tokens[gen] = (uint32_t)tok;
+          p.counts[tok] += 1;                        // past_tokens.push(token)
+          st->token = tok;
+          st->pos = st->pos + 1;
+          st->step = s + 1;
+        }
+        *p.counter = 0;
+        __threadfence();
+      }
+    }
+  }
+}
+
+template <int FMT, int PRO, int EPI>
+int launch_t(const GemvArgs& a, int n_wg, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((k_gemv<FMT, PRO, EPI>), dim3(n_wg), dim3(256), lds, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+template <int FMT, int PRO>
+int launch_e(const GemvArgs& a, int epi, int n_wg, size_t lds, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE: return launch_t<FMT, PRO, EPI_STORE>(a, n_wg, lds, s);
+    case EPI_ADD: return launch_t<FMT, PRO, EPI_ADD>(a, n_wg, lds, s);
+    case EPI_SILU: return launch_t<FMT, PRO, EPI_SILU>(a, n_wg, lds, s);
+    case EPI_LOGITS: return launch_t<FMT, PRO, EPI_LOGITS>(a, n_wg, lds, s);
+  }
+  return 1;
+}
+
+template <int FMT>
+int launch_p(const GemvArgs& a, int pro, int epi, int n_wg, size_t lds, hipStream_t s) {
+  switch (pro) {
+    case PRO_PACKED: return launch_e<FMT, PRO_PACKED>(a, epi, n_wg, lds, s);
+    case PRO_RMSNORM: return launch_e<FMT, PRO_RMSNORM>(a, epi, n_wg, lds, s);
+    case PRO_STDQ8: return launch_e<FMT, PRO_STDQ8>(a, epi, n_wg, lds, s);
+  }
+  return 1;
+}
+
+}  // namespace
+
+int hh_fmt_of(int ggml_type) {
+  switch (ggml_type) {
+    case 8: return FMT_Q8;
+    case 41: case 43: return FMT_Q1;
+    case 42: case 142: return FMT_Q2;
+  }
+  return -1;
+}
+
+int hh_unit_el(int fmt) { return fmt == FMT_Q8 ? 64 : 256; }
+
+// LDS bytes for a launch and the workgroup count.
+size_t hh_gemv_lds(int fmt, int K, int rows_total_per_wg) {
+  int el = hh_unit_el(fmt);
+  int P = K / el;
+  size_t qb = (size_t)(K / el) * (el + 16);
+  size_t b = qb + (size_t)(K / 32) * 8 + (size_t)rows_total_per_wg * P * 4 + 8 * 4 + (size_t)rows_total_per_wg * 4;
+  return (b + 15) & ~(size_t)15;
+}
+
+int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
+  int el = hh_unit_el(fmt);
+  if (a.K % el != 0) return 1;
+  a.P = a.K / el;
+  int n_wg, rows_total;
+  if (epi == EPI_SILU) {
+    n_wg = a.half_rows / a.rows_per_wg;
+    rows_total = 2 * a.rows_per_wg;
+  } else {
+    n_wg = (a.n_rows + a.rows_per_wg - 1) / a.rows_per_wg;
+    rows_total = a.rows_per_wg;
+  }
+  size_t lds = hh_gemv_lds(fmt, a.K, rows_total);
+  switch (fmt) {
+    case FMT_Q2: return launch_p<FMT_Q2>(a, pro, epi, n_wg, lds, s);
+    case FMT_Q1: return launch_p<FMT_Q1>(a, pro, epi, n_wg, lds, s);
+    case FMT_Q8: return launch_p<FMT_Q8>(a, pro, epi, n_wg, lds, s);
+  }
+  return 1;
+}
+
+int hh_gemv_grid(int epi, const GemvArgs& a) {
+  if (epi == EPI_SILU) return a.half_rows / a.rows_per_wg;
+  return (a.n_rows + a.rows_per_wg - 1) / a.rows_per_wg;
+}

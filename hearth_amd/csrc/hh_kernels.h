@@ -1,0 +1,117 @@
+// hh_kernels.h — launch interface between the runtime (hh_runtime.hip) and the
+// gfx950 kernels.  Internal to the library.
+#pragma once
+#include "hh_device.h"
+
+struct GemvArgs {
+  const uint8_t* w;     // matrix base, rows contiguous in native block layout
+  int n_rows;           // rows (EPI_SILU: unused; half_rows gives the gate count)
+  int K;                // n_cols
+  int P;                // units per row (set by the launcher)
+  int rows_per_wg;      // rows per workgroup (EPI_SILU: gate rows per workgroup)
+  int half_rows;        // EPI_SILU: row offset of the up half
+  // prologue inputs
+  const float* x;       // PRO_RMSNORM: f32 vector
+  const float* norm_w;  // PRO_RMSNORM: weight
+  float eps;
+  const uint8_t* act;   // PRO_PACKED: packed activation; PRO_STDQ8: Q8_0 blocks
+  // epilogue outputs
+  float* y;             // EPI_STORE / EPI_ADD target, EPI_LOGITS logits (may be null)
+  uint8_t* act_out;     // EPI_SILU packed output
+  int act_out_fmt;
+  int act_out_k;
+  // EPI_LOGITS
+  StepState* state;
+  const uint32_t* prompt;
+  uint32_t* out_tokens;
+  int max_out;
+  int* counts;
+  float pen;
+  int rule;
+  float* part_val;
+  int* part_idx;
+  int* counter;
+};
+
+enum { HH_PRO_PACKED = 0, HH_PRO_RMSNORM = 1, HH_PRO_STDQ8 = 2 };
+enum { HH_EPI_STORE = 0, HH_EPI_ADD = 1, HH_EPI_SILU = 2, HH_EPI_LOGITS = 3 };
+
+int hh_fmt_of(int ggml_type);
+int hh_unit_el(int fmt);
+size_t hh_gemv_lds(int fmt, int K, int rows_total_per_wg);
+int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s);
+int hh_gemv_grid(int epi, const GemvArgs& a);
+
+// Packed-activation byte size for a K-vector.
+inline size_t hh_packed_bytes(int K) { return (size_t)K + (size_t)(K / 32) * 8; }
+
+// ---- other operators (hh_ops.hip) ----
+struct AttnArgs {
+  const float* qkv;      // q region (gated: [q_h | gate_h] per head), then k, then v
+  int n_heads, n_kv, hd, rope_dim, gated;
+  int q_stride_heads;    // offset of k region from qkv start (floats)
+  const float* q_norm;   // null = no per-head RMSNorm
+  const float* k_norm;
+  float eps;
+  const float* rope;     // [max_seq][rope_dim] sin|cos (null = no RoPE)
+  int max_seq;
+  float* k_cache;        // [n_kv][max_seq][hd]
+  float* v_cache;
+  const StepState* state;  // pos source (null -> fixed_seq)
+  int fixed_seq;         // >0: attend this many rows, no KV write / prep
+  int chunk;             // positions per workgroup
+  int max_splits;
+  float* part_o;         // [n_kv][max_splits][G][hd]
+  float* part_ml;        // [n_kv][max_splits][G][2]
+  int* counters;         // [n_kv]
+  float* out_f32;        // optional [n_heads*hd]
+  uint8_t* act_out;      // optional packed activation (K = n_heads*hd)
+  int act_fmt;
+};
+int hh_attn_launch(const AttnArgs& a, hipStream_t s);
+
+int hh_quantize_launch(const float* x, int64_t n, uint8_t* out, hipStream_t s);
+int hh_dequant_launch(int type, const void* w, int64_t n, float* out, hipStream_t s);
+int hh_rmsnorm_launch(const float* x, const float* w, float eps, int64_t rows, int64_t n, float* out,
+                      hipStream_t s);
+int hh_rope_launch(float* x, int n_heads, int hd, int rope_dim, const float* table, int max_seq, int pos,
+                   hipStream_t s);
+int hh_embed_launch(int type, const uint8_t* table, int d, const StepState* st, float* hidden,
+                    hipStream_t s);
+int hh_argmax_launch(const float* logits, int64_t n, const int* counts, float pen, int rule,
+                     float* part_val, int* part_idx, int* counter, uint32_t* out, hipStream_t s);
+int hh_count_tokens_launch(const uint32_t* past, int64_t n_past, int* counts, hipStream_t s);
+int hh_fill_i32_launch(int* p, int64_t n, int v, hipStream_t s);
+
+// synthetic data
+int hh_synth_launch(int type, uint64_t key, int64_t rows, int64_t cols, float c, float cq, float mean,
+                    void* out, hipStream_t s);
+int hh_kv_synth_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq, float cs, float* cache,
+                       hipStream_t s);
+
+// qwen35 GDN step (hh_gdn.hip)
+struct GdnArgs {
+  const float* proj;      // [conv_dim] qkv projection (q | k | v), then [v_dim] z gate
+  const float* hidden;    // layer input; alpha/beta read rms_norm(hidden, attn_norm)
+  const float* attn_norm;
+  const float* w_alpha;   // [n_v][d] f32
+  const float* w_beta;    // [n_v][d] f32
+  const float* dt_bias;   // [n_v]
+  const float* ssm_a;     // [n_v]
+  const float* conv_w;    // [conv_dim][kernel]
+  float* conv_state;      // [conv_dim][kernel-1]
+  const float* ssm_norm;  // [hd]
+  float* state;           // [n_v][hd][hd]
+  int d, n_k, n_v, hd, kernel;
+  float eps;
+  uint8_t* act_out;       // packed activation of the gated-norm output (K = v_dim)
+  int act_fmt;
+  float* out_f32;         // optional
+  float* ab;              // scratch [2*n_v]
+  float* qk;              // scratch [2*k_dim] conv+silu+l2norm q,k
+  float* vconv;           // scratch [v_dim]
+  float* obuf;            // scratch [v_dim] recurrence output
+  const float* z;         // [v_dim] gate projection
+  int* counter;           // [n_v]
+};
+int hh_gdn_launch(const GdnArgs& a, hipStream_t s);

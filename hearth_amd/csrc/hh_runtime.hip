@@ -1,0 +1,926 @@
+// hh_runtime.hip — C ABI (include/hearth_hip.h): context, operators, model
+// storage in HBM, the per-token step as one captured HIP graph, and the
+// device-resident token loop.
+//
+// Host-side restatement of the reference's model/session layer:
+//   LlamaModel::forward / generate_text       mod.rs:451-860, :2718-3012
+//   Qwen35Core::forward / generate_text       qwen35.rs:1028-1236, :1654-1804
+//   upload_tensors_to_gpu (native blocks)     model/gpu.rs:8-50
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/hearth_hip.h"
+#include "hh_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                \
+  do {                                                                               \
+    hipError_t e_ = (expr);                                                          \
+    if (e_ != hipSuccess)                                                            \
+      return fail(HH_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_));    \
+  } while (0)
+
+#define KTRY(expr)                                                                   \
+  do {                                                                               \
+    if ((expr) != 0) {                                                               \
+      hipError_t e_ = hipGetLastError();                                             \
+      return fail(HH_ERR_HIP, std::string("launch failed: ") + #expr + ": " + hipGetErrorString(e_)); \
+    }                                                                                \
+  } while (0)
+
+size_t row_bytes(int type, int64_t n) {
+  switch (type) {
+    case HH_F32: return (size_t)n * 4;
+    case HH_F16: return (size_t)n * 2;
+    case HH_Q8_0: return (size_t)(n / 32) * 34;
+    case HH_Q1_0: case HH_Q1_0_G128: return (size_t)(n / 128) * 18;
+    case HH_Q2_0: case HH_PQ2_0: return (size_t)(n / 128) * 34;
+  }
+  return 0;
+}
+
+bool is_quant(int t) {
+  return t == HH_Q8_0 || t == HH_Q1_0 || t == HH_Q1_0_G128 || t == HH_Q2_0 || t == HH_PQ2_0;
+}
+
+uint64_t mix64h(uint64_t x) {
+  x ^= x >> 30;
+  x *= 0xbf58476d1ce4e5b9ull;
+  x ^= x >> 27;
+  x *= 0x94d049bb133111ebull;
+  x ^= x >> 31;
+  return x;
+}
+
+uint64_t name_key(uint64_t seed, const char* name) {
+  uint64_t h = 0xcbf29ce484222325ull;
+  for (const unsigned char* p = (const unsigned char*)name; *p; ++p) {
+    h ^= *p;
+    h *= 0x100000001b3ull;
+  }
+  return mix64h(seed ^ mix64h(h));
+}
+
+}  // namespace
+
+struct hh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // scratch for the standalone argmax operator
+  float* part_val = nullptr;
+  int* part_idx = nullptr;
+  int* counter = nullptr;
+  int* counts = nullptr;
+  int64_t counts_n = 0;
+};
+
+namespace {
+
+struct Tensor {
+  std::string name;
+  int type;
+  int64_t rows, cols;
+  float std, mean;
+  size_t nbytes;
+  uint8_t* d;       // device pointer (inside the model arena)
+};
+
+struct Layer {
+  bool gdn = false;
+  int attn_idx = -1;
+  // fused matrices (device pointers into the arena)
+  uint8_t* w_in = nullptr;    // dense: [q;k;v]  gdn: [qkv;gate]  q35 attn: [q(2nq);k;v]
+  int n_in = 0;               // rows of w_in
+  uint8_t* w_out = nullptr;   // attn_output / ssm_out
+  uint8_t* w_gu = nullptr;    // [gate; up]
+  uint8_t* w_down = nullptr;
+  float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+  float *ssm_conv = nullptr, *ssm_dt = nullptr, *ssm_a = nullptr, *ssm_alpha = nullptr, *ssm_beta = nullptr,
+        *ssm_norm = nullptr;
+  float *k_cache = nullptr, *v_cache = nullptr;
+  float *gdn_state = nullptr, *conv_state = nullptr;
+};
+
+}  // namespace
+
+struct hh_model {
+  hh_ctx* ctx = nullptr;
+  hh_model_config cfg{};
+  int rope_dim = 0;
+  int wfmt = 0;
+  std::vector<Tensor> tensors;
+  std::map<std::string, int> by_name;
+  std::vector<Layer> layers;
+  uint8_t* arena = nullptr;
+  size_t arena_bytes = 0;
+  Tensor *token_embd = nullptr, *output = nullptr, *output_norm = nullptr;
+  // state
+  float* kv = nullptr;
+  size_t kv_bytes = 0;
+  float* rec = nullptr;     // gdn + conv state
+  size_t rec_bytes = 0;
+  float* rope = nullptr;
+  // step buffers
+  float* hidden = nullptr;
+  float* proj = nullptr;        // QKV / GDN projection output
+  uint8_t* act_mid = nullptr;   // packed input of attn_output / ssm_out
+  uint8_t* act_ffn = nullptr;   // packed input of ffn_down
+  float* logits = nullptr;
+  float* head_pv = nullptr;
+  int* head_pi = nullptr;
+  int* counters = nullptr;      // [0] head, [1..] attention per kv head, then gdn
+  float* attn_po = nullptr;
+  float* attn_pml = nullptr;
+  int attn_chunk = 0, attn_splits = 0;
+  float* gdn_scratch = nullptr;
+  int* counts = nullptr;
+  uint32_t* prompt = nullptr;
+  uint32_t* out_tokens = nullptr;
+  int max_out = 0;
+  StepState* state = nullptr;
+  // graph
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  double last_decode_ms = 0.0;
+  int cancel = 0;
+  // launch geometry
+  int rows_in = 16, rows_out = 16, rows_gu = 32, rows_down = 16, rows_head = 64;
+};
+
+namespace {
+
+Tensor* find(hh_model* m, const std::string& n) {
+  auto it = m->by_name.find(n);
+  return it == m->by_name.end() ? nullptr : &m->tensors[it->second];
+}
+
+// Declares every tensor and where it lives inside the arena.  Matrices that one
+// GEMV launch consumes together are adjacent (rows concatenated, native blocks).
+void declare(hh_model* m) {
+  const hh_model_config& c = m->cfg;
+  int d = c.d_model, hd = c.head_dim, nq = c.n_heads * hd, nkv = c.n_kv_heads * hd;
+  int kdim = c.ssm_n_k_heads * c.ssm_head_dim, vdim = c.ssm_n_v_heads * c.ssm_head_dim;
+  int conv_dim = 2 * kdim + vdim;
+  auto add = [&](const std::string& name, int type, int64_t rows, int64_t cols, float sd, float mean) {
+    Tensor t{name, type, rows, cols, sd, mean, row_bytes(type, cols) * (size_t)rows, nullptr};
+    m->by_name[name] = (int)m->tensors.size();
+    m->tensors.push_back(t);
+  };
+  char b[96];
+  add("token_embd.weight", c.head_type, c.vocab, d, 0.02f, 0.0f);
+  add("output.weight", c.head_type, c.vocab, d, 0.02f, 0.0f);
+  add("output_norm.weight", HH_F32, 1, d, 0.02f, 1.0f);
+  int wt = c.wtype;
+  for (int i = 0; i < c.n_layers; ++i) {
+    bool gdn = (c.arch == 1) && ((i + 1) % c.full_attn_interval != 0);
+#define NM(s) (snprintf(b, sizeof b, "blk.%d." s, i), std::string(b))
+    add(NM("attn_norm.weight"), HH_F32, 1, d, 0.02f, 1.0f);
+    if (c.arch == 1) add(NM("post_attention_norm.weight"), HH_F32, 1, d, 0.02f, 1.0f);
+    else add(NM("ffn_norm.weight"), HH_F32, 1, d, 0.02f, 1.0f);
+    if (gdn) {
+      add(NM("attn_qkv.weight"), wt, conv_dim, d, 0.02f, 0.0f);
+      add(NM("attn_gate.weight"), wt, vdim, d, 0.02f, 0.0f);
+      add(NM("ssm_conv1d.weight"), HH_F32, conv_dim, c.ssm_conv_kernel, 0.3f, 0.0f);
+      add(NM("ssm_dt.bias"), HH_F32, 1, c.ssm_n_v_heads, 0.5f, 0.0f);
+      add(NM("ssm_a"), HH_F32, 1, c.ssm_n_v_heads, 0.1f, -1.0f);
+      add(NM("ssm_alpha.weight"), HH_F32, c.ssm_n_v_heads, d, 0.02f, 0.0f);
+      add(NM("ssm_beta.weight"), HH_F32, c.ssm_n_v_heads, d, 0.02f, 0.0f);
+      add(NM("ssm_norm.weight"), HH_F32, 1, c.ssm_head_dim, 0.02f, 1.0f);
+      add(NM("ssm_out.weight"), wt, d, vdim, 0.02f, 0.0f);
+    } else {
+      int qrows = c.attn_out_gate ? 2 * nq : nq;
+      add(NM("attn_q.weight"), wt, qrows, d, 0.02f, 0.0f);
+      add(NM("attn_k.weight"), wt, nkv, d, 0.02f, 0.0f);
+      add(NM("attn_v.weight"), wt, nkv, d, 0.02f, 0.0f);
+      add(NM("attn_output.weight"), wt, d, nq, 0.02f, 0.0f);
+      if (c.qk_norm) {
+        add(NM("attn_q_norm.weight"), HH_F32, 1, hd, 0.02f, 1.0f);
+        add(NM("attn_k_norm.weight"), HH_F32, 1, hd, 0.02f, 1.0f);
+      }
+    }
+    add(NM("ffn_gate.weight"), wt, c.d_ffn, d, 0.02f, 0.0f);
+    add(NM("ffn_up.weight"), wt, c.d_ffn, d, 0.02f, 0.0f);
+    add(NM("ffn_down.weight"), wt, d, c.d_ffn, 0.02f, 0.0f);
+#undef NM
+  }
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int enqueue_step(hh_model* m, hipStream_t s, int only_layer = -1, unsigned stages = ~0u);
+
+int capture(hh_model* m) {
+  hipStream_t s = m->ctx->stream;
+  if (m->gexec) { hipGraphExecDestroy(m->gexec); m->gexec = nullptr; }
+  if (m->graph) { hipGraphDestroy(m->graph); m->graph = nullptr; }
+  HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = enqueue_step(m, s);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(s, &g);
+  if (rc != 0) { if (g) hipGraphDestroy(g); return rc; }
+  if (e != hipSuccess) return fail(HH_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+  m->graph = g;
+  HIP_TRY(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
+  return HH_OK;
+}
+
+GemvArgs gemv_base(const uint8_t* w, int n_rows, int K, int rows_per_wg) {
+  GemvArgs a{};
+  a.w = w;
+  a.n_rows = n_rows;
+  a.K = K;
+  a.rows_per_wg = rows_per_wg;
+  return a;
+}
+
+// One decode step (mod.rs:451-860 / qwen35.rs:1028-1236) as a kernel sequence.
+// Stages: 0 embed, 1 input projection, 2 attention / GDN, 3 output projection,
+// 4 gate+up, 5 down, 6 LM head + greedy selection.  `only_layer`/`stages`
+// restrict the launch (stage timing); the captured graph holds everything.
+int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
+  auto want = [&](int st, int li) { return ((stages >> st) & 1u) && (only_layer < 0 || li == only_layer || li < 0); };
+  const hh_model_config& c = m->cfg;
+  const int d = c.d_model, hd = c.head_dim, nq = c.n_heads * hd, nkv = c.n_kv_heads * hd;
+  const int wf = m->wfmt;
+  if (want(0, -1)) KTRY(hh_embed_launch(c.head_type, m->token_embd->d, d, m->state, m->hidden, s));
+  for (int li = 0; li < c.n_layers; ++li) {
+    Layer& L = m->layers[li];
+    // input projection(s), RMSNorm + Q8_0 fused into the GEMV prologue
+    GemvArgs g = gemv_base(L.w_in, L.n_in, d, m->rows_in);
+    g.x = m->hidden;
+    g.norm_w = L.attn_norm;
+    g.eps = c.eps;
+    g.y = m->proj;
+    if (want(1, li)) KTRY(hh_gemv_launch(wf, HH_PRO_RMSNORM, HH_EPI_STORE, g, s));
+    int k_out;
+    if (L.gdn) {
+      int kdim = c.ssm_n_k_heads * c.ssm_head_dim, vdim = c.ssm_n_v_heads * c.ssm_head_dim;
+      GdnArgs ga{};
+      ga.proj = m->proj;
+      ga.z = m->proj + (2 * kdim + vdim);
+      ga.hidden = m->hidden;
+      ga.attn_norm = L.attn_norm;
+      ga.w_alpha = L.ssm_alpha;
+      ga.w_beta = L.ssm_beta;
+      ga.dt_bias = L.ssm_dt;
+      ga.ssm_a = L.ssm_a;
+      ga.conv_w = L.ssm_conv;
+      ga.conv_state = L.conv_state;
+      ga.ssm_norm = L.ssm_norm;
+      ga.state = L.gdn_state;
+      ga.d = d;
+      ga.n_k = c.ssm_n_k_heads;
+      ga.n_v = c.ssm_n_v_heads;
+      ga.hd = c.ssm_head_dim;
+      ga.kernel = c.ssm_conv_kernel;
+      ga.eps = c.eps;
+      ga.act_out = m->act_mid;
+      ga.act_fmt = wf;
+      ga.out_f32 = nullptr;
+      ga.ab = m->gdn_scratch;
+      ga.qk = m->gdn_scratch + 256;
+      ga.vconv = ga.qk + 2 * kdim;
+      ga.obuf = ga.vconv + vdim;
+      ga.counter = m->counters + 128;
+      if (want(2, li)) KTRY(hh_gdn_launch(ga, s));
+      k_out = vdim;
+    } else {
+      AttnArgs aa{};
+      aa.qkv = m->proj;
+      aa.n_heads = c.n_heads;
+      aa.n_kv = c.n_kv_heads;
+      aa.hd = hd;
+      aa.rope_dim = m->rope_dim;
+      aa.gated = c.attn_out_gate;
+      aa.q_stride_heads = (c.attn_out_gate ? 2 : 1) * nq;
+      aa.q_norm = L.q_norm;
+      aa.k_norm = L.k_norm;
+      aa.eps = c.eps;
+      aa.rope = m->rope;
+      aa.max_seq = c.max_seq;
+      aa.k_cache = L.k_cache;
+      aa.v_cache = L.v_cache;
+      aa.state = m->state;
+      aa.fixed_seq = 0;
+      aa.chunk = m->attn_chunk;
+      aa.max_splits = m->attn_splits;
+      aa.part_o = m->attn_po;
+      aa.part_ml = m->attn_pml;
+      aa.counters = m->counters + 1;
+      aa.out_f32 = nullptr;
+      aa.act_out = m->act_mid;
+      aa.act_fmt = wf;
+      if (want(2, li)) KTRY(hh_attn_launch(aa, s));
+      k_out = nq;
+      (void)nkv;
+    }
+    GemvArgs o = gemv_base(L.w_out, d, k_out, m->rows_out);
+    o.act = m->act_mid;
+    o.y = m->hidden;
+    if (want(3, li)) KTRY(hh_gemv_launch(wf, HH_PRO_PACKED, HH_EPI_ADD, o, s));
+    GemvArgs gu = gemv_base(L.w_gu, 2 * c.d_ffn, d, m->rows_gu);
+    gu.half_rows = c.d_ffn;
+    gu.x = m->hidden;
+    gu.norm_w = L.ffn_norm;
+    gu.eps = c.eps;
+    gu.act_out = m->act_ffn;
+    gu.act_out_fmt = wf;
+    gu.act_out_k = c.d_ffn;
+    if (want(4, li)) KTRY(hh_gemv_launch(wf, HH_PRO_RMSNORM, HH_EPI_SILU, gu, s));
+    GemvArgs dn = gemv_base(L.w_down, d, c.d_ffn, m->rows_down);
+    dn.act = m->act_ffn;
+    dn.y = m->hidden;
+    if (want(5, li)) KTRY(hh_gemv_launch(wf, HH_PRO_PACKED, HH_EPI_ADD, dn, s));
+  }
+  GemvArgs h = gemv_base(m->output->d, c.vocab, d, m->rows_head);
+  h.x = m->hidden;
+  h.norm_w = (const float*)m->output_norm->d;
+  h.eps = c.eps;
+  h.y = m->logits;
+  h.state = m->state;
+  h.prompt = m->prompt;
+  h.out_tokens = m->out_tokens;
+  h.max_out = m->max_out;
+  h.counts = m->counts;
+  h.pen = 1.0f;   // replaced from the state at run time (see k_gemv EPI_LOGITS)
+  h.rule = c.arch == 1 ? 1 : 0;
+  h.part_val = m->head_pv;
+  h.part_idx = m->head_pi;
+  h.counter = m->counters;
+  if (want(6, -1)) KTRY(hh_gemv_launch(hh_fmt_of(c.head_type), HH_PRO_RMSNORM, HH_EPI_LOGITS, h, s));
+  return HH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hh_last_error(void) { return g_err.c_str(); }
+const char* hh_version(void) { return "hearth_hip 0.1 gfx950"; }
+
+int hh_ctx_create(int device_ordinal, hh_ctx** out) {
+  if (!out) return fail(HH_ERR_INVALID, "out is null");
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  if (device_ordinal < 0 || device_ordinal >= n) return fail(HH_ERR_INVALID, "no such device");
+  HIP_TRY(hipSetDevice(device_ordinal));
+  hh_ctx* c = new hh_ctx();
+  c->device = device_ordinal;
+  HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+  HIP_TRY(hipMalloc(&c->part_val, 4096 * sizeof(float)));
+  HIP_TRY(hipMalloc(&c->part_idx, 4096 * sizeof(int)));
+  HIP_TRY(hipMalloc(&c->counter, 64 * sizeof(int)));
+  HIP_TRY(hipMemset(c->counter, 0, 64 * sizeof(int)));
+  *out = c;
+  return HH_OK;
+}
+
+int hh_ctx_destroy(hh_ctx* c) {
+  if (!c) return HH_OK;
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  hipFree(c->part_val);
+  hipFree(c->part_idx);
+  hipFree(c->counter);
+  if (c->counts) hipFree(c->counts);
+  hipStreamDestroy(c->stream);
+  delete c;
+  return HH_OK;
+}
+
+int hh_ctx_synchronize(hh_ctx* c) {
+  if (!c) return fail(HH_ERR_INVALID, "ctx is null");
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return HH_OK;
+}
+
+int hh_malloc(hh_ctx* c, size_t n, void** p) {
+  if (!c || !p) return fail(HH_ERR_INVALID, "null argument");
+  hipError_t e = hipMalloc(p, n ? n : 1);
+  if (e != hipSuccess) return fail(HH_ERR_OOM, std::string("hipMalloc: ") + hipGetErrorString(e));
+  return HH_OK;
+}
+int hh_free(hh_ctx* c, void* p) {
+  if (!c) return fail(HH_ERR_INVALID, "ctx is null");
+  HIP_TRY(hipFree(p));
+  return HH_OK;
+}
+int hh_memcpy_h2d(hh_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c) return fail(HH_ERR_INVALID, "ctx is null");
+  HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return HH_OK;
+}
+int hh_memcpy_d2h(hh_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c) return fail(HH_ERR_INVALID, "ctx is null");
+  HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return HH_OK;
+}
+int hh_memset(hh_ctx* c, void* dst, int v, size_t n) {
+  if (!c) return fail(HH_ERR_INVALID, "ctx is null");
+  HIP_TRY(hipMemsetAsync(dst, v, n, c->stream));
+  return HH_OK;
+}
+
+int hh_quantize_q8_0(hh_ctx* c, const float* x, int64_t n, uint8_t* out) {
+  if (!c || (!x && n) || (!out && n)) return fail(HH_ERR_INVALID, "null argument");
+  if (n < 0) return fail(HH_ERR_DIM, "negative length");
+  KTRY(hh_quantize_launch(x, n, out, c->stream));
+  return HH_OK;
+}
+
+int hh_dequantize(hh_ctx* c, int type, const void* w, int64_t n, float* out) {
+  if (!c || (!w && n) || (!out && n)) return fail(HH_ERR_INVALID, "null argument");
+  if (!(is_quant(type) || type == HH_F32 || type == HH_F16)) return fail(HH_ERR_DTYPE, "unsupported dtype");
+  int64_t blk = type == HH_Q8_0 ? 32 : (is_quant(type) ? 128 : 1);
+  if (n % blk) return fail(HH_ERR_DIM, "length is not a whole number of blocks");
+  KTRY(hh_dequant_launch(type, w, n, out, c->stream));
+  return HH_OK;
+}
+
+int hh_gemv_q8(hh_ctx* c, int type, const void* w, int64_t n_rows, int64_t n_cols, const uint8_t* xq8, float* y) {
+  if (!c || !w || !xq8 || !y) return fail(HH_ERR_INVALID, "null argument");
+  int fmt = hh_fmt_of(type);
+  if (fmt < 0) return fail(HH_ERR_DTYPE, "unsupported weight dtype for the Q8_0 GEMV");
+  int el = hh_unit_el(fmt);
+  if (n_cols <= 0 || n_cols % el != 0)
+    return fail(HH_ERR_DIM, "n_cols must be a positive multiple of " + std::to_string(el));
+  if (n_cols > 32768) return fail(HH_ERR_DIM, "n_cols above 32768");
+  if (n_rows <= 0 || n_rows > (1ll << 30)) return fail(HH_ERR_DIM, "bad n_rows");
+  int P = (int)n_cols / el;
+  int rows = 4096 / P;
+  if (rows < 4) rows = 4;
+  if (rows > 64) rows = 64;
+  GemvArgs a = gemv_base((const uint8_t*)w, (int)n_rows, (int)n_cols, rows);
+  a.act = xq8;
+  a.y = y;
+  KTRY(hh_gemv_launch(fmt, HH_PRO_STDQ8, HH_EPI_STORE, a, c->stream));
+  return HH_OK;
+}
+
+int hh_rms_norm(hh_ctx* c, const float* x, const float* w, float eps, int64_t rows, int64_t n, float* out) {
+  if (!c || !x || !w || !out) return fail(HH_ERR_INVALID, "null argument");
+  if (n <= 0 || rows < 0) return fail(HH_ERR_DIM, "bad shape");
+  KTRY(hh_rmsnorm_launch(x, w, eps, rows, n, out, c->stream));
+  return HH_OK;
+}
+
+int hh_rope(hh_ctx* c, float* x, int n_heads, int hd, int rope_dim, const float* table, int max_seq, int pos) {
+  if (!c || !x || !table) return fail(HH_ERR_INVALID, "null argument");
+  if (rope_dim > hd || rope_dim % 2 || pos < 0) return fail(HH_ERR_DIM, "bad rope shape");
+  KTRY(hh_rope_launch(x, n_heads, hd, rope_dim, table, max_seq, pos, c->stream));
+  return HH_OK;
+}
+
+int hh_attention(hh_ctx* c, const float* q, const float* k, const float* v, int n_heads, int n_kv, int hd,
+                 int max_seq, int seq_len, float* out) {
+  if (!c || !q || !k || !v || !out) return fail(HH_ERR_INVALID, "null argument");
+  if (n_kv <= 0 || n_heads % n_kv || hd <= 0 || 4096 % hd || hd < 64 || hd > 256)
+    return fail(HH_ERR_DIM, "unsupported attention geometry");
+  if (seq_len <= 0 || seq_len > max_seq) return fail(HH_ERR_RANGE, "seq_len out of range");
+  int G = n_heads / n_kv;
+  if (G > 16) return fail(HH_ERR_DIM, "too many query heads per kv head");
+  int chunk = 4096 / hd;
+  int splits = (seq_len + chunk - 1) / chunk;
+  float *po = nullptr, *pml = nullptr;
+  int* cnt = nullptr;
+  HIP_TRY(hipMallocAsync((void**)&po, sizeof(float) * (size_t)n_kv * splits * G * hd, c->stream));
+  HIP_TRY(hipMallocAsync((void**)&pml, sizeof(float) * (size_t)n_kv * splits * G * 2, c->stream));
+  HIP_TRY(hipMallocAsync((void**)&cnt, sizeof(int) * (size_t)n_kv, c->stream));
+  HIP_TRY(hipMemsetAsync(cnt, 0, sizeof(int) * (size_t)n_kv, c->stream));
+  AttnArgs a{};
+  a.qkv = q;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv;
+  a.hd = hd;
+  a.k_cache = const_cast<float*>(k);
+  a.v_cache = const_cast<float*>(v);
+  a.max_seq = max_seq;
+  a.fixed_seq = seq_len;
+  a.chunk = chunk;
+  a.max_splits = splits;
+  a.part_o = po;
+  a.part_ml = pml;
+  a.counters = cnt;
+  a.out_f32 = out;
+  int rc = hh_attn_launch(a, c->stream);
+  hipFreeAsync(po, c->stream);
+  hipFreeAsync(pml, c->stream);
+  hipFreeAsync(cnt, c->stream);
+  if (rc) return fail(HH_ERR_HIP, std::string("attention launch: ") + hipGetErrorString(hipGetLastError()));
+  return HH_OK;
+}
+
+int hh_argmax(hh_ctx* c, const float* logits, int64_t n, const uint32_t* past, int64_t n_past, float pen, int rule,
+              uint32_t* out) {
+  if (!c || !logits || !out || (n_past && !past)) return fail(HH_ERR_INVALID, "null argument");
+  if (n <= 0 || n > (1ll << 31) - 1) return fail(HH_ERR_DIM, "bad length");
+  if (rule != 0 && rule != 1) return fail(HH_ERR_INVALID, "rule must be 0 or 1");
+  const int* counts = nullptr;
+  if (rule == 0 && n_past > 0) {
+    if (c->counts_n < n) {
+      if (c->counts) hipFree(c->counts);
+      HIP_TRY(hipMalloc(&c->counts, sizeof(int) * (size_t)n));
+      c->counts_n = n;
+    }
+    KTRY(hh_fill_i32_launch(c->counts, n, 0, c->stream));
+    KTRY(hh_count_tokens_launch(past, n_past, c->counts, c->stream));
+    counts = c->counts;
+  }
+  KTRY(hh_argmax_launch(logits, n, counts, pen, rule, c->part_val, c->part_idx, c->counter, out, c->stream));
+  return HH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+
+int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
+  if (!ctx || !cfg || !out) return fail(HH_ERR_INVALID, "null argument");
+  const hh_model_config& c = *cfg;
+  if (c.arch != 0 && c.arch != 1) return fail(HH_ERR_INVALID, "arch must be 0 (dense) or 1 (qwen35)");
+  int wf = hh_fmt_of(c.wtype);
+  if (wf < 0 || wf == 0) return fail(HH_ERR_DTYPE, "layer weights must be Q1_0/Q1_0_G128/Q2_0/PQ2_0");
+  if (c.head_type != HH_Q8_0) return fail(HH_ERR_DTYPE, "token_embd/output must be Q8_0");
+  if (c.d_model % 1024 || c.d_ffn % 1024 || c.n_layers <= 0 || c.vocab <= 0)
+    return fail(HH_ERR_DIM, "d_model and d_ffn must be multiples of 1024");
+  if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || c.head_dim < 64 || c.head_dim > 256 || 4096 % c.head_dim)
+    return fail(HH_ERR_DIM, "unsupported attention geometry");
+  if ((c.n_heads * c.head_dim) % 256) return fail(HH_ERR_DIM, "n_heads*head_dim must be a multiple of 256");
+  if (c.max_seq <= 0) return fail(HH_ERR_DIM, "max_seq must be positive");
+  if (c.arch == 1) {
+    if (c.full_attn_interval <= 0 || c.ssm_n_k_heads <= 0 || c.ssm_n_v_heads % c.ssm_n_k_heads ||
+        c.ssm_head_dim != 128 || c.ssm_conv_kernel < 2 || c.ssm_conv_kernel > 8)
+      return fail(HH_ERR_DIM, "unsupported qwen35 recurrent geometry");
+  }
+  HIP_TRY(hipSetDevice(ctx->device));
+  hh_model* m = new hh_model();
+  m->ctx = ctx;
+  m->cfg = c;
+  m->wfmt = wf;
+  m->rope_dim = c.rope_dim > 0 ? c.rope_dim : c.head_dim;
+  declare(m);
+  // arena: every tensor, 256-byte aligned, fused groups contiguous in declaration order
+  size_t off = 0;
+  std::vector<size_t> offs(m->tensors.size());
+  for (size_t i = 0; i < m->tensors.size(); ++i) {
+    Tensor& t = m->tensors[i];
+    bool fuse_prev = false;
+    const std::string& n = t.name;
+    auto ends = [&](const char* suf) { return n.size() > strlen(suf) && n.compare(n.size() - strlen(suf), strlen(suf), suf) == 0; };
+    if (ends("attn_k.weight") || ends("attn_v.weight") || ends("attn_gate.weight") || ends("ffn_up.weight")) fuse_prev = true;
+    if (!fuse_prev) off = align256(off);
+    offs[i] = off;
+    off += t.nbytes;
+  }
+  m->arena_bytes = align256(off);
+  hipError_t e = hipMalloc(&m->arena, m->arena_bytes);
+  if (e != hipSuccess) {
+    delete m;
+    return fail(HH_ERR_OOM, "weight arena allocation failed (" + std::to_string(m->arena_bytes) + " bytes)");
+  }
+  for (size_t i = 0; i < m->tensors.size(); ++i) m->tensors[i].d = m->arena + offs[i];
+  m->token_embd = find(m, "token_embd.weight");
+  m->output = find(m, "output.weight");
+  m->output_norm = find(m, "output_norm.weight");
+  // layers
+  int hd = c.head_dim, nq = c.n_heads * hd, nkv = c.n_kv_heads * hd;
+  int kdim = c.ssm_n_k_heads * c.ssm_head_dim, vdim = c.ssm_n_v_heads * c.ssm_head_dim;
+  int conv_dim = 2 * kdim + vdim;
+  m->layers.resize(c.n_layers);
+  int n_attn = 0, n_gdn = 0;
+  char b[96];
+  for (int i = 0; i < c.n_layers; ++i) {
+    Layer& L = m->layers[i];
+    L.gdn = (c.arch == 1) && ((i + 1) % c.full_attn_interval != 0);
+    auto T = [&](const char* s) -> Tensor* { snprintf(b, sizeof b, "blk.%d.%s", i, s); return find(m, b); };
+    L.attn_norm = (float*)T("attn_norm.weight")->d;
+    L.ffn_norm = (float*)(c.arch == 1 ? T("post_attention_norm.weight") : T("ffn_norm.weight"))->d;
+    if (L.gdn) {
+      L.w_in = T("attn_qkv.weight")->d;
+      L.n_in = conv_dim + vdim;
+      L.w_out = T("ssm_out.weight")->d;
+      L.ssm_conv = (float*)T("ssm_conv1d.weight")->d;
+      L.ssm_dt = (float*)T("ssm_dt.bias")->d;
+      L.ssm_a = (float*)T("ssm_a")->d;
+      L.ssm_alpha = (float*)T("ssm_alpha.weight")->d;
+      L.ssm_beta = (float*)T("ssm_beta.weight")->d;
+      L.ssm_norm = (float*)T("ssm_norm.weight")->d;
+      n_gdn++;
+    } else {
+      L.w_in = T("attn_q.weight")->d;
+      L.n_in = (c.attn_out_gate ? 2 * nq : nq) + 2 * nkv;
+      L.w_out = T("attn_output.weight")->d;
+      if (c.qk_norm) {
+        L.q_norm = (float*)T("attn_q_norm.weight")->d;
+        L.k_norm = (float*)T("attn_k_norm.weight")->d;
+      }
+      L.attn_idx = n_attn++;
+    }
+    L.w_gu = T("ffn_gate.weight")->d;
+    L.w_down = T("ffn_down.weight")->d;
+  }
+  // KV cache: [attn layer][K|V][kv_head][max_seq][hd] f32 (kvcache.rs:11-39)
+  size_t per = (size_t)c.n_kv_heads * c.max_seq * hd;
+  m->kv_bytes = sizeof(float) * per * 2 * (size_t)n_attn;
+  if (m->kv_bytes) {
+    e = hipMalloc(&m->kv, m->kv_bytes);
+    if (e != hipSuccess) { hh_model_destroy(m); return fail(HH_ERR_OOM, "KV cache allocation failed"); }
+  }
+  size_t rec_per = 0;
+  if (c.arch == 1) {
+    rec_per = (size_t)c.ssm_n_v_heads * c.ssm_head_dim * c.ssm_head_dim + (size_t)conv_dim * (c.ssm_conv_kernel - 1);
+    m->rec_bytes = sizeof(float) * rec_per * (size_t)n_gdn;
+    e = hipMalloc(&m->rec, m->rec_bytes);
+    if (e != hipSuccess) { hh_model_destroy(m); return fail(HH_ERR_OOM, "recurrent state allocation failed"); }
+  }
+  int ai = 0, gi = 0;
+  for (auto& L : m->layers) {
+    if (L.gdn) {
+      L.gdn_state = m->rec + rec_per * gi;
+      L.conv_state = L.gdn_state + (size_t)c.ssm_n_v_heads * c.ssm_head_dim * c.ssm_head_dim;
+      gi++;
+    } else {
+      L.k_cache = m->kv + per * 2 * ai;
+      L.v_cache = L.k_cache + per;
+      ai++;
+    }
+  }
+  // RoPE table (ops.rs:78-138), computed on the host with libm like the reference
+  {
+    int half = m->rope_dim / 2;
+    std::vector<float> inv(half), tab((size_t)c.max_seq * m->rope_dim);
+    for (int i = 0; i < half; ++i) inv[i] = 1.0f / powf(c.rope_theta, 2.0f * (float)i / (float)m->rope_dim);
+    for (int p = 0; p < c.max_seq; ++p)
+      for (int i = 0; i < half; ++i) {
+        float f = (float)p * 1.0f * inv[i];
+        tab[(size_t)p * half * 2 + i] = sinf(f);
+        tab[(size_t)p * half * 2 + half + i] = cosf(f);
+      }
+    HIP_TRY(hipMalloc(&m->rope, tab.size() * sizeof(float)));
+    HIP_TRY(hipMemcpy(m->rope, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
+  }
+  // step buffers
+  int wide = std::max(std::max(c.d_model, c.d_ffn), std::max((c.attn_out_gate ? 2 : 1) * nq + 2 * nkv, conv_dim + vdim));
+  m->attn_chunk = 4096 / hd;
+  m->attn_splits = (c.max_seq + m->attn_chunk - 1) / m->attn_chunk;
+  int G = c.n_heads / c.n_kv_heads;
+  int head_wg = (c.vocab + m->rows_head - 1) / m->rows_head;
+  m->max_out = c.max_seq + 8;
+  HIP_TRY(hipMalloc(&m->hidden, sizeof(float) * c.d_model));
+  HIP_TRY(hipMalloc(&m->proj, sizeof(float) * wide));
+  HIP_TRY(hipMalloc(&m->act_mid, hh_packed_bytes(std::max(nq, vdim)) + 64));
+  HIP_TRY(hipMalloc(&m->act_ffn, hh_packed_bytes(c.d_ffn) + 64));
+  HIP_TRY(hipMalloc(&m->logits, sizeof(float) * c.vocab));
+  HIP_TRY(hipMalloc(&m->head_pv, sizeof(float) * head_wg));
+  HIP_TRY(hipMalloc(&m->head_pi, sizeof(int) * head_wg));
+  HIP_TRY(hipMalloc(&m->counters, sizeof(int) * 256));
+  HIP_TRY(hipMemset(m->counters, 0, sizeof(int) * 256));
+  HIP_TRY(hipMalloc(&m->attn_po, sizeof(float) * (size_t)c.n_kv_heads * m->attn_splits * G * hd));
+  HIP_TRY(hipMalloc(&m->attn_pml, sizeof(float) * (size_t)c.n_kv_heads * m->attn_splits * G * 2));
+  HIP_TRY(hipMalloc(&m->gdn_scratch, sizeof(float) * (size_t)(256 + 2 * kdim + 2 * vdim + 64)));
+  HIP_TRY(hipMalloc(&m->counts, sizeof(int) * c.vocab));
+  HIP_TRY(hipMemset(m->counts, 0, sizeof(int) * c.vocab));
+  HIP_TRY(hipMalloc(&m->prompt, sizeof(uint32_t) * (c.max_seq + 8)));
+  HIP_TRY(hipMalloc(&m->out_tokens, sizeof(uint32_t) * m->max_out));
+  HIP_TRY(hipMalloc(&m->state, sizeof(StepState)));
+  HIP_TRY(hipMemset(m->state, 0, sizeof(StepState)));
+  HIP_TRY(hipEventCreate(&m->ev0));
+  HIP_TRY(hipEventCreate(&m->ev1));
+  // launch geometry: ~256-1024 units of work per workgroup
+  {
+    int el = hh_unit_el(wf);
+    int P = c.d_model / el;
+    m->rows_in = std::max(4, std::min(64, 256 / P));
+    m->rows_gu = 32;
+    m->rows_out = std::max(4, std::min(64, 256 / std::max(1, std::max(nq, vdim) / el)));
+    m->rows_down = std::max(4, std::min(64, 1024 / (c.d_ffn / el)));
+    m->rows_head = 64;
+  }
+  HIP_TRY(hipDeviceSynchronize());
+  int rc = capture(m);
+  if (rc) { std::string msg = g_err; hh_model_destroy(m); return fail(rc, "graph capture: " + msg); }
+  *out = m;
+  return HH_OK;
+}
+
+int hh_model_destroy(hh_model* m) {
+  if (!m) return HH_OK;
+  hipSetDevice(m->ctx->device);
+  hipStreamSynchronize(m->ctx->stream);
+  if (m->gexec) hipGraphExecDestroy(m->gexec);
+  if (m->graph) hipGraphDestroy(m->graph);
+  void* bufs[] = {m->arena, m->kv, m->rec, m->rope, m->hidden, m->proj, m->act_mid, m->act_ffn, m->logits,
+                  m->head_pv, m->head_pi, m->counters, m->attn_po, m->attn_pml, m->gdn_scratch, m->counts,
+                  m->prompt, m->out_tokens, m->state};
+  for (void* p : bufs)
+    if (p) hipFree(p);
+  if (m->ev0) hipEventDestroy(m->ev0);
+  if (m->ev1) hipEventDestroy(m->ev1);
+  delete m;
+  return HH_OK;
+}
+
+int hh_model_upload_tensor(hh_model* m, const char* name, int type, int64_t ne0, int64_t ne1, const void* host,
+                           size_t nbytes) {
+  if (!m || !name || !host) return fail(HH_ERR_INVALID, "null argument");
+  Tensor* t = find(m, name);
+  if (!t) return fail(HH_ERR_NOT_FOUND, std::string("Tensor not found: ") + name);
+  if (t->type != type) return fail(HH_ERR_DTYPE, std::string("dtype mismatch for ") + name);
+  if (t->cols != ne0 || t->rows != ne1 || t->nbytes != nbytes)
+    return fail(HH_ERR_DIM, std::string("shape mismatch for ") + name);
+  HIP_TRY(hipMemcpyAsync(t->d, host, nbytes, hipMemcpyHostToDevice, m->ctx->stream));
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  return HH_OK;
+}
+
+int hh_model_download_tensor(hh_model* m, const char* name, void* host, size_t nbytes) {
+  if (!m || !name || !host) return fail(HH_ERR_INVALID, "null argument");
+  Tensor* t = find(m, name);
+  if (!t) return fail(HH_ERR_NOT_FOUND, std::string("Tensor not found: ") + name);
+  if (nbytes != t->nbytes) return fail(HH_ERR_DIM, "byte size mismatch");
+  HIP_TRY(hipMemcpyAsync(host, t->d, nbytes, hipMemcpyDeviceToHost, m->ctx->stream));
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  return HH_OK;
+}
+
+int hh_model_tensor_count(hh_model* m) { return m ? (int)m->tensors.size() : 0; }
+
+int hh_model_tensor_info(hh_model* m, int i, const char** name, int* type, int64_t* ne0, int64_t* ne1,
+                         size_t* nbytes) {
+  if (!m || i < 0 || i >= (int)m->tensors.size()) return fail(HH_ERR_INVALID, "bad tensor index");
+  const Tensor& t = m->tensors[i];
+  if (name) *name = t.name.c_str();
+  if (type) *type = t.type;
+  if (ne0) *ne0 = t.cols;
+  if (ne1) *ne1 = t.rows;
+  if (nbytes) *nbytes = t.nbytes;
+  return HH_OK;
+}
+
+int hh_model_synthesize(hh_model* m, uint64_t seed) {
+  if (!m) return fail(HH_ERR_INVALID, "null model");
+  for (const Tensor& t : m->tensors) {
+    float cc = t.std / 37837.227f;
+    float cq = cc / 128.0f;
+    KTRY(hh_synth_launch(t.type, name_key(seed, t.name.c_str()), t.rows, t.cols, cc, cq, t.mean, t.d,
+                         m->ctx->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  return HH_OK;
+}
+
+int hh_model_reset(hh_model* m) {
+  if (!m) return fail(HH_ERR_INVALID, "null model");
+  hipStream_t s = m->ctx->stream;
+  if (m->kv) HIP_TRY(hipMemsetAsync(m->kv, 0, m->kv_bytes, s));
+  if (m->rec) HIP_TRY(hipMemsetAsync(m->rec, 0, m->rec_bytes, s));
+  HIP_TRY(hipMemsetAsync(m->counts, 0, sizeof(int) * m->cfg.vocab, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return HH_OK;
+}
+
+int hh_model_prefill_kv_synthetic(hh_model* m, uint64_t seed, int n_pos) {
+  if (!m) return fail(HH_ERR_INVALID, "null model");
+  if (n_pos < 0 || n_pos > m->cfg.max_seq) return fail(HH_ERR_RANGE, "n_pos beyond max_seq");
+  float cs = 1.0f / 37837.227f;
+  char b[64];
+  for (int i = 0; i < m->cfg.n_layers; ++i) {
+    Layer& L = m->layers[i];
+    if (L.gdn) continue;
+    snprintf(b, sizeof b, "blk.%d.kv_k", i);
+    KTRY(hh_kv_synth_launch(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->cfg.max_seq, cs,
+                            L.k_cache, m->ctx->stream));
+    snprintf(b, sizeof b, "blk.%d.kv_v", i);
+    KTRY(hh_kv_synth_launch(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->cfg.max_seq, cs,
+                            L.v_cache, m->ctx->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  return HH_OK;
+}
+
+int hh_model_set_cancel(hh_model* m, int cancel) {
+  if (!m) return fail(HH_ERR_INVALID, "null model");
+  m->cancel = cancel;
+  return HH_OK;
+}
+
+int hh_model_forward(hh_model* m, uint32_t token, int pos, float* logits_host, uint32_t* argmax_host) {
+  if (!m) return fail(HH_ERR_INVALID, "null model");
+  if (m->cancel) return fail(HH_ERR_CANCELLED, "Cancelled");
+  if (token >= (uint32_t)m->cfg.vocab) return fail(HH_ERR_RANGE, "token id out of range");
+  if (pos < 0 || pos >= m->cfg.max_seq) return fail(HH_ERR_RANGE, "position beyond max_seq");
+  hipStream_t s = m->ctx->stream;
+  StepState st{};
+  st.pos = pos;
+  st.step = 0;
+  st.token = (int)token;
+  st.n_prompt = 1;
+  st.update = 0;
+  HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipGraphLaunch(m->gexec, s));
+  if (logits_host)
+    HIP_TRY(hipMemcpyAsync(logits_host, m->logits, sizeof(float) * m->cfg.vocab, hipMemcpyDeviceToHost, s));
+  StepState out{};
+  HIP_TRY(hipMemcpyAsync(&out, m->state, sizeof out, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (argmax_host) *argmax_host = (uint32_t)out.argmax;
+  return HH_OK;
+}
+
+int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int start_pos, int n_gen, float pen,
+                      uint32_t* out_tokens, float* last_logits) {
+  if (!m || !prompt || (n_gen > 0 && !out_tokens)) return fail(HH_ERR_INVALID, "null argument");
+  if (n_prompt <= 0) return fail(HH_ERR_INVALID, "Empty prompt");
+  if (n_gen < 0 || n_gen > m->max_out) return fail(HH_ERR_RANGE, "n_gen out of range");
+  if (start_pos < 0 || start_pos + n_prompt + n_gen > m->cfg.max_seq)
+    return fail(HH_ERR_RANGE, "sequence exceeds max_seq");
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] >= (uint32_t)m->cfg.vocab) return fail(HH_ERR_RANGE, "prompt token out of range");
+  if (m->cancel) return fail(HH_ERR_CANCELLED, "Cancelled");
+  hipStream_t s = m->ctx->stream;
+  HIP_TRY(hipMemcpyAsync(m->prompt, prompt, sizeof(uint32_t) * n_prompt, hipMemcpyHostToDevice, s));
+  // past_tokens = [last prompt token] (mod.rs:2879); counts start from it
+  KTRY(hh_fill_i32_launch(m->counts, m->cfg.vocab, 0, s));
+  KTRY(hh_count_tokens_launch(m->prompt + (n_prompt - 1), 1, m->counts, s));
+  StepState st{};
+  st.pos = start_pos;
+  st.step = 0;
+  st.token = (int)prompt[0];
+  st.n_prompt = n_prompt;
+  st.update = 1;
+  st.pen = pen;
+  HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
+  // prompt steps (the last one yields the first generated token)
+  for (int i = 0; i < n_prompt; ++i) HIP_TRY(hipGraphLaunch(m->gexec, s));
+  HIP_TRY(hipEventRecord(m->ev0, s));
+  // decode steps: forward each generated token (the last forward only when its logits are wanted)
+  int steps = n_gen - 1 + (last_logits ? 1 : 0);
+  for (int i = 0; i < steps; ++i) HIP_TRY(hipGraphLaunch(m->gexec, s));
+  HIP_TRY(hipEventRecord(m->ev1, s));
+  if (n_gen > 0)
+    HIP_TRY(hipMemcpyAsync(out_tokens, m->out_tokens, sizeof(uint32_t) * n_gen, hipMemcpyDeviceToHost, s));
+  if (last_logits)
+    HIP_TRY(hipMemcpyAsync(last_logits, m->logits, sizeof(float) * m->cfg.vocab, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  m->last_decode_ms = ms;
+  return HH_OK;
+}
+
+int hh_model_time_stages(hh_model* m, int layer, int iters, double* out_ms, int n_out) {
+  if (!m || !out_ms || iters <= 0) return fail(HH_ERR_INVALID, "bad argument");
+  if (layer < 0 || layer >= m->cfg.n_layers) return fail(HH_ERR_RANGE, "layer out of range");
+  hipStream_t s = m->ctx->stream;
+  // keep the head kernel in decode mode with the state untouched between launches
+  StepState st{};
+  HIP_TRY(hipMemcpyAsync(&st, m->state, sizeof st, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  StepState fixed = st;
+  fixed.update = 0;
+  fixed.n_prompt = 1;
+  fixed.step = 0;
+  HIP_TRY(hipMemcpyAsync(m->state, &fixed, sizeof fixed, hipMemcpyHostToDevice, s));
+  for (int stg = 0; stg < n_out && stg < 7; ++stg) {
+    int rc = enqueue_step(m, s, layer, 1u << stg);   // warm
+    if (rc) return rc;
+    HIP_TRY(hipEventRecord(m->ev0, s));
+    for (int i = 0; i < iters; ++i) {
+      rc = enqueue_step(m, s, layer, 1u << stg);
+      if (rc) return rc;
+    }
+    HIP_TRY(hipEventRecord(m->ev1, s));
+    HIP_TRY(hipEventSynchronize(m->ev1));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+    out_ms[stg] = (double)ms / iters;
+  }
+  HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return HH_OK;
+}
+
+int hh_model_last_decode_ms(hh_model* m, double* ms) {
+  if (!m || !ms) return fail(HH_ERR_INVALID, "null argument");
+  *ms = m->last_decode_ms;
+  return HH_OK;
+}
+
+}  // extern "C"

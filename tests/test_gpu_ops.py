@@ -1,0 +1,172 @@
+"""GPU parity of the operators through the C ABI, against the CPU oracle.
+
+Bars: Q8_0 bytes and dequantized weights bit-exact; GEMV within 1e-3 relative
+(max |diff| / max |ref| over the output, fp32 accumulate); f32 ops 1e-4..1e-3."""
+import numpy as np
+import pytest
+
+from tests.fixtures import ref_act, ref_q1_weights, ref_q2_weights
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rel_err(got, want):
+    return float(np.abs(got.astype(np.float64) - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+@pytest.mark.parametrize("n", [32, 40, 4096, 12288, 100000])
+def test_quantize_bit_exact(ctx, oracle, n):
+    print(f"quantize n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * rng.uniform(1e-3, 50)).astype(np.float32)
+    x[:32] = 0.0          # an all-zero block
+    if n > 64:
+        x[40] = 127.0
+        x[41:64] = np.float32(0.5)
+    out = torch.zeros((n + 31) // 32 * 34, dtype=torch.uint8, device="cuda")
+    ctx.quantize_q8_0(dev(x), n, out)
+    assert np.array_equal(host(out), oracle.quantize_q8_0(x))
+
+
+@pytest.mark.parametrize("t", [8, 41, 42, 43, 142])
+def test_dequantize_bit_exact(ctx, oracle, t):
+    n = 128 * 256
+    w = oracle.synth_tensor(t, 3, "w", 1, n, 0.02, 0.0)
+    out = torch.zeros(n, dtype=torch.float32, device="cuda")
+    ctx.dequantize(t, dev(w), n, out)
+    assert np.array_equal(host(out), oracle.dequantize(t, w, n))
+
+
+SHAPES = [(6144, 2048), (2048, 6144), (151936, 2048), (4096, 4096), (12288, 4096), (4096, 12288),
+          (1, 4096), (3, 256), (37, 5120), (5120, 17408)]
+
+
+@pytest.mark.parametrize("t", [42, 41])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_gemv_parity(ctx, oracle, t, shape):
+    n_rows, n_cols = shape
+    print(f"gemv t={t} shape={shape}", flush=True)
+    w = oracle.synth_tensor(t, 11, f"w{n_rows}x{n_cols}", n_rows, n_cols, 0.02, 0.0, threads=8)
+    rng = np.random.default_rng(n_rows * 7 + n_cols)
+    a = oracle.quantize_q8_0(rng.standard_normal(n_cols).astype(np.float32))
+    want = oracle.gemv(t, w, n_rows, n_cols, a, threads=8)
+    y = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
+    ctx.gemv_q8(t, dev(w), n_rows, n_cols, dev(a), y)
+    assert rel_err(host(y), want) < 1e-3
+
+
+@pytest.mark.parametrize("shape", [(151936, 4096), (64, 2048), (5, 64)])
+def test_gemv_q8_head_parity(ctx, oracle, shape):
+    n_rows, n_cols = shape
+    w = oracle.synth_tensor(8, 12, "head", n_rows, n_cols, 0.02, 0.0, threads=8)
+    a = oracle.quantize_q8_0(np.random.default_rng(1).standard_normal(n_cols).astype(np.float32))
+    want = oracle.gemv(8, w, n_rows, n_cols, a, threads=8)
+    y = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
+    ctx.gemv_q8(8, dev(w), n_rows, n_cols, dev(a), y)
+    assert rel_err(host(y), want) < 1e-3
+
+
+@pytest.mark.parametrize("n", [128, 256, 2048, 6144])
+def test_gemv_reference_generators(ctx, oracle, n):
+    """q2_0.rs:939-986 / q1_0g128.rs:1504-1551 byte generators (codes include 3,
+    activations include -128): the device matches the scalar reference kernel."""
+    for salt in (53, 97):
+        a = ref_act(n, salt)
+        for t, w in ((42, ref_q2_weights(n)), (41, ref_q1_weights(n))):
+            want = oracle.dot(t, w, a, n)
+            y = torch.zeros(1, dtype=torch.float32, device="cuda")
+            ctx.gemv_q8(t, dev(w), 1, n, dev(a), y)
+            got = host(y)[0]
+            assert abs(got - want) <= 1e-5 * max(1.0, abs(want)), (t, n, salt, got, want)
+
+
+def test_gemv_errors(ctx):
+    from hearth_amd import HHError
+    w = torch.zeros(1024, dtype=torch.uint8, device="cuda")
+    y = torch.zeros(4, dtype=torch.float32, device="cuda")
+    with pytest.raises(HHError) as e:
+        ctx.gemv_q8(42, w, 4, 100, w, y)       # not a multiple of 256
+    assert e.value.status == 3
+    with pytest.raises(HHError) as e:
+        ctx.gemv_q8(2, w, 4, 256, w, y)        # Q4_0: not on this path
+    assert e.value.status == 2
+
+
+def test_rms_norm_rope_attention(ctx, oracle):
+    lib = oracle.load()
+    rng = np.random.default_rng(5)
+    n, rows = 4096, 3
+    x = rng.standard_normal(rows * n).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    out = torch.zeros(rows * n, dtype=torch.float32, device="cuda")
+    ctx.rms_norm(dev(x), dev(w), 1e-6, rows, n, out)
+    got = host(out)
+    for r in range(rows):
+        want = np.zeros(n, np.float32)
+        lib.ho_rms_norm(x[r * n:].ctypes.data, w.ctypes.data, 1e-6, n, want.ctypes.data)
+        assert rel_err(got[r * n:(r + 1) * n], want) < 1e-5
+    # rope
+    max_seq, hd = 256, 128
+    tab = np.zeros(max_seq * hd, np.float32)
+    lib.ho_rope_table(max_seq, hd, 1e6, tab.ctypes.data)
+    q = rng.standard_normal(8 * hd).astype(np.float32)
+    qd = dev(q)
+    ctx.rope(qd, 8, hd, hd, dev(tab), max_seq, 77)
+    want = q.copy()
+    for h in range(8):
+        hh = want[h * hd:(h + 1) * hd].copy()
+        lib.ho_rope_apply(tab.ctypes.data, max_seq, hd, hh.ctypes.data, 77)
+        want[h * hd:(h + 1) * hd] = hh
+    assert np.array_equal(host(qd), want)
+    # attention (GQA 32/8, hd 128, seq 2049)
+    for (nh, nkv, hd, seq) in ((32, 8, 128, 2049), (16, 4, 256, 300), (16, 8, 128, 1)):
+        ms = seq + 7
+        qv = rng.standard_normal(nh * hd).astype(np.float32)
+        kc = rng.standard_normal(nkv * ms * hd).astype(np.float32)
+        vc = rng.standard_normal(nkv * ms * hd).astype(np.float32)
+        o = torch.zeros(nh * hd, dtype=torch.float32, device="cuda")
+        ctx.attention(dev(qv), dev(kc), dev(vc), nh, nkv, hd, ms, seq, o)
+        got = host(o)
+        want = np.zeros(nh * hd, np.float32)
+        scr = np.zeros(seq, np.float32)
+        for qh in range(nh):
+            kvh = qh // (nh // nkv)
+            lib.ho_attention(qv[qh * hd:].ctypes.data, kc[kvh * ms * hd:].ctypes.data, vc[kvh * ms * hd:].ctypes.data,
+                             seq, hd, want[qh * hd:].ctypes.data, scr.ctypes.data)
+        assert rel_err(got, want) < 1e-4, (nh, nkv, hd, seq)
+
+
+def test_argmax_rules(ctx, oracle):
+    lib = oracle.load()
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for n, pos in ((151936, 42), (151936, 0), (248320, 123456), (1000, 999)):
+        x = np.random.default_rng(n + pos).standard_normal(n).astype(np.float32)
+        x[pos] = 100.0
+        for rule in (0, 1):
+            ctx.argmax(dev(x), n, None, 0, 1.0, rule, out)
+            assert int(host(out)[0]) == pos
+    # ties
+    x = np.zeros(100000, np.float32)
+    x[[5, 70000, 99999]] = 3.0
+    ctx.argmax(dev(x), x.size, None, 0, 1.0, 0, out)
+    assert int(host(out)[0]) == 99999
+    ctx.argmax(dev(x), x.size, None, 0, 1.0, 1, out)
+    assert int(host(out)[0]) == 5
+    # repetition penalty with repeated past tokens
+    x = np.random.default_rng(9).standard_normal(50000).astype(np.float32)
+    x[[10, 20]] = [5.0, 4.9]
+    past = np.array([10, 10, 3, 10], np.uint32)
+    ctx.argmax(dev(x), x.size, dev(past), 4, 1.1, 0, out)
+    want = lib.ho_sample_greedy_dense(x.copy().ctypes.data, x.size, past.ctypes.data, 4, 1.1)
+    assert int(host(out)[0]) == want == 20

@@ -1,0 +1,119 @@
+"""CPU pins of the oracle's f32 operators and greedy selection (ops.rs,
+hearth-sampler lib.rs, qwen35.rs) via invariants, numpy brute force and the
+reference tests' known answers."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def test_rms_norm_unit_rms(oracle):
+    lib = oracle.load()
+    rng = np.random.default_rng(0)
+    for n in (7, 128, 4096, 4100):
+        x = rng.standard_normal(n).astype(np.float32) * 3
+        w = np.ones(n, np.float32)
+        out = np.zeros(n, np.float32)
+        lib.ho_rms_norm(_p(x), _p(w), 1e-6, n, _p(out))
+        assert abs(np.sqrt(np.mean(out.astype(np.float64) ** 2)) - 1.0) < 1e-5
+        ref = x / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6)
+        assert np.allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_is_rotation(oracle):
+    lib = oracle.load()
+    max_seq, rd = 64, 128
+    tab = np.zeros(max_seq * rd, np.float32)
+    lib.ho_rope_table(max_seq, rd, 1e6, _p(tab))
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(128).astype(np.float32)
+    for pos in (0, 1, 17, 63):
+        y = x.copy()
+        lib.ho_rope_apply(_p(tab), max_seq, rd, _p(y), pos)
+        assert abs(np.linalg.norm(y) - np.linalg.norm(x)) < 1e-4
+        half = rd // 2
+        ang = pos * (1.0 / 1e6 ** (2.0 * np.arange(half) / rd))
+        want0 = x[:half] * np.cos(ang) - x[half:] * np.sin(ang)
+        want1 = x[:half] * np.sin(ang) + x[half:] * np.cos(ang)
+        assert np.allclose(y, np.concatenate([want0, want1]), atol=2e-5)
+    y = x.copy()
+    lib.ho_rope_apply(_p(tab), max_seq, rd, _p(y), 0)
+    assert np.array_equal(y, x)
+
+
+def test_softmax_and_attention(oracle):
+    lib = oracle.load()
+    rng = np.random.default_rng(2)
+    for n in (1, 5, 64, 2049):
+        x = rng.standard_normal(n).astype(np.float32) * 4
+        y = x.copy()
+        lib.ho_softmax(_p(y), n)
+        assert abs(y.astype(np.float64).sum() - 1.0) < 1e-5
+        e = np.exp(x - x.max())
+        assert np.allclose(y, e / e.sum(), rtol=1e-5, atol=1e-8)
+    hd, seq = 128, 300
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal((seq, hd)).astype(np.float32)
+    v = rng.standard_normal((seq, hd)).astype(np.float32)
+    out = np.zeros(hd, np.float32)
+    scr = np.zeros(seq, np.float32)
+    lib.ho_attention(_p(q), _p(k), _p(v), seq, hd, _p(out), _p(scr))
+    s = k.astype(np.float64) @ q / np.sqrt(hd)
+    p = np.exp(s - s.max())
+    p /= p.sum()
+    assert np.allclose(out, p @ v, rtol=1e-4, atol=1e-5)
+
+
+def test_silu_known_answer(oracle):
+    x = np.array([1.0, 0.0, -1.0], np.float32)
+    oracle.load().ho_silu(_p(x), 3)
+    assert abs(x[0] - 0.7310586) < 1e-6 and x[1] == 0.0   # ops.rs:1186-1190
+
+
+def test_greedy_rules(oracle):
+    lib = oracle.load()
+    none = np.zeros(1, np.uint32)
+    # hearth-sampler lib.rs:214-233 known answers
+    for logits, want in (([-1.0, -2.0, 5.0, 0.5], 2), ([0.1, 0.2, 0.7, 0.05], 2)):
+        a = np.array(logits, np.float32)
+        assert lib.ho_sample_greedy_dense(_p(a), 4, _p(none), 0, 1.0) == want
+    # ties: max_by keeps the LAST maximum; the qwen35 scan keeps the FIRST
+    a = np.array([1.0, 3.0, 3.0, 2.0, 3.0], np.float32)
+    assert lib.ho_sample_greedy_dense(_p(a.copy()), 5, _p(none), 0, 1.0) == 4
+    assert lib.ho_argmax_first(_p(a), 5) == 1
+    # repetition penalty: positive logits divided, negative multiplied, once per occurrence
+    a = np.array([2.0, 2.1, -0.5, -0.4], np.float32)
+    past = np.array([1, 1, 3], np.uint32)
+    b = a.copy()
+    tok = lib.ho_sample_greedy_dense(_p(b), 4, _p(past), 3, 1.1)
+    assert tok == 0
+    assert b[1] == np.float32(np.float32(2.1) / np.float32(1.1)) / np.float32(1.1)
+    assert b[3] == np.float32(-0.4) * np.float32(1.1)
+    # penalty 1.0 (within 1e-6) is a no-op
+    b = a.copy()
+    assert lib.ho_sample_greedy_dense(_p(b), 4, _p(past), 3, 1.0000001) == 1
+
+
+def test_synth_generator_properties(oracle):
+    lib = oracle.load()
+    key = lib.ho_name_key(7, b"x")
+    v = np.array([lib.ho_synth_int(key, i) for i in range(20000)], np.float64)
+    assert abs(v.mean()) < 1500 and abs(v.std() / 37837.23 - 1) < 0.03
+    # ternary: ~31% zeros (|w| < absmean/2 for a Gaussian), codes in {0,1,2}
+    w = oracle.synth_tensor(42, 1, "t", 64, 1024, 0.02, 0.0)
+    codes = np.stack([(w.reshape(-1, 34)[:, 2:] >> (2 * k)) & 3 for k in range(4)])
+    frac0 = (codes == 1).mean()
+    assert 0.28 < frac0 < 0.35 and not (codes == 3).any()
+    # absmean scale: f16(sum|I| * c / 128)
+    deq = oracle.dequantize(42, w, 64 * 1024)
+    assert abs(np.abs(deq[deq != 0]).mean() / (0.02 * 0.7979) - 1) < 0.05
+    # Q8_0 synth == quantize(float weights)
+    q8 = oracle.synth_tensor(8, 1, "e", 2, 64, 0.02, 0.0)
+    c = lib.ho_synth_scale(0.02)
+    k2 = lib.ho_name_key(1, b"e")
+    f = np.array([lib.ho_synth_int(k2, i) for i in range(128)], np.float32) * np.float32(c)
+    assert np.array_equal(q8, oracle.quantize_q8_0(f))
