@@ -1,7 +1,10 @@
 """Builds the gfx950 library hearth_amd/libhearth_hip.so with hipcc (in-tree).
 
 Every HIP source is compiled for gfx950 only, with packed-FP32 instructions
-disabled (-packed-fp32-ops) and IEEE-exact f32 division/sqrt (hipcc default).
+disabled (-packed-fp32-ops), IEEE-exact f32 division/sqrt, and no implicit
+multiply-add contraction (-ffp-contract=off): element-wise arithmetic rounds
+exactly like the reference's Rust code, and kernels that want a fused
+multiply-add say so with fmaf().
 """
 import os
 import subprocess
@@ -17,7 +20,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-fno-fast-math", "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-fno-fast-math", "-fhip-fp32-correctly-rounded-divide-sqrt", "-ffp-contract=off",
     "-Wall", "-Wno-unused-result", "-Wno-unused-value",
 ]
 

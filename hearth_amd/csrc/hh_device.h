@@ -37,7 +37,90 @@ template <> struct UnitT<FMT_Q8> { static constexpr int EL = 64, DW = 17, BYTES 
 template <int FMT> HH_DEV constexpr int qstride() { return UnitT<FMT>::EL + 16; }
 
 HH_DEV float h2f(uint32_t h16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(h16 & 0xffffu)); }
-HH_DEV uint32_t f2h(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// f32 -> f16 bits, round to nearest even (half 2.7.1 f16::from_f32), written
+// with integer operations.  A plain (_Float16) cast is not used because the
+// compiler may fold fptrunc(a * b) into a mixed-precision multiply that rounds
+// the exact product to f16 once, which differs from rounding the f32 product
+// when that product sits exactly on an f16 tie.
+HH_DEV uint32_t f2h(float xf) {
+  uint32_t x = __float_as_uint(xf);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t exp = (x >> 23) & 0xffu;
+  uint32_t man = x & 0x7fffffu;
+  if (exp == 0xffu) return sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u);
+  int half_exp = (int)exp - 127 + 15;
+  if (half_exp >= 0x1f) return sign | 0x7c00u;
+  if (half_exp <= 0) {
+    if (14 - half_exp > 24) return sign;
+    man |= 0x800000u;
+    uint32_t shift = (uint32_t)(14 - half_exp);
+    uint32_t half_man = man >> shift;
+    uint32_t round_bit = 1u << (shift - 1);
+    if ((man & round_bit) && (man & (3u * round_bit - 1u))) half_man++;
+    return sign | half_man;
+  }
+  uint32_t r = sign | ((uint32_t)half_exp << 10);
+  r += man >> 13;
+  if ((man & 0x1000u) && (man & 0x2fffu)) r++;
+  return r;
+}
+
+// exp and log used by every transcendental of the path (softmax, silu,
+// sigmoid, softplus, the GDN decay).  Cody & Waite range reduction
+// x = n ln2 + r (ln2 split in a 16-bit-exact high part and a low part), then the
+// Taylor series of e^r to degree 7 (|r| <= ln2/2: truncation < 2^-27) and a
+// two-step power-of-two scale (inputs below -87.33, whose results would be
+// subnormal, give 0); log via m = 2^-e x in [sqrt(1/2), sqrt(2)),
+// s = (m-1)/(m+1), log m = 2 atanh(s) (odd series to s^13).  Every step is an
+// IEEE single operation with explicit fmaf, so the CPU checker evaluates the
+// identical function bit for bit.  Accuracy ~1-2 ulp (tested against libm).
+HH_DEV float hx_exp(float x) {
+  if (x != x) return x;
+  if (x > 88.72f) return __uint_as_float(0x7f800000u);
+  if (x < -87.33f) return 0.0f;   // results below the normal range are flushed (both sides)
+  float n = rintf(x * 1.44269504088896341f);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.428606765330187e-06f, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  int n1 = ni / 2, n2 = ni - n1;
+  return p * __uint_as_float((uint32_t)(127 + n1) << 23) * __uint_as_float((uint32_t)(127 + n2) << 23);
+}
+HH_DEV float hx_log(float x) {
+  if (!(x > 0.0f)) return x == 0.0f ? __uint_as_float(0xff800000u) : __uint_as_float(0x7fc00000u);
+  if (x == __uint_as_float(0x7f800000u)) return x;
+  uint32_t b = __float_as_uint(x);
+  int e;
+  if ((b >> 23) == 0) {  // subnormal: scale up by 2^23
+    x = x * 8388608.0f;
+    b = __float_as_uint(x);
+    e = (int)(b >> 23) - 127 - 23;
+  } else {
+    e = (int)(b >> 23) - 127;
+  }
+  float m = __uint_as_float((b & 0x7fffffu) | 0x3f800000u);
+  if (m > 1.41421356f) { m = m * 0.5f; e += 1; }
+  float s = (m - 1.0f) / (m + 1.0f);
+  float s2 = s * s;
+  float p = 1.0f / 13.0f;
+  p = fmaf(p, s2, 1.0f / 11.0f);
+  p = fmaf(p, s2, 1.0f / 9.0f);
+  p = fmaf(p, s2, 1.0f / 7.0f);
+  p = fmaf(p, s2, 1.0f / 5.0f);
+  p = fmaf(p, s2, 1.0f / 3.0f);
+  p = fmaf(p, s2, 1.0f);
+  float lm = (2.0f * s) * p;
+  float fe = (float)e;
+  return fmaf(fe, 0.693145751953125f, fmaf(fe, 1.428606765330187e-06f, lm));
+}
 
 // Position of element e (within the vector) in the permuted int8 array.
 //   Q2: chunk of 16; element 4i+k -> k*4+i     (matches (D >> 2k) & 0x03030303)
@@ -75,6 +158,23 @@ HH_DEV float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+// Sum of squares of a K-vector (K % 1024 == 0) by a 256-lane workgroup in a
+// fixed order: lane t sums its float4s x[4t + 1024k .. +3] as
+// ss + (((x0^2 + x1^2) + x2^2) + x3^2), waves reduce by butterfly, then
+// (w0 + w1) + (w2 + w3).  Every full-width RMSNorm of the path uses this order.
+HH_DEV float block_sumsq_f4(const float* __restrict__ x, int K, float* red4) {
+  const int tid = threadIdx.x;
+  float ss = 0.0f;
+  for (int e = tid * 4; e < K; e += 1024) {
+    float4 v = *(const float4*)(x + e);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red4[tid >> 6] = ss;
+  __syncthreads();
+  return (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
 // Reductions over aligned groups of W lanes (W power of two <= 64).
 template <int W> HH_DEV float group_max(float v) {
 #pragma unroll

@@ -23,7 +23,7 @@
 
 namespace {
 
-HH_DEV float softplus_f(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+HH_DEV float softplus_f(float x) { return x > 20.0f ? x : hx_log(1.0f + hx_exp(x)); }
 
 __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
     const float* w = a.conv_w + (size_t)ch * K;
     float acc = 0.0f;
     for (int t = 0; t < K; ++t) acc += w[t] * win[t];
-    float y = acc / (1.0f + expf(-acc));             // silu
+    float y = acc / (1.0f + hx_exp(-acc));             // silu
     if (ch < 2 * kdim) {
       // L2 norm over the 128-channel head this lane belongs to (2 waves per head)
       float ss = wave_sum(y * y);
@@ -59,12 +59,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   // alpha/beta for v-heads [4*j, 4*j+4)
   extern __shared__ float xs[];   // d floats: rms_norm(hidden, attn_norm)
   const int d = a.d;
-  float ss = 0.0f;
-  for (int i = tid; i < d; i += 256) ss += a.hidden[i] * a.hidden[i];
-  ss = wave_sum(ss);
-  if (lane == 0) red[wid] = ss;
-  __syncthreads();
-  float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  float tot = block_sumsq_f4(a.hidden, d, red);
   float inv = 1.0f / sqrtf(tot / (float)d + a.eps);
   for (int i = tid; i < d; i += 256) xs[i] = a.hidden[i] * inv * a.attn_norm[i];
   __syncthreads();
@@ -81,7 +76,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   sb = wave_sum(sb);
   if (lane == 0) {
     a.ab[h] = softplus_f(sa + a.dt_bias[h]) * a.ssm_a[h];
-    a.ab[a.n_v + h] = 1.0f / (1.0f + expf(-sb));
+    a.ab[a.n_v + h] = 1.0f / (1.0f + hx_exp(-sb));
   }
 }
 
@@ -96,7 +91,7 @@ __global__ __launch_bounds__(256) void k_gdn_rec(GdnArgs a) {
   const int kdim = a.n_k * hd;
   const float* qn = a.qk + (size_t)kg * hd;
   const float* kn = a.qk + kdim + (size_t)kg * hd;
-  const float decay = expf(a.ab[h]);
+  const float decay = hx_exp(a.ab[h]);
   const float b = a.ab[a.n_v + h];
   float* S = a.state + (size_t)h * hd * hd;
   __shared__ float part[8][33];
@@ -152,7 +147,7 @@ __global__ __launch_bounds__(256) void k_gdn_rec(GdnArgs a) {
     int dd = k * 64 + lane;
     float nv = vals[k] * inv * a.ssm_norm[dd];
     float z = a.z[(size_t)h * hd + dd];
-    float o = nv * (z / (1.0f + expf(-z)));
+    float o = nv * (z / (1.0f + hx_exp(-z)));
     if (a.out_f32) a.out_f32[(size_t)h * hd + dd] = o;
     float am = group_max<32>(fabsf(o));
     float sc = q8_scale(am);

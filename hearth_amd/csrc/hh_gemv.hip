@@ -38,8 +38,13 @@ constexpr uint32_t M1 = 0x01010101u;
 HH_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
 // ---- unit dot products: w = unit dwords, aq/ad/as = the unit's activation ----
-HH_DEV float unit_q2(const uint32_t (&w)[17], const int8_t* aq, const float* ad, const int* as) {
-  float acc = 0.0f;
+// Each returns the two per-block products p[blk] = block_acc * w_scale with the
+// scalar kernels' exact fp32 operation order (separate multiply and add, no
+// contraction): block_acc = (((0 + s0*d0) + s1*d1) + s2*d2) + s3*d3.  The row
+// sum then adds the products in block order, so a row equals the scalar
+// DotFn bit for bit.
+HH_DEV void unit_q2(const uint32_t (&w)[17], const int8_t* aq, const float* ad, const int* as, float (&pr)[2]) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     uint32_t c[8];
@@ -71,13 +76,12 @@ HH_DEV float unit_q2(const uint32_t (&w)[17], const int8_t* aq, const float* ad,
       s -= as[blk * 4 + sub];                 // sum (code-1)*a = sum code*a - sum a
       bacc += (float)s * ad[blk * 4 + sub];   // block_acc += dot * a_scale
     }
-    acc += bacc * dw;                         // sum += block_acc * w_scale
+    pr[blk] = bacc * dw;                      // sum += block_acc * w_scale
   }
-  return acc;
 }
 
-HH_DEV float unit_q1(const uint32_t (&w)[9], const int8_t* aq, const float* ad, const int* as) {
-  float acc = 0.0f;
+HH_DEV void unit_q1(const uint32_t (&w)[9], const int8_t* aq, const float* ad, const int* as, float (&pr)[2]) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     uint32_t c[4];
@@ -109,13 +113,12 @@ HH_DEV float unit_q1(const uint32_t (&w)[9], const int8_t* aq, const float* ad, 
       s = 2 * s - as[blk * 4 + sub];          // sum (+-1)*a = 2*sum bit*a - sum a
       bacc += (float)s * ad[blk * 4 + sub];
     }
-    acc += bacc * dw;
+    pr[blk] = bacc * dw;
   }
-  return acc;
 }
 
-HH_DEV float unit_q8(const uint32_t (&w)[17], const int8_t* aq, const float* ad, const int* /*as*/) {
-  float acc = 0.0f;
+HH_DEV void unit_q8(const uint32_t (&w)[17], const int8_t* aq, const float* ad, const int* /*as*/, float (&pr)[2]) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     uint32_t c[8];
@@ -134,9 +137,8 @@ HH_DEV float unit_q8(const uint32_t (&w)[17], const int8_t* aq, const float* ad,
     int s = 0;
     s = sdot4(c[0], a0.x, s); s = sdot4(c[1], a0.y, s); s = sdot4(c[2], a0.z, s); s = sdot4(c[3], a0.w, s);
     s = sdot4(c[4], a1.x, s); s = sdot4(c[5], a1.y, s); s = sdot4(c[6], a1.z, s); s = sdot4(c[7], a1.w, s);
-    acc += (float)s * dw * ad[blk];           // sumf += sumi as f32 * d0 * d1
+    pr[blk] = (float)s * dw * ad[blk];        // sumf += sumi as f32 * d0 * d1
   }
-  return acc;
 }
 
 template <int FMT> HH_DEV void load_unit(uint32_t (&w)[UnitT<FMT>::DW], const uint8_t* p) {
@@ -156,11 +158,11 @@ template <int FMT> HH_DEV void load_unit(uint32_t (&w)[UnitT<FMT>::DW], const ui
   }
 }
 
-template <int FMT> HH_DEV float unit_dot(const uint32_t (&w)[UnitT<FMT>::DW], const int8_t* aq,
-                                         const float* ad, const int* as) {
-  if constexpr (FMT == FMT_Q2) return unit_q2(w, aq, ad, as);
-  else if constexpr (FMT == FMT_Q1) return unit_q1(w, aq, ad, as);
-  else return unit_q8(w, aq, ad, as);
+template <int FMT> HH_DEV void unit_dot(const uint32_t (&w)[UnitT<FMT>::DW], const int8_t* aq,
+                                        const float* ad, const int* as, float (&pr)[2]) {
+  if constexpr (FMT == FMT_Q2) unit_q2(w, aq, ad, as, pr);
+  else if constexpr (FMT == FMT_Q1) unit_q1(w, aq, ad, as, pr);
+  else unit_q8(w, aq, ad, as, pr);
 }
 
 // Packed activation into LDS from a dense f32 vector x (optionally RMS-normed).
@@ -171,15 +173,7 @@ HH_DEV void prologue_quant(const float* __restrict__ x, const float* __restrict_
   const int tid = threadIdx.x;
   float inv = 1.0f;
   if (rmsnorm) {
-    float ss = 0.0f;
-    for (int e = tid * 4; e < K; e += 1024) {
-      float4 v = *(const float4*)(x + e);
-      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    float tot = block_sumsq_f4(x, K, red);
     inv = 1.0f / sqrtf(tot / (float)K + eps);   // ops.rs:22-23
   }
   for (int e = tid * 4; e < K; e += 1024) {
@@ -302,7 +296,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
   float* ad = (float*)(smem + nunits_act * qstride<FMT>());
   int* as = (int*)(ad + K / 32);
   float* part = (float*)(as + K / 32);
-  float* red = part + U;
+  float* red = part + 2 * U;
   float* rowsum = red + 8;
 
   auto unit_addr = [&](int lu) -> const uint8_t* {
@@ -330,7 +324,9 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
       int lu = (b * DEPTH + d) * 256 + tid;
       if (lu < U) {
         int t = lu % P;
-        part[lu] = unit_dot<FMT>(wr[d], aq + t * qstride<FMT>(), ad + t * SUBS, as + t * SUBS);
+        float pr[2];
+        unit_dot<FMT>(wr[d], aq + t * qstride<FMT>(), ad + t * SUBS, as + t * SUBS, pr);
+        *(float2*)(part + 2 * lu) = make_float2(pr[0], pr[1]);
       }
     }
   };
@@ -350,11 +346,11 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
   }
   __syncthreads();
 
-  // per-row sums in unit order
+  // per-row sums over the block products in block order (the scalar loop)
   for (int r = tid; r < rows_total; r += 256) {
-    const float* pr = part + r * P;
+    const float* pr = part + 2 * r * P;
     float s = 0.0f;
-    for (int t = 0; t < P; ++t) s += pr[t];
+    for (int t = 0; t < 2 * P; ++t) s += pr[t];
     rowsum[r] = s;
   }
   __syncthreads();
@@ -372,7 +368,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
       float h = 0.0f;
       if (i < R2) {
         float g = rowsum[i];
-        float sg = g / (1.0f + expf(-g));
+        float sg = g / (1.0f + hx_exp(-g));
         h = sg * rowsum[R2 + i];
       }
       float am = group_max<32>(fabsf(h));
@@ -523,7 +519,7 @@ size_t hh_gemv_lds(int fmt, int K, int rows_total_per_wg) {
   int el = hh_unit_el(fmt);
   int P = K / el;
   size_t qb = (size_t)(K / el) * (el + 16);
-  size_t b = qb + (size_t)(K / 32) * 8 + (size_t)rows_total_per_wg * P * 4 + 8 * 4 + (size_t)rows_total_per_wg * 4;
+  size_t b = qb + (size_t)(K / 32) * 8 + (size_t)rows_total_per_wg * P * 8 + 8 * 4 + (size_t)rows_total_per_wg * 4;
   return (b + 15) & ~(size_t)15;
 }
 

@@ -246,7 +246,10 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
       float acc = 0.0f;
       for (int d4 = 0; d4 < hd / 4; ++d4) {
         float4 k4 = kq[d4], q4 = qq[d4];
-        acc += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+        acc = fmaf(q4.x, k4.x, acc);
+        acc = fmaf(q4.y, k4.y, acc);
+        acc = fmaf(q4.z, k4.z, acc);
+        acc = fmaf(q4.w, k4.w, acc);
       }
       sc_v = acc * inv_sqrt;
     }
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   for (int h = wid; h < G; h += 4) {
     float v = lane < C ? sc[h * C + lane] : -INFINITY;
     float m = wave_max(v);
-    float e = (lane < np) ? expf(v - m) : 0.0f;
+    float e = (lane < np) ? hx_exp(v - m) : 0.0f;
     float l = wave_sum(e);
     if (lane < C) sc[h * C + lane] = e;
     if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   for (int idx = tid; idx < G * hd; idx += 256) {
     int h = idx / hd, d = idx % hd;
     float acc = 0.0f;
-    for (int j = 0; j < np; ++j) acc += sc[h * C + j] * Vs[j * hd + d];
+    for (int j = 0; j < np; ++j) acc = fmaf(sc[h * C + j], Vs[j * hd + d], acc);
     a.part_o[(pbase + h) * hd + d] = acc;
   }
   if (tid < G) {
@@ -292,7 +295,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     M = wave_max(M);
     float L = 0.0f;
     for (int t = lane; t < n_active; t += 64) {
-      float e = expf(a.part_ml[(hb + (size_t)t * G) * 2] - M);
+      float e = hx_exp(a.part_ml[(hb + (size_t)t * G) * 2] - M);
       wts[h * a.max_splits + t] = e;
       L += e * a.part_ml[(hb + (size_t)t * G) * 2 + 1];
     }
@@ -302,11 +305,11 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     for (int d0 = 0; d0 < hd; d0 += 64) {
       int d = d0 + lane;
       float o = 0.0f;
-      for (int t = 0; t < n_active; ++t) o += wts[h * a.max_splits + t] * a.part_o[(hb + (size_t)t * G) * hd + d];
+      for (int t = 0; t < n_active; ++t) o = fmaf(wts[h * a.max_splits + t], a.part_o[(hb + (size_t)t * G) * hd + d], o);
       o = o * invL;
       if (a.gated) {   // qwen35.rs:1627-1629 attn_out /= 1 + exp(-gate)
         float g = a.qkv[(size_t)qh * 2 * hd + hd + d];
-        o = o / (1.0f + expf(-g));
+        o = o / (1.0f + hx_exp(-g));
       }
       if (a.out_f32) a.out_f32[(size_t)qh * hd + d] = o;
       if (a.act_out) {
@@ -402,6 +405,7 @@ __global__ void k_fill_i32(int* p, int64_t n, int v) {
 // Seeded synthetic tensors (same definition as the CPU checker in tests).
 // ---------------------------------------------------------------------------
 __global__ void k_synth_f32(uint64_t key, int64_t n, float c, float mean, float* out) {
+#pragma clang fp contract(off)
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float t = __fmul_rn((float)synth_int(key, (uint64_t)i), c);

@@ -650,6 +650,8 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
     e = hipMalloc(&m->rec, m->rec_bytes);
     if (e != hipSuccess) { hh_model_destroy(m); return fail(HH_ERR_OOM, "recurrent state allocation failed"); }
   }
+  if (m->kv) HIP_TRY(hipMemset(m->kv, 0, m->kv_bytes));
+  if (m->rec) HIP_TRY(hipMemset(m->rec, 0, m->rec_bytes));
   int ai = 0, gi = 0;
   for (auto& L : m->layers) {
     if (L.gdn) {

@@ -193,13 +193,18 @@ class Ctx:
     """One device context with its own HIP stream."""
 
     def __init__(self, device: int = 0):
+        import weakref
         self.lib = load_library()
         h = C.c_void_p()
         _check(self.lib.hh_ctx_create(device, C.byref(h)))
         self.h = h
+        self._models = weakref.WeakSet()
 
     def close(self) -> None:
+        """Destroy the context; models created on it are destroyed first."""
         if self.h:
+            for m in list(self._models):
+                m.close()
             self.lib.hh_ctx_destroy(self.h)
             self.h = None
 
@@ -247,11 +252,12 @@ class Model:
         h = C.c_void_p()
         _check(self.lib.hh_model_create(ctx.h, C.byref(self._c), C.byref(h)))
         self.h = h
+        ctx._models.add(self)
 
     def close(self) -> None:
-        if self.h:
+        if self.h and self.ctx.h:
             self.lib.hh_model_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:

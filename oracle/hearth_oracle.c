@@ -91,6 +91,69 @@ float ho_f16_to_f32(uint16_t h) {
   return f;
 }
 
+/* exp / log shared with the device kernels (hearth_amd/csrc/hh_device.h):
+ * Cody & Waite reduction x = n ln2 + r with ln2 = 0.693145751953125 +
+ * 1.428606765330187e-06, Taylor series of e^r to degree 7, power-of-two scale
+ * in two steps; log m (m in [sqrt(1/2), sqrt(2))) = 2 atanh((m-1)/(m+1)) to the
+ * s^13 term.  The reference's own exp is wide::f32x8::exp (a polynomial in the
+ * `wide` crate, used by ops.rs:246/:284/:331) and Rust f32::exp/ln elsewhere;
+ * neither is reproducible bit for bit here (parity unpinned at the ulp level),
+ * so both implementations of this path evaluate this one function. */
+float ho_exp(float x) {
+  if (x != x) return x;
+  if (x > 88.72f) return INFINITY;
+  if (x < -87.33f) return 0.0f;
+  float n = rintf(x * 1.44269504088896341f);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.428606765330187e-06f, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  int n1 = ni / 2, n2 = ni - n1;
+  uint32_t b1 = (uint32_t)(127 + n1) << 23, b2 = (uint32_t)(127 + n2) << 23;
+  float f1, f2;
+  memcpy(&f1, &b1, 4);
+  memcpy(&f2, &b2, 4);
+  return p * f1 * f2;
+}
+
+float ho_log(float x) {
+  if (!(x > 0.0f)) return x == 0.0f ? -INFINITY : NAN;
+  if (isinf(x)) return x;
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  int e;
+  if ((b >> 23) == 0) {
+    x = x * 8388608.0f;
+    memcpy(&b, &x, 4);
+    e = (int)(b >> 23) - 127 - 23;
+  } else {
+    e = (int)(b >> 23) - 127;
+  }
+  uint32_t mb = (b & 0x7fffffu) | 0x3f800000u;
+  float m;
+  memcpy(&m, &mb, 4);
+  if (m > 1.41421356f) { m = m * 0.5f; e += 1; }
+  float s = (m - 1.0f) / (m + 1.0f);
+  float s2 = s * s;
+  float p = 1.0f / 13.0f;
+  p = fmaf(p, s2, 1.0f / 11.0f);
+  p = fmaf(p, s2, 1.0f / 9.0f);
+  p = fmaf(p, s2, 1.0f / 7.0f);
+  p = fmaf(p, s2, 1.0f / 5.0f);
+  p = fmaf(p, s2, 1.0f / 3.0f);
+  p = fmaf(p, s2, 1.0f);
+  float lm = (2.0f * s) * p;
+  float fe = (float)e;
+  return fmaf(fe, 0.693145751953125f, fmaf(fe, 1.428606765330187e-06f, lm));
+}
+
 static inline float rd_f16(const uint8_t* p) { return ho_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
 
 /* ------------------------------------------------------------------------- */
@@ -435,7 +498,7 @@ void ho_rope_apply(const float* table, int max_seq, int rope_dim, float* x, int 
 
 /* ops.rs:240-253 silu. */
 void ho_silu(float* x, int64_t n) {
-  for (int64_t i = 0; i < n; i++) x[i] = x[i] / (1.0f + expf(-x[i]));
+  for (int64_t i = 0; i < n; i++) x[i] = x[i] / (1.0f + ho_exp(-x[i]));
 }
 
 /* ops.rs:308-351 softmax. */
@@ -452,13 +515,13 @@ void ho_softmax(float* x, int64_t n) {
   float lanes[8] = {0};
   for (int64_t i = 0; i < chunks; i++)
     for (int l = 0; l < 8; l++) {
-      float e = expf(x[i * 8 + l] - max_val);
+      float e = ho_exp(x[i * 8 + l] - max_val);
       lanes[l] = fmaf(e, 1.0f, lanes[l]);
       x[i * 8 + l] = e;
     }
   float sum = reduce8(lanes);
   for (int64_t i = n - rem; i < n; i++) {
-    x[i] = expf(x[i] - max_val);
+    x[i] = ho_exp(x[i] - max_val);
     sum += x[i];
   }
   if (sum > 0.0f) {
@@ -624,6 +687,114 @@ void ho_synth_tensor(int type, uint64_t seed, const char* name, int64_t rows, in
   }
 }
 
+
+/* ------------------------------------------------------------------------- */
+/* device association order (ORDER_DEVICE)                                   */
+/* ------------------------------------------------------------------------- */
+/* The same mathematics as the reference-order functions above, with the fp32
+ * additions grouped as the HIP kernels group them, so the two implementations
+ * can be compared bit for bit.  Wave reductions are butterflies over 64 lanes
+ * (lane i adds lane i^o for o = 32..1); the 256-lane vector sum of squares is
+ * lane-strided float4 partials, per-wave butterflies, then (w0+w1)+(w2+w3). */
+
+static float bfly64(const float* v) {
+  float a[64], b[64];
+  memcpy(a, v, sizeof a);
+  for (int o = 32; o > 0; o >>= 1) {
+    for (int i = 0; i < 64; i++) b[i] = a[i] + a[i ^ o];
+    memcpy(a, b, sizeof a);
+  }
+  return a[0];
+}
+
+static float dev_sumsq_block(const float* x, int64_t K) {
+  float lanes[256], w[4];
+  for (int t = 0; t < 256; t++) {
+    float ss = 0.0f;
+    for (int64_t e = 4 * t; e < K; e += 1024) {
+      float q = x[e] * x[e] + x[e + 1] * x[e + 1];
+      q = q + x[e + 2] * x[e + 2];
+      q = q + x[e + 3] * x[e + 3];
+      ss = ss + q;
+    }
+    lanes[t] = ss;
+  }
+  for (int k = 0; k < 4; k++) w[k] = bfly64(lanes + 64 * k);
+  return (w[0] + w[1]) + (w[2] + w[3]);
+}
+
+static void dev_rms_norm_block(const float* x, const float* w, float eps, int64_t K, float* out) {
+  float inv = 1.0f / sqrtf(dev_sumsq_block(x, K) / (float)K + eps);
+  for (int64_t i = 0; i < K; i++) out[i] = x[i] * inv * w[i];
+}
+
+static float dev_sumsq_wave(const float* x, int n) {
+  float lanes[64];
+  for (int l = 0; l < 64; l++) {
+    float ss = 0.0f;
+    for (int d = l; d < n; d += 64) ss = ss + x[d] * x[d];
+    lanes[l] = ss;
+  }
+  return bfly64(lanes);
+}
+
+static void dev_rms_norm_wave(const float* x, const float* w, float eps, int n, float* out) {
+  float inv = 1.0f / sqrtf(dev_sumsq_wave(x, n) / (float)n + eps);
+  for (int i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+}
+
+/* Split-sequence attention for one query head: chunks of C = 4096/hd positions,
+ * per chunk max / exp / butterfly sum / sequential fma of p*v, then the chunks
+ * merged with exp(m_s - M) weights. */
+static void dev_attention(const float* q, const float* k, const float* v, int seq, int hd, float* out) {
+  int C = 4096 / hd, ns = (seq + C - 1) / C;
+  float inv_sqrt = 1.0f / sqrtf((float)hd);
+  float* ms = (float*)malloc(sizeof(float) * (size_t)ns * (hd + 3));
+  float* ls = ms + ns;
+  float* wts = ls + ns;
+  float* os = wts + ns;
+  for (int s = 0; s < ns; s++) {
+    int p0 = s * C, np = seq - p0 < C ? seq - p0 : C;
+    float sc[64], e[64];
+    for (int l = 0; l < 64; l++) sc[l] = -INFINITY;
+    for (int j = 0; j < np; j++) {
+      const float* kr = k + (size_t)(p0 + j) * hd;
+      float acc = 0.0f;
+      for (int d = 0; d < hd; d++) acc = fmaf(q[d], kr[d], acc);
+      sc[j] = acc * inv_sqrt;
+    }
+    float m = -INFINITY;
+    for (int l = 0; l < 64; l++) m = fmaxf(m, sc[l]);
+    for (int l = 0; l < 64; l++) e[l] = l < np ? ho_exp(sc[l] - m) : 0.0f;
+    ms[s] = m;
+    ls[s] = bfly64(e);
+    for (int d = 0; d < hd; d++) {
+      float acc = 0.0f;
+      for (int j = 0; j < np; j++) acc = fmaf(e[j], v[(size_t)(p0 + j) * hd + d], acc);
+      os[(size_t)s * hd + d] = acc;
+    }
+  }
+  float M = -INFINITY;
+  for (int s = 0; s < ns; s++) M = fmaxf(M, ms[s]);
+  float lanes[64];
+  for (int l = 0; l < 64; l++) {
+    float L = 0.0f;
+    for (int t = l; t < ns; t += 64) {
+      float w = ho_exp(ms[t] - M);
+      wts[t] = w;
+      L = L + w * ls[t];
+    }
+    lanes[l] = L;
+  }
+  float invL = 1.0f / bfly64(lanes);
+  for (int d = 0; d < hd; d++) {
+    float o = 0.0f;
+    for (int t = 0; t < ns; t++) o = fmaf(wts[t], os[(size_t)t * hd + d], o);
+    out[d] = o * invL;
+  }
+  free(ms);
+}
+
 /* ------------------------------------------------------------------------- */
 /* model                                                                     */
 /* ------------------------------------------------------------------------- */
@@ -663,6 +834,7 @@ struct ho_model {
   float *hidden, *normed, *q, *k, *v, *attn_out, *gate, *up, *tmp, *scores, *logits_tmp, *big;
   uint8_t* q8;
   int n_threads, arm;
+  int order; /* 0 = reference association order, 1 = device order */
 };
 
 static tensor_t* add_tensor(ho_model* m, const char* name, int type, int64_t rows, int64_t cols,
@@ -869,6 +1041,18 @@ int ho_model_kv_prefill_synth(ho_model* m, uint64_t seed, int n_pos) {
   return 0;
 }
 
+void ho_model_set_order(ho_model* m, int order) { m->order = order; }
+
+/* full-width RMSNorm / per-head RMSNorm / attention in the model's order */
+static void norm_d(const ho_model* m, const float* x, const float* w, int64_t n, float* out) {
+  if (m->order) dev_rms_norm_block(x, w, m->cfg.eps, n, out);
+  else ho_rms_norm(x, w, m->cfg.eps, n, out);
+}
+static void norm_head(const ho_model* m, const float* x, const float* w, int n, float* out) {
+  if (m->order) dev_rms_norm_wave(x, w, m->cfg.eps, n, out);
+  else ho_rms_norm(x, w, m->cfg.eps, n, out);
+}
+
 void ho_model_set_threads(ho_model* m, int n_threads, int arm) {
   m->n_threads = n_threads < 1 ? 1 : n_threads;
   m->arm = arm;
@@ -883,7 +1067,7 @@ static void mm(ho_model* m, const tensor_t* w, const float* x, float* out) {
 }
 
 /* qwen35.rs:1809-1815 */
-static float softplus(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+static float softplus(float x) { return x > 20.0f ? x : ho_log(1.0f + ho_exp(x)); }
 
 /* mod.rs:451-860 (dense decode step) */
 static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
@@ -896,20 +1080,20 @@ static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
                 d, m->hidden);
   for (int li = 0; li < c->n_layers; li++) {
     layer_t* ly = &m->layers[li];
-    ho_rms_norm(m->hidden, (const float*)ly->attn_norm->data, c->eps, d, m->normed);
+    norm_d(m, m->hidden, (const float*)ly->attn_norm->data, d, m->normed);
     mm(m, ly->attn_q, m->normed, m->q);
     mm(m, ly->attn_k, m->normed, m->k);
     mm(m, ly->attn_v, m->normed, m->v);
     if (ly->attn_q_norm) {
       for (int h = 0; h < nh; h++) {
         memcpy(m->tmp, m->q + h * hd, sizeof(float) * hd);
-        ho_rms_norm(m->tmp, (const float*)ly->attn_q_norm->data, c->eps, hd, m->q + h * hd);
+        norm_head(m, m->tmp, (const float*)ly->attn_q_norm->data, hd, m->q + h * hd);
       }
     }
     if (ly->attn_k_norm) {
       for (int h = 0; h < nkvh; h++) {
         memcpy(m->tmp, m->k + h * hd, sizeof(float) * hd);
-        ho_rms_norm(m->tmp, (const float*)ly->attn_k_norm->data, c->eps, hd, m->k + h * hd);
+        norm_head(m, m->tmp, (const float*)ly->attn_k_norm->data, hd, m->k + h * hd);
       }
     }
     for (int h = 0; h < nh; h++) ho_rope_apply(m->rope, c->max_seq, m->rope_dim, m->q + h * hd, pos);
@@ -927,12 +1111,16 @@ static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
     int rep = nh / nkvh;
     for (int qh = 0; qh < nh; qh++) {
       int kvh = qh / rep;
-      ho_attention(m->q + qh * hd, kbase + kvh * head_stride, vbase + kvh * head_stride, seq_len, hd,
-                   m->attn_out + qh * hd, m->scores);
+      if (m->order)
+        dev_attention(m->q + qh * hd, kbase + kvh * head_stride, vbase + kvh * head_stride, seq_len, hd,
+                      m->attn_out + qh * hd);
+      else
+        ho_attention(m->q + qh * hd, kbase + kvh * head_stride, vbase + kvh * head_stride, seq_len, hd,
+                     m->attn_out + qh * hd, m->scores);
     }
     mm(m, ly->attn_output, m->attn_out, m->tmp);
     for (int i = 0; i < d; i++) m->hidden[i] += m->tmp[i];
-    ho_rms_norm(m->hidden, (const float*)ly->ffn_norm->data, c->eps, d, m->normed);
+    norm_d(m, m->hidden, (const float*)ly->ffn_norm->data, d, m->normed);
     mm(m, ly->ffn_gate, m->normed, m->gate);
     mm(m, ly->ffn_up, m->normed, m->up);
     ho_silu(m->gate, c->d_ffn);
@@ -940,7 +1128,7 @@ static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
     mm(m, ly->ffn_down, m->big, m->tmp);
     for (int i = 0; i < d; i++) m->hidden[i] += m->tmp[i];
   }
-  ho_rms_norm(m->hidden, (const float*)m->output_norm->data, c->eps, d, m->normed);
+  norm_d(m, m->hidden, (const float*)m->output_norm->data, d, m->normed);
   ho_quantize_q8_0(m->normed, d, m->q8);
   ho_gemv(m->output->type, m->output->data, m->output->rows, d, m->q8, logits, m->n_threads, m->arm);
   (void)nq;
@@ -964,6 +1152,18 @@ static void gdn_layer(ho_model* m, int li, layer_t* ly) {
   for (int r = 0; r < nv; r++) {
     const float* wa = (const float*)ly->ssm_alpha->data + (size_t)r * d;
     const float* wb = (const float*)ly->ssm_beta->data + (size_t)r * d;
+    if (m->order) {   /* lane-strided partial sums, butterfly */
+      float la[64], lb[64];
+      for (int l = 0; l < 64; l++) {
+        float a = 0.0f, b = 0.0f;
+        for (int j = l; j < d; j += 64) { a = a + wa[j] * m->normed[j]; b = b + wb[j] * m->normed[j]; }
+        la[l] = a;
+        lb[l] = b;
+      }
+      abuf[r] = bfly64(la);
+      bbuf[r] = bfly64(lb);
+      continue;
+    }
     float acc = 0.0f, accb = 0.0f;
     for (int j = 0; j < d; j++) { acc += wa[j] * m->normed[j]; accb += wb[j] * m->normed[j]; }
     abuf[r] = acc;
@@ -987,6 +1187,14 @@ static void gdn_layer(ho_model* m, int li, layer_t* ly) {
   memcpy(qn, conv_out, sizeof(float) * 2 * (size_t)kdim);
   for (int h = 0; h < 2 * nk; h++) {
     float ss = 0.0f;
+    if (m->order) {   /* two 64-lane butterflies, then their sum */
+      float la[64], lb[64];
+      for (int l = 0; l < 64; l++) {
+        la[l] = qn[h * hd + l] * qn[h * hd + l];
+        lb[l] = qn[h * hd + 64 + l] * qn[h * hd + 64 + l];
+      }
+      ss = bfly64(la) + bfly64(lb);
+    } else
     for (int j = 0; j < hd; j++) ss += qn[h * hd + j] * qn[h * hd + j];
     float inv = 1.0f / sqrtf(ss + c->eps);
     for (int j = 0; j < hd; j++) qn[h * hd + j] *= inv;
@@ -997,17 +1205,43 @@ static void gdn_layer(ho_model* m, int li, layer_t* ly) {
   const float* sa = (const float*)ly->ssm_a->data;
   for (int h = 0; h < nv; h++) {
     gdec[h] = softplus(abuf[h] + dtb[h]) * sa[h];
-    beta[h] = 1.0f / (1.0f + expf(-bbuf[h]));
+    beta[h] = 1.0f / (1.0f + ho_exp(-bbuf[h]));
   }
   float scale_q = 1.0f / sqrtf((float)hd);
   float* state = m->gdn_state + (size_t)li * nv * hd * hd;
   for (int h = 0; h < nv; h++) { /* :1371-1404 */
     int kg = h % nk;
-    float decay = expf(gdec[h]);
+    float decay = ho_exp(gdec[h]);
     float b = beta[h];
     float* S = state + (size_t)h * hd * hd;
     const float* kk = kn + kg * hd;
     const float* qq = qn + kg * hd;
+    if (m->order) {   /* 8 row-chunks of 16, each summed sequentially, chunks in order */
+      for (int j = 0; j < hd; j++) {
+        float dp[8], dot = 0.0f;
+        for (int c = 0; c < 8; c++) {
+          float a = 0.0f;
+          for (int r = 0; r < 16; r++) a = a + S[(size_t)(c * 16 + r) * hd + j] * kk[c * 16 + r];
+          dp[c] = a;
+        }
+        for (int c = 0; c < 8; c++) dot = dot + dp[c];
+        float bd = b * (vconv[h * hd + j] - dot);
+        float o = 0.0f, op[8];
+        for (int c = 0; c < 8; c++) {
+          float a = 0.0f;
+          for (int r = 0; r < 16; r++) {
+            size_t ix = (size_t)(c * 16 + r) * hd + j;
+            float sn = S[ix] * decay + kk[c * 16 + r] * bd;
+            S[ix] = sn;
+            a = a + sn * qq[c * 16 + r];
+          }
+          op[c] = a;
+        }
+        for (int c = 0; c < 8; c++) o = o + op[c];
+        m->attn_out[h * hd + j] = o * scale_q;
+      }
+      continue;
+    }
     for (int j = 0; j < hd; j++) {
       float dot = 0.0f;
       for (int i = 0; i < hd; i++) dot += S[(size_t)i * hd + j] * kk[i];
@@ -1022,7 +1256,7 @@ static void gdn_layer(ho_model* m, int li, layer_t* ly) {
   }
   /* gated RMSNorm (:1427-1439) */
   for (int h = 0; h < nv; h++)
-    ho_rms_norm(m->attn_out + h * hd, (const float*)ly->ssm_norm->data, c->eps, hd, oh + h * hd);
+    norm_head(m, m->attn_out + h * hd, (const float*)ly->ssm_norm->data, hd, oh + h * hd);
   ho_silu(z, vdim);
   for (int i = 0; i < vdim; i++) oh[i] *= z[i];
   mm(m, ly->ssm_out, oh, m->attn_out);
@@ -1042,11 +1276,11 @@ static void attn_layer_q35(ho_model* m, int pos, layer_t* ly) {
     memmove(m->q + h * hd, qg + (size_t)h * 2 * hd, sizeof(float) * hd);
   }
   for (int h = 0; h < nh; h++) {
-    ho_rms_norm(m->q + h * hd, (const float*)ly->attn_q_norm->data, c->eps, hd, m->tmp);
+    norm_head(m, m->q + h * hd, (const float*)ly->attn_q_norm->data, hd, m->tmp);
     memcpy(m->q + h * hd, m->tmp, sizeof(float) * hd);
   }
   for (int h = 0; h < nkvh; h++) {
-    ho_rms_norm(m->k + h * hd, (const float*)ly->attn_k_norm->data, c->eps, hd, m->tmp);
+    norm_head(m, m->k + h * hd, (const float*)ly->attn_k_norm->data, hd, m->tmp);
     memcpy(m->k + h * hd, m->tmp, sizeof(float) * hd);
   }
   for (int h = 0; h < nh; h++) ho_rope_apply(m->rope, c->max_seq, m->rope_dim, m->q + h * hd, pos);
@@ -1066,6 +1300,10 @@ static void attn_layer_q35(ho_model* m, int pos, layer_t* ly) {
   for (int qh = 0; qh < nh; qh++) { /* :1599-1624 scalar loops */
     int kvh = qh / rep;
     const float* qq = m->q + qh * hd;
+    if (m->order) {
+      dev_attention(qq, kb + kvh * hs, vb + kvh * hs, seq_len, hd, m->attn_out + qh * hd);
+      continue;
+    }
     for (int t = 0; t < seq_len; t++) {
       const float* kr = kb + kvh * hs + (size_t)t * hd;
       float acc = 0.0f;
@@ -1079,7 +1317,7 @@ static void attn_layer_q35(ho_model* m, int pos, layer_t* ly) {
       m->attn_out[qh * hd + i] = acc;
     }
   }
-  for (int i = 0; i < nq; i++) m->attn_out[i] /= 1.0f + expf(-gate[i]);
+  for (int i = 0; i < nq; i++) m->attn_out[i] /= 1.0f + ho_exp(-gate[i]);
   memcpy(m->up, m->attn_out, sizeof(float) * nq);
   mm(m, ly->attn_output, m->up, m->attn_out);
 }
@@ -1093,11 +1331,11 @@ static int forward_hybrid(ho_model* m, uint32_t token, int pos, float* logits) {
                 d, m->hidden);
   for (int li = 0; li < c->n_layers; li++) {
     layer_t* ly = &m->layers[li];
-    ho_rms_norm(m->hidden, (const float*)ly->attn_norm->data, c->eps, d, m->normed);
+    norm_d(m, m->hidden, (const float*)ly->attn_norm->data, d, m->normed);
     if (ly->is_gdn) gdn_layer(m, li, ly);
     else attn_layer_q35(m, pos, ly);
     for (int i = 0; i < d; i++) m->hidden[i] += m->attn_out[i];
-    ho_rms_norm(m->hidden, (const float*)ly->post_norm->data, c->eps, d, m->normed);
+    norm_d(m, m->hidden, (const float*)ly->post_norm->data, d, m->normed);
     mm(m, ly->ffn_gate, m->normed, m->gate);
     mm(m, ly->ffn_up, m->normed, m->up);
     ho_silu(m->gate, c->d_ffn);
@@ -1105,7 +1343,7 @@ static int forward_hybrid(ho_model* m, uint32_t token, int pos, float* logits) {
     mm(m, ly->ffn_down, m->gate, m->attn_out);
     for (int i = 0; i < d; i++) m->hidden[i] += m->attn_out[i];
   }
-  ho_rms_norm(m->hidden, (const float*)m->output_norm->data, c->eps, d, m->normed);
+  norm_d(m, m->hidden, (const float*)m->output_norm->data, d, m->normed);
   mm(m, m->output, m->normed, logits);
   return 0;
 }

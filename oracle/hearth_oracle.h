@@ -27,6 +27,10 @@ enum { HO_F32 = 0, HO_F16 = 1, HO_Q8_0 = 8, HO_Q1_0 = 41, HO_Q2_0 = 42, HO_Q1_0_
 uint16_t ho_f32_to_f16(float x);
 float ho_f16_to_f32(uint16_t h);
 
+/* exp / log shared with the device kernels (definition in hearth_oracle.c) */
+float ho_exp(float x);
+float ho_log(float x);
+
 /* ---- block formats ---- */
 size_t ho_row_bytes(int type, int64_t n_cols);
 void ho_quantize_q8_0(const float* x, int64_t n, uint8_t* out);          /* q8_0.rs:20-51 */
@@ -102,6 +106,10 @@ void ho_model_reset(ho_model* m);
 /* Write one position of the f32 KV cache for a layer (prefilled-cache configs). */
 int ho_model_kv_prefill_synth(ho_model* m, uint64_t seed, int n_pos);
 void ho_model_set_threads(ho_model* m, int n_threads, int arm);
+/* fp32 association order of the reductions: 0 = the reference's (ops.rs loops,
+ * default), 1 = the HIP kernels' (butterfly / split-sequence), for bit-level
+ * comparison with the device.  Same mathematics either way. */
+void ho_model_set_order(ho_model* m, int order);
 /* One decode step (mod.rs:451-860 dense / qwen35.rs:1028-1236 hybrid). */
 int ho_forward(ho_model* m, uint32_t token, int pos, float* logits);
 /* Token loop: prompt token-by-token, then n_gen greedy tokens. */

@@ -78,6 +78,9 @@ def load() -> C.CDLL:
         "ho_model_reset": (None, [C.c_void_p]),
         "ho_model_kv_prefill_synth": (C.c_int, [C.c_void_p, C.c_uint64, C.c_int]),
         "ho_model_set_threads": (None, [C.c_void_p, C.c_int, C.c_int]),
+        "ho_model_set_order": (None, [C.c_void_p, C.c_int]),
+        "ho_exp": (C.c_float, [C.c_float]),
+        "ho_log": (C.c_float, [C.c_float]),
         "ho_forward": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int, f32p]),
         "ho_generate": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int, C.c_int, C.c_float, u32p, f32p]),
         "ho_model_hidden": (C.c_void_p, [C.c_void_p]),
@@ -144,12 +147,15 @@ def synth_token(seed: int, i: int, vocab: int) -> int:
 
 
 class OracleModel:
-    def __init__(self, cfg, seed: Optional[int] = None, threads: int = 4, arm: int = 0):
+    REFERENCE, DEVICE = 0, 1
+
+    def __init__(self, cfg, seed: Optional[int] = None, threads: int = 4, arm: int = 0, order: int = 0):
         self.lib = load()
         self.cfg = cfg
         self._c = HoConfig(*[getattr(cfg, f[0]) for f in HoConfig._fields_])
         self.h = self.lib.ho_model_new(C.byref(self._c))
         self.lib.ho_model_set_threads(self.h, threads, arm)
+        self.lib.ho_model_set_order(self.h, order)
         if seed is not None:
             self.lib.ho_model_synth(self.h, seed, threads)
 
@@ -163,6 +169,9 @@ class OracleModel:
             self.close()
         except Exception:
             pass
+
+    def set_order(self, order: int) -> None:
+        self.lib.ho_model_set_order(self.h, order)
 
     def set_threads(self, threads: int, arm: int) -> None:
         self.lib.ho_model_set_threads(self.h, threads, arm)

@@ -1,7 +1,15 @@
 """GPU parity of whole decode steps and the token loop against the CPU oracle.
 
 Bars (north star): synthesized weight bytes bit-exact; logits within 1e-3
-relative (max |diff| / max |ref|); greedy tokens identical for the first 32."""
+relative (max |diff| / max |ref|); greedy tokens identical for the first 32.
+
+The oracle runs in its device association order (the HIP kernels' reduction
+grouping, same mathematics): GEMVs, quantization, norms, attention and the GDN
+step then agree bit for bit, so the logits are compared for equality as well as
+against the 1e-3 bar.  The reference-order oracle is compared at a looser bar
+in test_reference_order_spread: there every reduction regroups, which moves
+logits by Q8_0 rounding flips, as the reference's own scalar and AVX2 GEMV arms
+do to each other."""
 import numpy as np
 import pytest
 
@@ -22,11 +30,11 @@ def rel(a, b):
     return float(np.abs(a.astype(np.float64) - b).max() / np.abs(b).max())
 
 
-def make(ctx, oracle, cfg, seed, threads=16):
+def make(ctx, oracle, cfg, seed, threads=16, order=1):
     from hearth_amd import Model
     m = Model(ctx, cfg)
     m.synthesize(seed)
-    o = oracle.OracleModel(cfg, seed=seed, threads=threads)
+    o = oracle.OracleModel(cfg, seed=seed, threads=threads, order=order)
     return m, o
 
 
@@ -52,6 +60,7 @@ def test_forward_logits_parity(ctx, oracle, cfg):
         lg, am = m.forward(tok, pos)
         lw = o.forward(tok, pos)
         assert rel(lg, lw) < 1e-3, pos
+        assert np.array_equal(lg, lw), (pos, rel(lg, lw))
         assert np.isfinite(lg).all()
 
 
@@ -64,6 +73,7 @@ def test_generate_tokens_parity(ctx, oracle, cfg, pen):
     tw, lw = o.generate(prompt, 32, repeat_pen=pen, want_logits=True)
     assert list(toks) == list(tw)
     assert rel(lg, lw) < 1e-3
+    assert np.array_equal(lg, lw)
 
 
 def test_8b_shaped_prefilled_kv(ctx, oracle):
@@ -75,10 +85,23 @@ def test_8b_shaped_prefilled_kv(ctx, oracle):
     m.prefill_kv_synthetic(99, 2048)
     o.prefill_kv_synthetic(99, 2048)
     tok0 = oracle.synth_token(3, 0, cfg.vocab)
-    toks, lg = m.generate([tok0], 8, start_pos=2048, repeat_pen=1.1, want_logits=True)
-    tw, lw = o.generate([tok0], 8, start_pos=2048, repeat_pen=1.1, want_logits=True)
+    toks, lg = m.generate([tok0], 32, start_pos=2048, repeat_pen=1.1, want_logits=True)
+    tw, lw = o.generate([tok0], 32, start_pos=2048, repeat_pen=1.1, want_logits=True)
     assert list(toks) == list(tw)
     assert rel(lg, lw) < 1e-3
+    assert np.array_equal(lg, lw)
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY_HYB], ids=["dense", "hybrid"])
+def test_reference_order_spread(ctx, oracle, cfg):
+    """Against the reference-order oracle: first-step logits within 5e-2.  The
+    reference's own scalar vs AVX2 GEMV arms differ by up to 1.3e-2 on these
+    models (measured with the oracle's two arms); regrouping every reduction
+    (norms, attention, GDN) as well gives up to 2.5e-2 on the hybrid."""
+    m, o = make(ctx, oracle, cfg, seed=9, order=0)
+    lg, _ = m.forward(123, 0)
+    lw = o.forward(123, 0)
+    assert rel(lg, lw) < 5e-2
 
 
 def test_model_errors(ctx):

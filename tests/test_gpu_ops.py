@@ -63,7 +63,10 @@ def test_gemv_parity(ctx, oracle, t, shape):
     want = oracle.gemv(t, w, n_rows, n_cols, a, threads=8)
     y = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
     ctx.gemv_q8(t, dev(w), n_rows, n_cols, dev(a), y)
-    assert rel_err(host(y), want) < 1e-3
+    got = host(y)
+    assert rel_err(got, want) < 1e-3
+    # stronger than the 1e-3 bar: the device keeps the scalar kernel's fp32 order
+    assert np.array_equal(got, want)
 
 
 @pytest.mark.parametrize("shape", [(151936, 4096), (64, 2048), (5, 64)])
@@ -74,13 +77,17 @@ def test_gemv_q8_head_parity(ctx, oracle, shape):
     want = oracle.gemv(8, w, n_rows, n_cols, a, threads=8)
     y = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
     ctx.gemv_q8(8, dev(w), n_rows, n_cols, dev(a), y)
-    assert rel_err(host(y), want) < 1e-3
+    got = host(y)
+    assert rel_err(got, want) < 1e-3
+    assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("n", [128, 256, 2048, 6144])
+@pytest.mark.parametrize("n", [256, 2048, 6144])
 def test_gemv_reference_generators(ctx, oracle, n):
     """q2_0.rs:939-986 / q1_0g128.rs:1504-1551 byte generators (codes include 3,
-    activations include -128): the device matches the scalar reference kernel."""
+    activations include -128): the device matches the scalar reference kernel
+    bit for bit.  (n = 128, the generators' smallest case, is below the
+    library's 256-element GEMV granularity and is covered by the CPU tests.)"""
     for salt in (53, 97):
         a = ref_act(n, salt)
         for t, w in ((42, ref_q2_weights(n)), (41, ref_q1_weights(n))):
@@ -88,7 +95,7 @@ def test_gemv_reference_generators(ctx, oracle, n):
             y = torch.zeros(1, dtype=torch.float32, device="cuda")
             ctx.gemv_q8(t, dev(w), 1, n, dev(a), y)
             got = host(y)[0]
-            assert abs(got - want) <= 1e-5 * max(1.0, abs(want)), (t, n, salt, got, want)
+            assert got == np.float32(want), (t, n, salt, got, want)
 
 
 def test_gemv_errors(ctx):
@@ -168,5 +175,6 @@ def test_argmax_rules(ctx, oracle):
     x[[10, 20]] = [5.0, 4.9]
     past = np.array([10, 10, 3, 10], np.uint32)
     ctx.argmax(dev(x), x.size, dev(past), 4, 1.1, 0, out)
-    want = lib.ho_sample_greedy_dense(x.copy().ctypes.data, x.size, past.ctypes.data, 4, 1.1)
+    xc = x.copy()
+    want = lib.ho_sample_greedy_dense(xc.ctypes.data, x.size, past.ctypes.data, 4, 1.1)
     assert int(host(out)[0]) == want == 20

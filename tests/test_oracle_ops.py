@@ -117,3 +117,54 @@ def test_synth_generator_properties(oracle):
     k2 = lib.ho_name_key(1, b"e")
     f = np.array([lib.ho_synth_int(k2, i) for i in range(128)], np.float32) * np.float32(c)
     assert np.array_equal(q8, oracle.quantize_q8_0(f))
+
+
+def test_shared_exp_log_accuracy(oracle):
+    """ho_exp / ho_log (the one exp/log both implementations use) against
+    float64 numpy: exp within 2 ulp, log within 3 ulp of the correctly rounded value over the ranges
+    the path feeds them (softmax and silu arguments, softplus of 1+e^x)."""
+    lib = oracle.load()
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([rng.uniform(-87.0, 88.0, 20000), rng.uniform(-20, 20, 20000),
+                         np.array([0.0, -0.0, 1.0, -1.0, 1e-8, -1e-8, 88.7, -87.3])]).astype(np.float32)
+    got = np.array([lib.ho_exp(float(x)) for x in xs], np.float32)
+    want = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - want) / ulp).max() <= 2.0
+    assert lib.ho_exp(-100.0) == 0.0 and np.isinf(lib.ho_exp(100.0))
+    ys = np.concatenate([rng.uniform(1.0, 4.9e8, 20000), rng.uniform(1e-30, 10, 20000),
+                         np.array([1.0, 2.0, 0.5, 1e-40, 3.4e38])]).astype(np.float32)
+    got = np.array([lib.ho_log(float(y)) for y in ys], np.float32)
+    want = np.log(ys.astype(np.float64))
+    err = np.abs(got - want) / np.maximum(np.spacing(np.abs(want).astype(np.float32)), 1e-45)
+    assert err.max() <= 3.0
+    assert lib.ho_log(1.0) == 0.0
+
+
+def test_device_order_matches_reference_order(oracle):
+    """The device-order model (butterfly / split-sequence reductions) computes the
+    same function as the reference-order model: identical greedy tokens on a tiny
+    model and first-step logits within 1e-3; over longer runs the two diverge by
+    Q8_0 rounding flips, the same effect as the reference's own scalar vs AVX2
+    GEMV arms."""
+    from hearth_amd.lib import ModelConfig, GGML_Q2_0
+    cfg = ModelConfig(d_model=1024, n_layers=2, n_heads=8, n_kv_heads=4, head_dim=128, d_ffn=1024,
+                      vocab=4096, max_seq=64, wtype=GGML_Q2_0)
+    a = oracle.OracleModel(cfg, seed=3, threads=2, order=0)
+    b = oracle.OracleModel(cfg, seed=3, threads=2, order=1)
+    la, lb = a.forward(9, 0), b.forward(9, 0)
+    assert np.abs(la - lb).max() / np.abs(la).max() < 1e-3
+    # long attention: split-sequence vs single softmax on random data
+    lib = oracle.load()
+    rng = np.random.default_rng(4)
+    hd, seq = 128, 2049
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal((seq, hd)).astype(np.float32)
+    v = rng.standard_normal((seq, hd)).astype(np.float32)
+    s = k.astype(np.float64) @ q / np.sqrt(hd)
+    p = np.exp(s - s.max())
+    ref = (p / p.sum()) @ v
+    out = np.zeros(hd, np.float32)
+    scr = np.zeros(seq, np.float32)
+    lib.ho_attention(q.ctypes.data, k.ctypes.data, v.ctypes.data, seq, hd, out.ctypes.data, scr.ctypes.data)
+    assert np.allclose(out, ref, rtol=1e-4, atol=1e-5)
