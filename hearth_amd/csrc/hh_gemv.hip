@@ -141,20 +141,22 @@ HH_DEV void unit_q8(const uint32_t (&w)[17], const int8_t* aq, const float* ad, 
   }
 }
 
+// Plain loads: on gfx950 the non-temporal variant of this stream measured
+// ~4.0 TB/s against ~6.2 TB/s for ordinary loads of the same 68-byte units.
 template <int FMT> HH_DEV void load_unit(uint32_t (&w)[UnitT<FMT>::DW], const uint8_t* p) {
   const u32x4_a4* v = (const u32x4_a4*)p;
   if constexpr (FMT == FMT_Q1) {
-    u32x4_a4 a = __builtin_nontemporal_load(v), b = __builtin_nontemporal_load(v + 1);
+    u32x4_a4 a = v[0], b = v[1];
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-    w[8] = __builtin_nontemporal_load((const uint32_t*)(p + 32));
+    w[8] = *(const uint32_t*)(p + 32);
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      u32x4_a4 a = __builtin_nontemporal_load(v + i);
+      u32x4_a4 a = v[i];
       w[4 * i] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
     }
-    w[16] = __builtin_nontemporal_load((const uint32_t*)(p + 64));
+    w[16] = *(const uint32_t*)(p + 64);
   }
 }
 
@@ -165,26 +167,56 @@ template <int FMT> HH_DEV void unit_dot(const uint32_t (&w)[UnitT<FMT>::DW], con
   else unit_q8(w, aq, ad, as, pr);
 }
 
-// Packed activation into LDS from a dense f32 vector x (optionally RMS-normed).
-// 8 lanes per 32-element block, 4 consecutive elements per lane.
-template <int FMT>
-HH_DEV void prologue_quant(const float* __restrict__ x, const float* __restrict__ nw, float eps, int K,
-                           bool rmsnorm, int8_t* aq, float* ad, int* as, float* red) {
+// ---------------------------------------------------------------------------
+// Activation staging.  Each prologue has an issue half (global loads into
+// registers) and a store half (registers -> LDS).  The issue half runs before
+// any weight load: vector loads retire in order, so an activation load issued
+// after the weight loads would wait for them.
+//
+// LDS layout: aq = int8 activations, unit t at t*qstride; ds = per unit
+// [d_0 .. d_{SUBS-1}, s_0 .. s_{SUBS-1}] padded to DSS words (conflict-free
+// 128-bit reads by consecutive units); part = block products transposed.
+// ---------------------------------------------------------------------------
+template <int FMT> HH_DEV constexpr int dss() { return FMT == FMT_Q8 ? 8 : 20; }
+
+template <int FMT> HH_DEV void put_ds(float* ds, int blk32, float d, int s) {
+  constexpr int SUBS = UnitT<FMT>::SUBS;
+  int t = blk32 / SUBS, sub = blk32 - t * SUBS;
+  ds[t * dss<FMT>() + sub] = d;
+  ((int*)ds)[t * dss<FMT>() + SUBS + sub] = s;
+}
+
+// PRO_RMSNORM: rms_norm(x, w) then Q8_0; NCH = K / 1024 float4 per lane.
+template <int NCH> struct NormRegs { float4 x[NCH], w[NCH]; };
+
+template <int NCH> HH_DEV void norm_issue(const GemvArgs& p, NormRegs<NCH>& r) {
   const int tid = threadIdx.x;
-  float inv = 1.0f;
-  if (rmsnorm) {
-    float tot = block_sumsq_f4(x, K, red);
-    inv = 1.0f / sqrtf(tot / (float)K + eps);   // ops.rs:22-23
-  }
-  for (int e = tid * 4; e < K; e += 1024) {
-    float4 v = *(const float4*)(x + e);
-    float vv[4] = {v.x, v.y, v.z, v.w};
-    if (rmsnorm) {
-      float4 w4 = *(const float4*)(nw + e);
-      float ww[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vv[i] = vv[i] * inv * ww[i];   // ops.rs:29 (x * inv) * w
-    }
+  for (int c = 0; c < NCH; ++c) {
+    r.x[c] = *(const float4*)(p.x + tid * 4 + c * 1024);
+    r.w[c] = *(const float4*)(p.norm_w + tid * 4 + c * 1024);
+  }
+}
+
+template <int FMT, int NCH>
+HH_DEV void norm_store(const GemvArgs& p, const NormRegs<NCH>& r, int8_t* aq, float* ds, float* red) {
+  const int tid = threadIdx.x;
+  const int K = NCH * 1024;
+  // block_sumsq_f4's order: ss + (((x0^2 + x1^2) + x2^2) + x3^2) per float4
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    ss += r.x[c].x * r.x[c].x + r.x[c].y * r.x[c].y + r.x[c].z * r.x[c].z + r.x[c].w * r.x[c].w;
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  float inv = 1.0f / sqrtf(tot / (float)K + p.eps);   // ops.rs:22-23
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e = tid * 4 + c * 1024;
+    float vv[4] = {r.x[c].x * inv * r.w[c].x, r.x[c].y * inv * r.w[c].y,   // ops.rs:29 (x * inv) * w
+                   r.x[c].z * inv * r.w[c].z, r.x[c].w * inv * r.w[c].w};
     float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
     am = group_max<8>(am);
     float sc = q8_scale(am);
@@ -196,58 +228,108 @@ HH_DEV void prologue_quant(const float* __restrict__ x, const float* __restrict_
       aq[lds_qpos(FMT, e + i)] = (int8_t)q;
     }
     qs = group_sum_i<8>(qs);
-    if ((tid & 7) == 0) {
-      ad[e >> 5] = h2f(f2h(sc));
-      as[e >> 5] = qs;
-    }
+    if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
   }
 }
 
-// Standard Q8_0 blocks -> LDS packed layout.
-template <int FMT>
-HH_DEV void prologue_stdq8(const uint8_t* __restrict__ xq, int K, int8_t* aq, float* ad, int* as) {
-  const int tid = threadIdx.x;
-  for (int e = tid * 4; e < K; e += 1024) {
-    const uint8_t* blk = xq + (size_t)(e >> 5) * 34;
-    int off = e & 31;
-    int qs = 0;
+// PRO_PACKED: packed activation [q K][d K/32][s K/32] from a producer kernel.
+constexpr int PK_Q = 5;   // 16-byte chunks per lane: K <= 20480
+constexpr int PK_D = 3;   // blocks per lane: K/32 <= 768
+struct PackedRegs { i32x4 q[PK_Q]; float d[PK_D]; int s[PK_D]; };
+
+HH_DEV void packed_issue(const GemvArgs& p, PackedRegs& r) {
+  const int tid = threadIdx.x, K = p.K;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int q = (int8_t)blk[2 + off + i];
-      qs += q;
-      aq[lds_qpos(FMT, e + i)] = (int8_t)q;
-    }
-    qs = group_sum_i<8>(qs);
-    if ((tid & 7) == 0) {
-      ad[e >> 5] = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-      as[e >> 5] = qs;
-    }
+  for (int i = 0; i < PK_Q; ++i) {
+    int c = tid + 256 * i;
+    if (c < K / 16) r.q[i] = *(const i32x4*)(p.act + c * 16);
+  }
+  const float* gd = (const float*)(p.act + K);
+  const int* gs = (const int*)(p.act + K + (K / 32) * 4);
+#pragma unroll
+  for (int i = 0; i < PK_D; ++i) {
+    int b = tid + 256 * i;
+    if (b < K / 32) { r.d[i] = gd[b]; r.s[i] = gs[b]; }
   }
 }
 
-// Packed activation in global memory -> LDS (adds the per-unit padding).
-template <int FMT>
-HH_DEV void prologue_packed(const uint8_t* __restrict__ act, int K, int8_t* aq, float* ad, int* as) {
-  const int tid = threadIdx.x;
+template <int FMT> HH_DEV void packed_store(const GemvArgs& p, const PackedRegs& r, int8_t* aq, float* ds) {
+  const int tid = threadIdx.x, K = p.K;
   constexpr int EL = UnitT<FMT>::EL;
-  for (int c = tid; c < K / 16; c += 256) {
-    int e = c * 16;
-    i32x4 v = *(const i32x4*)(act + e);
-    *(i32x4*)(aq + (e / EL) * qstride<FMT>() + (e % EL)) = v;
+#pragma unroll
+  for (int i = 0; i < PK_Q; ++i) {
+    int c = tid + 256 * i;
+    if (c < K / 16) {
+      int e = c * 16;
+      *(i32x4*)(aq + (e / EL) * qstride<FMT>() + (e % EL)) = r.q[i];
+    }
   }
-  const float* gd = (const float*)(act + K);
-  const int* gs = (const int*)(act + K + (K / 32) * 4);
-  for (int b = tid; b < K / 32; b += 256) {
-    ad[b] = gd[b];
-    as[b] = gs[b];
+#pragma unroll
+  for (int i = 0; i < PK_D; ++i) {
+    int b = tid + 256 * i;
+    if (b < K / 32) put_ds<FMT>(ds, b, r.d[i], r.s[i]);
   }
 }
 
-template <int FMT, int PRO, int EPI>
+// PRO_STDQ8: standard Q8_0 blocks (DotFn activation format), K <= 20480.
+constexpr int SQ_C = 20;
+struct StdRegs { uint32_t q[SQ_C]; uint32_t d[SQ_C]; };
+
+HH_DEV void std_issue(const GemvArgs& p, StdRegs& r) {
+  const int tid = threadIdx.x, K = p.K;
+#pragma unroll
+  for (int c = 0; c < SQ_C; ++c) {
+    int e = tid * 4 + c * 1024;
+    if (e < K) {
+      const uint8_t* blk = p.act + (size_t)(e >> 5) * 34;
+      const uint16_t* q16 = (const uint16_t*)(blk + 2 + (e & 31));
+      r.q[c] = (uint32_t)q16[0] | ((uint32_t)q16[1] << 16);
+      r.d[c] = *(const uint16_t*)blk;
+    }
+  }
+}
+
+template <int FMT> HH_DEV void std_store(const GemvArgs& p, const StdRegs& r, int8_t* aq, float* ds) {
+  const int tid = threadIdx.x, K = p.K;
+#pragma unroll
+  for (int c = 0; c < SQ_C; ++c) {
+    int e = tid * 4 + c * 1024;
+    if (e < K) {
+      int qs = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int q = (int8_t)((r.q[c] >> (8 * i)) & 0xffu);
+        qs += q;
+        aq[lds_qpos(FMT, e + i)] = (int8_t)q;
+      }
+      qs = group_sum_i<8>(qs);
+      if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(r.d[c]), qs);
+    }
+  }
+}
+
+template <int FMT, int PRO, int NCH> struct ActStage;
+template <int FMT, int NCH> struct ActStage<FMT, PRO_RMSNORM, NCH> {
+  NormRegs<NCH> r;
+  HH_DEV void issue(const GemvArgs& p) { norm_issue<NCH>(p, r); }
+  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT, NCH>(p, r, aq, ds, red); }
+};
+template <int FMT, int NCH> struct ActStage<FMT, PRO_PACKED, NCH> {
+  PackedRegs r;
+  HH_DEV void issue(const GemvArgs& p) { packed_issue(p, r); }
+  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float*) { packed_store<FMT>(p, r, aq, ds); }
+};
+template <int FMT, int NCH> struct ActStage<FMT, PRO_STDQ8, NCH> {
+  StdRegs r;
+  HH_DEV void issue(const GemvArgs& p) { std_issue(p, r); }
+  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float*) { std_store<FMT>(p, r, aq, ds); }
+};
+
+template <int FMT, int PRO, int EPI, int NCH>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
   constexpr int DW = UnitT<FMT>::DW;
   constexpr int UB = UnitT<FMT>::BYTES;
-  constexpr int SUBS = UnitT<FMT>::SUBS;
+  // units per lane per batch; two batches are in flight
   constexpr int DEPTH = (FMT == FMT_Q1) ? 4 : 2;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
@@ -293,10 +375,12 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
   // LDS carve-up
   const int nunits_act = K / UnitT<FMT>::EL;
   int8_t* aq = (int8_t*)smem;
-  float* ad = (float*)(smem + nunits_act * qstride<FMT>());
-  int* as = (int*)(ad + K / 32);
-  float* part = (float*)(as + K / 32);
-  float* red = part + 2 * U;
+  float* ds = (float*)(smem + nunits_act * qstride<FMT>());
+  // block products, transposed: part[j * RS + row] for product j = 2*unit + blk,
+  // RS = rows + 1, so the row-sum pass (one lane per row) reads consecutive words
+  float* part = ds + nunits_act * dss<FMT>();
+  const int RS = rows_total + 1;
+  float* red = part + 2 * P * RS;
   float* rowsum = red + 8;
 
   auto unit_addr = [&](int lu) -> const uint8_t* {
@@ -323,34 +407,35 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
     for (int d = 0; d < DEPTH; ++d) {
       int lu = (b * DEPTH + d) * 256 + tid;
       if (lu < U) {
-        int t = lu % P;
+        int rl = lu / P, t = lu - rl * P;
         float pr[2];
-        unit_dot<FMT>(wr[d], aq + t * qstride<FMT>(), ad + t * SUBS, as + t * SUBS, pr);
-        *(float2*)(part + 2 * lu) = make_float2(pr[0], pr[1]);
+        const float* ud = ds + t * dss<FMT>();
+        unit_dot<FMT>(wr[d], aq + t * qstride<FMT>(), ud, (const int*)(ud + UnitT<FMT>::SUBS), pr);
+        part[(2 * t) * RS + rl] = pr[0];
+        part[(2 * t + 1) * RS + rl] = pr[1];
       }
     }
   };
 
-  if (NB > 0) load_batch(wa, 0);
-
-  if constexpr (PRO == PRO_PACKED) prologue_packed<FMT>(p.act, K, aq, ad, as);
-  else if constexpr (PRO == PRO_RMSNORM) prologue_quant<FMT>(p.x, p.norm_w, p.eps, K, true, aq, ad, as, red);
-  else prologue_stdq8<FMT>(p.act, K, aq, ad, as);
+  ActStage<FMT, PRO, NCH> act;
+  act.issue(p);                      // activation first (in-order retirement)
+  if (NB > 0) load_batch(wa, 0);     // then the first weight batch
+  if (NB > 1) load_batch(wb, 1);     // and the second
+  act.store(p, aq, ds, red);
   __syncthreads();
 
   for (int b = 0; b < NB; b += 2) {
-    if (b + 1 < NB) load_batch(wb, b + 1);
     comp_batch(wa, b);
     if (b + 2 < NB) load_batch(wa, b + 2);
     if (b + 1 < NB) comp_batch(wb, b + 1);
+    if (b + 3 < NB) load_batch(wb, b + 3);
   }
   __syncthreads();
 
   // per-row sums over the block products in block order (the scalar loop)
   for (int r = tid; r < rows_total; r += 256) {
-    const float* pr = part + 2 * r * P;
     float s = 0.0f;
-    for (int t = 0; t < 2 * P; ++t) s += pr[t];
+    for (int j = 0; j < 2 * P; ++j) s += part[j * RS + r];
     rowsum[r] = s;
   }
   __syncthreads();
@@ -474,19 +559,19 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
   }
 }
 
-template <int FMT, int PRO, int EPI>
+template <int FMT, int PRO, int EPI, int NCH>
 int launch_t(const GemvArgs& a, int n_wg, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((k_gemv<FMT, PRO, EPI>), dim3(n_wg), dim3(256), lds, s, a);
+  hipLaunchKernelGGL((k_gemv<FMT, PRO, EPI, NCH>), dim3(n_wg), dim3(256), lds, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
-template <int FMT, int PRO>
+template <int FMT, int PRO, int NCH>
 int launch_e(const GemvArgs& a, int epi, int n_wg, size_t lds, hipStream_t s) {
   switch (epi) {
-    case EPI_STORE: return launch_t<FMT, PRO, EPI_STORE>(a, n_wg, lds, s);
-    case EPI_ADD: return launch_t<FMT, PRO, EPI_ADD>(a, n_wg, lds, s);
-    case EPI_SILU: return launch_t<FMT, PRO, EPI_SILU>(a, n_wg, lds, s);
-    case EPI_LOGITS: return launch_t<FMT, PRO, EPI_LOGITS>(a, n_wg, lds, s);
+    case EPI_STORE: return launch_t<FMT, PRO, EPI_STORE, NCH>(a, n_wg, lds, s);
+    case EPI_ADD: return launch_t<FMT, PRO, EPI_ADD, NCH>(a, n_wg, lds, s);
+    case EPI_SILU: return launch_t<FMT, PRO, EPI_SILU, NCH>(a, n_wg, lds, s);
+    case EPI_LOGITS: return launch_t<FMT, PRO, EPI_LOGITS, NCH>(a, n_wg, lds, s);
   }
   return 1;
 }
@@ -494,9 +579,20 @@ int launch_e(const GemvArgs& a, int epi, int n_wg, size_t lds, hipStream_t s) {
 template <int FMT>
 int launch_p(const GemvArgs& a, int pro, int epi, int n_wg, size_t lds, hipStream_t s) {
   switch (pro) {
-    case PRO_PACKED: return launch_e<FMT, PRO_PACKED>(a, epi, n_wg, lds, s);
-    case PRO_RMSNORM: return launch_e<FMT, PRO_RMSNORM>(a, epi, n_wg, lds, s);
-    case PRO_STDQ8: return launch_e<FMT, PRO_STDQ8>(a, epi, n_wg, lds, s);
+    case PRO_PACKED:
+      if (a.K > PK_Q * 4096 || a.K / 32 > PK_D * 256) return 1;
+      return launch_e<FMT, PRO_PACKED, 0>(a, epi, n_wg, lds, s);
+    case PRO_STDQ8:
+      if (a.K > SQ_C * 1024) return 1;
+      return launch_e<FMT, PRO_STDQ8, 0>(a, epi, n_wg, lds, s);
+    case PRO_RMSNORM:
+      switch (a.K) {   // NCH = K / 1024 float4 per lane
+        case 1024: return launch_e<FMT, PRO_RMSNORM, 1>(a, epi, n_wg, lds, s);
+        case 2048: return launch_e<FMT, PRO_RMSNORM, 2>(a, epi, n_wg, lds, s);
+        case 4096: return launch_e<FMT, PRO_RMSNORM, 4>(a, epi, n_wg, lds, s);
+        case 5120: return launch_e<FMT, PRO_RMSNORM, 5>(a, epi, n_wg, lds, s);
+      }
+      return 1;
   }
   return 1;
 }
@@ -519,7 +615,8 @@ size_t hh_gemv_lds(int fmt, int K, int rows_total_per_wg) {
   int el = hh_unit_el(fmt);
   int P = K / el;
   size_t qb = (size_t)(K / el) * (el + 16);
-  size_t b = qb + (size_t)(K / 32) * 8 + (size_t)rows_total_per_wg * P * 8 + 8 * 4 + (size_t)rows_total_per_wg * 4;
+  size_t dsb = (size_t)(K / el) * (fmt == FMT_Q8 ? 8 : 20) * 4;
+  size_t b = qb + dsb + (size_t)(rows_total_per_wg + 1) * P * 8 + 8 * 4 + (size_t)rows_total_per_wg * 4;
   return (b + 15) & ~(size_t)15;
 }
 

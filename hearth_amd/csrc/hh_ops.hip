@@ -116,8 +116,8 @@ __global__ __launch_bounds__(256) void k_embed(int type, const uint8_t* __restri
 // GQA decode attention (ops.rs:353-406 per q-head, mod.rs:687-704 head map
 // kvh = qh / (n_heads/n_kv); qwen35.rs:1495-1640 with the q|gate split and
 // sigmoid gate).  Split over the sequence: workgroup (s, kvh) owns positions
-// [s*C, s*C+C) for the G query heads of kv head kvh, with C*hd = 4096 so a
-// chunk of K and of V is 16 KB each, staged through LDS.  Prep (per-head
+// [s*C, s*C+C) for the G query heads of kv head kvh, with C*hd = 8192 so a
+// chunk of K and of V is 32 KB each, staged through LDS.  Prep (per-head
 // RMSNorm mod.rs:551-578, RoPE :582-593, KV write :596-605) is fused: every
 // workgroup normalises its q heads; the one holding `pos` also writes K/V.
 // The last workgroup of a kv head (device counter) merges the splits
@@ -183,10 +183,10 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   const float* kg = a.k_cache + (size_t)kvh * hstride;
   const float* vg = a.v_cache + (size_t)kvh * hstride;
 
-  // 1. issue this chunk's K/V loads (C*hd == 4096 floats each: 4 float4 per lane)
-  float4 kr[4], vr[4];
+  // 1. issue this chunk's K/V loads (C*hd == 8192 floats each: 8 float4 per lane)
+  float4 kr[8], vr[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
     int f = (i * 256 + tid) * 4;
     int row = f / hd, col = f % hd;
     if (row < np && p0 + row != pos) {
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   }
   // 3. chunk into LDS
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
     int f = (i * 256 + tid) * 4;
     int row = f / hd, col = f % hd;
     if (row < np) {
@@ -302,10 +302,21 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     L = wave_sum(L);
     float invL = 1.0f / L;
     int qh = kvh * G + h;
+    // o[d] = sum_t w_t o_t[d] in split order; the partials of 16 splits are
+    // fetched together so the loop waits on one round trip per batch
+    const size_t tstride = (size_t)G * hd;
     for (int d0 = 0; d0 < hd; d0 += 64) {
       int d = d0 + lane;
       float o = 0.0f;
-      for (int t = 0; t < n_active; ++t) o = fmaf(wts[h * a.max_splits + t], a.part_o[(hb + (size_t)t * G) * hd + d], o);
+      const float* pb = a.part_o + hb * hd + d;
+      for (int t0 = 0; t0 < n_active; t0 += 16) {
+        float pv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) pv[i] = (t0 + i < n_active) ? pb[(size_t)(t0 + i) * tstride] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (t0 + i < n_active) o = fmaf(wts[h * a.max_splits + t0 + i], pv[i], o);
+      }
       o = o * invL;
       if (a.gated) {   // qwen35.rs:1627-1629 attn_out /= 1 + exp(-gate)
         float g = a.qkv[(size_t)qh * 2 * hd + hd + d];
@@ -525,6 +536,7 @@ int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
   int G = a.n_heads / a.n_kv;
   size_t floats = (size_t)G * a.hd + (size_t)a.chunk * (a.hd + 4) + (size_t)a.chunk * a.hd + (size_t)G * a.chunk +
                   2 * (size_t)a.hd + 2 * G + 8 + (size_t)G * a.max_splits;
+  if (a.hd != 128 && a.hd != 256) return 1;
   hipLaunchKernelGGL(k_attn, dim3(a.max_splits, a.n_kv), dim3(256), floats * 4, s, a);
   return ok();
 }

@@ -86,6 +86,9 @@ struct hh_ctx {
   int* counter = nullptr;
   int* counts = nullptr;
   int64_t counts_n = 0;
+  hipEvent_t ev[8] = {};
+  void* attn_scratch = nullptr;     // standalone attention partials + counters
+  size_t attn_scratch_bytes = 0;
 };
 
 namespace {
@@ -221,6 +224,15 @@ void declare(hh_model* m) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Rows per GEMV workgroup: about 512 units (1-2 per lane) per workgroup, halved
+// until the launch has at least 512 workgroups (2 per CU) or one row each.
+int gemv_rows_for(int n_rows, int P) {
+  int rows = 1;
+  while (rows * 2 * P <= 512 && rows < 64) rows *= 2;
+  while (rows > 1 && (n_rows + rows - 1) / rows < 512) rows /= 2;
+  return rows;
+}
 
 int enqueue_step(hh_model* m, hipStream_t s, int only_layer = -1, unsigned stages = ~0u);
 
@@ -398,6 +410,9 @@ int hh_ctx_destroy(hh_ctx* c) {
   hipFree(c->part_idx);
   hipFree(c->counter);
   if (c->counts) hipFree(c->counts);
+  if (c->attn_scratch) hipFree(c->attn_scratch);
+  for (hipEvent_t e : c->ev)
+    if (e) hipEventDestroy(e);
   hipStreamDestroy(c->stream);
   delete c;
   return HH_OK;
@@ -406,6 +421,21 @@ int hh_ctx_destroy(hh_ctx* c) {
 int hh_ctx_synchronize(hh_ctx* c) {
   if (!c) return fail(HH_ERR_INVALID, "ctx is null");
   HIP_TRY(hipStreamSynchronize(c->stream));
+  return HH_OK;
+}
+
+int hh_ctx_event_record(hh_ctx* c, int slot) {
+  if (!c || slot < 0 || slot >= 8) return fail(HH_ERR_INVALID, "bad event slot");
+  if (!c->ev[slot]) HIP_TRY(hipEventCreate(&c->ev[slot]));
+  HIP_TRY(hipEventRecord(c->ev[slot], c->stream));
+  return HH_OK;
+}
+
+int hh_ctx_event_elapsed(hh_ctx* c, int a, int b, float* ms) {
+  if (!c || !ms || a < 0 || b < 0 || a >= 8 || b >= 8 || !c->ev[a] || !c->ev[b])
+    return fail(HH_ERR_INVALID, "bad event slot");
+  HIP_TRY(hipEventSynchronize(c->ev[b]));
+  HIP_TRY(hipEventElapsedTime(ms, c->ev[a], c->ev[b]));
   return HH_OK;
 }
 
@@ -461,12 +491,10 @@ int hh_gemv_q8(hh_ctx* c, int type, const void* w, int64_t n_rows, int64_t n_col
   int el = hh_unit_el(fmt);
   if (n_cols <= 0 || n_cols % el != 0)
     return fail(HH_ERR_DIM, "n_cols must be a positive multiple of " + std::to_string(el));
-  if (n_cols > 32768) return fail(HH_ERR_DIM, "n_cols above 32768");
+  if (n_cols > 20480) return fail(HH_ERR_DIM, "n_cols above 20480");
   if (n_rows <= 0 || n_rows > (1ll << 30)) return fail(HH_ERR_DIM, "bad n_rows");
   int P = (int)n_cols / el;
-  int rows = 4096 / P;
-  if (rows < 4) rows = 4;
-  if (rows > 64) rows = 64;
+  int rows = gemv_rows_for((int)n_rows, P);
   GemvArgs a = gemv_base((const uint8_t*)w, (int)n_rows, (int)n_cols, rows);
   a.act = xq8;
   a.y = y;
@@ -491,19 +519,29 @@ int hh_rope(hh_ctx* c, float* x, int n_heads, int hd, int rope_dim, const float*
 int hh_attention(hh_ctx* c, const float* q, const float* k, const float* v, int n_heads, int n_kv, int hd,
                  int max_seq, int seq_len, float* out) {
   if (!c || !q || !k || !v || !out) return fail(HH_ERR_INVALID, "null argument");
-  if (n_kv <= 0 || n_heads % n_kv || hd <= 0 || 4096 % hd || hd < 64 || hd > 256)
-    return fail(HH_ERR_DIM, "unsupported attention geometry");
+  if (n_kv <= 0 || n_heads % n_kv || (hd != 128 && hd != 256))
+    return fail(HH_ERR_DIM, "unsupported attention geometry (head_dim 128 or 256)");
   if (seq_len <= 0 || seq_len > max_seq) return fail(HH_ERR_RANGE, "seq_len out of range");
   int G = n_heads / n_kv;
   if (G > 16) return fail(HH_ERR_DIM, "too many query heads per kv head");
-  int chunk = 4096 / hd;
+  int chunk = 8192 / hd;
   int splits = (seq_len + chunk - 1) / chunk;
-  float *po = nullptr, *pml = nullptr;
-  int* cnt = nullptr;
-  HIP_TRY(hipMallocAsync((void**)&po, sizeof(float) * (size_t)n_kv * splits * G * hd, c->stream));
-  HIP_TRY(hipMallocAsync((void**)&pml, sizeof(float) * (size_t)n_kv * splits * G * 2, c->stream));
-  HIP_TRY(hipMallocAsync((void**)&cnt, sizeof(int) * (size_t)n_kv, c->stream));
-  HIP_TRY(hipMemsetAsync(cnt, 0, sizeof(int) * (size_t)n_kv, c->stream));
+  // split partials live in a context scratch buffer grown on demand; the
+  // per-kv-head counters are reset by the kernel itself after use
+  size_t need = sizeof(float) * (size_t)n_kv * splits * G * (hd + 2) + sizeof(int) * 1024;
+  if (n_kv > 1024) return fail(HH_ERR_DIM, "too many kv heads");
+  if (c->attn_scratch_bytes < need) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->attn_scratch) HIP_TRY(hipFree(c->attn_scratch));
+    c->attn_scratch = nullptr;
+    c->attn_scratch_bytes = 0;
+    HIP_TRY(hipMalloc(&c->attn_scratch, need));
+    HIP_TRY(hipMemset(c->attn_scratch, 0, need));
+    c->attn_scratch_bytes = need;
+  }
+  int* cnt = (int*)c->attn_scratch;
+  float* po = (float*)((char*)c->attn_scratch + sizeof(int) * 1024);
+  float* pml = po + (size_t)n_kv * splits * G * hd;
   AttnArgs a{};
   a.qkv = q;
   a.n_heads = n_heads;
@@ -520,9 +558,6 @@ int hh_attention(hh_ctx* c, const float* q, const float* k, const float* v, int 
   a.counters = cnt;
   a.out_f32 = out;
   int rc = hh_attn_launch(a, c->stream);
-  hipFreeAsync(po, c->stream);
-  hipFreeAsync(pml, c->stream);
-  hipFreeAsync(cnt, c->stream);
   if (rc) return fail(HH_ERR_HIP, std::string("attention launch: ") + hipGetErrorString(hipGetLastError()));
   return HH_OK;
 }
@@ -560,8 +595,8 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   if (c.head_type != HH_Q8_0) return fail(HH_ERR_DTYPE, "token_embd/output must be Q8_0");
   if (c.d_model % 1024 || c.d_ffn % 1024 || c.n_layers <= 0 || c.vocab <= 0)
     return fail(HH_ERR_DIM, "d_model and d_ffn must be multiples of 1024");
-  if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || c.head_dim < 64 || c.head_dim > 256 || 4096 % c.head_dim)
-    return fail(HH_ERR_DIM, "unsupported attention geometry");
+  if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || (c.head_dim != 128 && c.head_dim != 256))
+    return fail(HH_ERR_DIM, "unsupported attention geometry (head_dim 128 or 256)");
   if ((c.n_heads * c.head_dim) % 256) return fail(HH_ERR_DIM, "n_heads*head_dim must be a multiple of 256");
   if (c.max_seq <= 0) return fail(HH_ERR_DIM, "max_seq must be positive");
   if (c.arch == 1) {
@@ -680,7 +715,7 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   }
   // step buffers
   int wide = std::max(std::max(c.d_model, c.d_ffn), std::max((c.attn_out_gate ? 2 : 1) * nq + 2 * nkv, conv_dim + vdim));
-  m->attn_chunk = 4096 / hd;
+  m->attn_chunk = 8192 / hd;
   m->attn_splits = (c.max_seq + m->attn_chunk - 1) / m->attn_chunk;
   int G = c.n_heads / c.n_kv_heads;
   int head_wg = (c.vocab + m->rows_head - 1) / m->rows_head;
@@ -708,11 +743,11 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   // launch geometry: ~256-1024 units of work per workgroup
   {
     int el = hh_unit_el(wf);
-    int P = c.d_model / el;
-    m->rows_in = std::max(4, std::min(64, 256 / P));
+    int n_in_max = std::max((c.attn_out_gate ? 2 : 1) * nq + 2 * nkv, c.arch == 1 ? conv_dim + vdim : 0);
+    m->rows_in = gemv_rows_for(n_in_max, c.d_model / el);
     m->rows_gu = 32;
-    m->rows_out = std::max(4, std::min(64, 256 / std::max(1, std::max(nq, vdim) / el)));
-    m->rows_down = std::max(4, std::min(64, 1024 / (c.d_ffn / el)));
+    m->rows_out = gemv_rows_for(c.d_model, std::max(nq, vdim) / el);
+    m->rows_down = gemv_rows_for(c.d_model, c.d_ffn / el);
     m->rows_head = 64;
   }
   HIP_TRY(hipDeviceSynchronize());
@@ -900,12 +935,19 @@ int hh_model_time_stages(hh_model* m, int layer, int iters, double* out_ms, int 
   fixed.n_prompt = 1;
   fixed.step = 0;
   HIP_TRY(hipMemcpyAsync(m->state, &fixed, sizeof fixed, hipMemcpyHostToDevice, s));
+  // Each stage is launched for every layer in turn (layers of one kind only),
+  // so its weights stream from HBM as in a real step rather than from the
+  // 256 MB last-level cache a single repeated layer would sit in.
+  const bool want_gdn = m->layers[layer].gdn;
+  std::vector<int> same;
+  for (int li = 0; li < m->cfg.n_layers; ++li)
+    if (m->layers[li].gdn == want_gdn) same.push_back(li);
   for (int stg = 0; stg < n_out && stg < 7; ++stg) {
     int rc = enqueue_step(m, s, layer, 1u << stg);   // warm
     if (rc) return rc;
     HIP_TRY(hipEventRecord(m->ev0, s));
     for (int i = 0; i < iters; ++i) {
-      rc = enqueue_step(m, s, layer, 1u << stg);
+      rc = enqueue_step(m, s, same[i % same.size()], 1u << stg);
       if (rc) return rc;
     }
     HIP_TRY(hipEventRecord(m->ev1, s));

@@ -123,6 +123,8 @@ _EXPORTS = {
     "hh_memcpy_h2d": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     "hh_memcpy_d2h": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     "hh_memset": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_size_t]),
+    "hh_ctx_event_record": (C.c_int, [C.c_void_p, C.c_int]),
+    "hh_ctx_event_elapsed": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "hh_quantize_q8_0": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
     "hh_dequantize": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int64, C.c_void_p]),
     "hh_gemv_q8": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]),
@@ -216,6 +218,14 @@ class Ctx:
 
     def sync(self) -> None:
         _check(self.lib.hh_ctx_synchronize(self.h))
+
+    def event(self, slot: int) -> None:
+        _check(self.lib.hh_ctx_event_record(self.h, slot))
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        v = C.c_float()
+        _check(self.lib.hh_ctx_event_elapsed(self.h, a, b, C.byref(v)))
+        return v.value
 
     # ---- operators on device tensors (torch cuda tensors or raw addresses) ----
     def quantize_q8_0(self, x, n: int, out) -> None:

@@ -71,6 +71,10 @@ int hh_free(hh_ctx* ctx, void* dptr);
 int hh_memcpy_h2d(hh_ctx* ctx, void* dst, const void* src, size_t nbytes);
 int hh_memcpy_d2h(hh_ctx* ctx, void* dst, const void* src, size_t nbytes);
 int hh_memset(hh_ctx* ctx, void* dst, int value, size_t nbytes);
+/* Device-clock timing on the context's stream (hipEvents in 8 slots): record
+ * a slot, then read the milliseconds between two recorded slots (waits for b). */
+int hh_ctx_event_record(hh_ctx* ctx, int slot);
+int hh_ctx_event_elapsed(hh_ctx* ctx, int slot_a, int slot_b, float* ms);
 
 /* ---- operators (all pointers are device pointers; enqueued on the ctx stream) ---- */
 
@@ -85,7 +89,8 @@ int hh_dequantize(hh_ctx* ctx, int ggml_type, const void* w, int64_t n, float* o
  * r < n_rows.  Replaces ThreadPool::par_dot_rows with dot_fn in
  * {dot_q2_0_q8_0_ptr (q2_0.rs:628), dot_q1_0g128_q8_0_ptr (q1_0g128.rs:1000),
  *  dot_q8_0_q8_0_ptr (q8_0.rs:154)} (pool.rs:510-566, matmul.rs:153-269).
- * x_q8: n_cols/32 standard Q8_0 blocks. */
+ * x_q8: n_cols/32 standard Q8_0 blocks.  n_cols: a multiple of 256 (Q1_0/Q2_0)
+ * or 64 (Q8_0), at most 20480. */
 int hh_gemv_q8(hh_ctx* ctx, int ggml_type, const void* w, int64_t n_rows, int64_t n_cols,
                const uint8_t* x_q8, float* y);
 

@@ -743,11 +743,11 @@ static void dev_rms_norm_wave(const float* x, const float* w, float eps, int n, 
   for (int i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
 }
 
-/* Split-sequence attention for one query head: chunks of C = 4096/hd positions,
+/* Split-sequence attention for one query head: chunks of C = 8192/hd positions,
  * per chunk max / exp / butterfly sum / sequential fma of p*v, then the chunks
  * merged with exp(m_s - M) weights. */
 static void dev_attention(const float* q, const float* k, const float* v, int seq, int hd, float* out) {
-  int C = 4096 / hd, ns = (seq + C - 1) / C;
+  int C = 8192 / hd, ns = (seq + C - 1) / C;
   float inv_sqrt = 1.0f / sqrtf((float)hd);
   float* ms = (float*)malloc(sizeof(float) * (size_t)ns * (hd + 3));
   float* ls = ms + ns;
