@@ -154,11 +154,51 @@ HH_DEV void head_norm_rope(float* v, int hd, const float* nw, float eps, const f
   (void)tmp_pair;
 }
 
-__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+// Butterfly sum of NV values held by each lane of an aligned LPR-lane group,
+// done as a reduce-scatter: at offset O every lane keeps one half of its
+// values and adds the partner's copy of that half.  Each kept value equals
+// the all-lanes butterfly x_l + x_(l^O) at that level, so the result for
+// value k is the butterfly sum with offsets LPR/2, ..., 1.  On return lane l
+// holds value k = (l % LPR) >> log2(LPR / NV).
+template <int N, int O> struct ReduceScatter {
+  static HH_DEV float run(float* v, int lane) {
+    if constexpr (N > 1) {
+      static_assert(O > 0, "more values than lanes");
+      const bool up = (lane & O) != 0;
+#pragma unroll
+      for (int k = 0; k < N / 2; ++k) {
+        float send = up ? v[k] : v[k + N / 2];
+        float keep = up ? v[k + N / 2] : v[k];
+        v[k] = keep + __shfl_xor(send, O, 64);
+      }
+      return ReduceScatter<N / 2, O / 2>::run(v, lane);
+    } else {
+      float x = v[0];
+#pragma unroll
+      for (int o = O; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+      return x;
+    }
+  }
+};
+
+// Split kernel: workgroup (s, kvh) owns positions [s*C, s*C + C) of kv head
+// kvh for its G query heads.  Thread t holds one float4 column slice
+// (c = t % LPR) of rows j = i*RPI + t/LPR, i < 8, of K and V in registers,
+// so the chunk is read from HBM exactly once and never staged through LDS.
+//  * score(h, j) = (butterfly over the LPR lanes of the row of the 4-term
+//    fma chain q.k) * 1/sqrt(hd)
+//  * e = exp(score - m), m and l = sum e by a 64-lane butterfly
+//  * o(h, d): per row group `sub` an fma chain over i; hd 128: the two row
+//    groups of a wave are added, then waves as (w0 + w1) + (w2 + w3);
+//    hd 256: (w0 + w1) + (w2 + w3) directly.
+// Writes the unnormalised partial o and (m, l) of every (split, head).
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
+  constexpr int LPR = HD / 4, RPI = 256 / LPR, C = RPI * 8;
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int s = blockIdx.x, kvh = blockIdx.y;
-  const int hd = a.hd, G = a.n_heads / a.n_kv, C = a.chunk;
+  const int G = a.n_heads / a.n_kv;
   int seq, pos;
   bool prep;
   if (a.fixed_seq > 0) {
@@ -170,178 +210,222 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   if (s >= n_active) return;
   const int p0 = s * C, np = min(C, seq - p0);
   const bool has_new = prep && pos >= p0 && pos < p0 + np;
-  const int KS = hd + 4;
-  float* qs = sm;                 // G*hd
-  float* Ks = qs + G * hd;        // C*KS
-  float* Vs = Ks + C * KS;        // C*hd
-  float* sc = Vs + C * hd;        // G*C
-  float* kn = sc + G * C;         // hd
-  float* vn = kn + hd;            // hd
-  float* ml = vn + hd;            // 2*G
-  float* wts = ml + 2 * G + 8;    // G * max_splits (combine)
-  const size_t hstride = (size_t)a.max_seq * hd;
-  const float* kg = a.k_cache + (size_t)kvh * hstride;
-  const float* vg = a.v_cache + (size_t)kvh * hstride;
+  const int sub = tid / LPR, c = tid % LPR;
+  float* qs = sm;                 // G*HD
+  float* kn = qs + G * HD;        // HD
+  float* vn = kn + HD;            // HD
+  float* sc = vn + HD;            // G*C
+  float* ml = sc + G * C;         // 2*G (+pad)
+  float* red = ml + 2 * G + 4;    // 4 waves * 4 heads * HD
+  const size_t hstride = (size_t)a.max_seq * HD;
+  const float* kg = a.k_cache + (size_t)kvh * hstride + 4 * c;
+  const float* vg = a.v_cache + (size_t)kvh * hstride + 4 * c;
 
-  // 1. issue this chunk's K/V loads (C*hd == 8192 floats each: 8 float4 per lane)
+  // 1. issue this chunk's K/V loads
   float4 kr[8], vr[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    int f = (i * 256 + tid) * 4;
-    int row = f / hd, col = f % hd;
-    if (row < np && p0 + row != pos) {
-      kr[i] = *(const float4*)(kg + (size_t)(p0 + row) * hd + col);
-      vr[i] = *(const float4*)(vg + (size_t)(p0 + row) * hd + col);
+    const int j = i * RPI + sub;
+    kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    vr[i] = kr[i];
+    if (j < np && p0 + j != pos) {
+      kr[i] = *(const float4*)(kg + (size_t)(p0 + j) * HD);
+      vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
     }
   }
-  // 2. q heads (and the new k/v) : raw -> LDS, norm + rope by one wave per head
+  // 2. q heads (and the new k/v): raw -> LDS, then norm + rope, one wave per head
   for (int h = 0; h < G; ++h) {
-    int qh = kvh * G + h;
-    const float* src = a.qkv + (a.gated ? (size_t)qh * 2 * hd : (size_t)qh * hd);
-    for (int d = tid; d < hd; d += 256) qs[h * hd + d] = src[d];
+    const int qh = kvh * G + h;
+    const float* src = a.qkv + (a.gated ? (size_t)qh * 2 * HD : (size_t)qh * HD);
+    for (int d = tid; d < HD; d += 256) qs[h * HD + d] = src[d];
   }
   if (has_new) {
-    const float* ksrc = a.qkv + a.q_stride_heads + (size_t)kvh * hd;
-    const float* vsrc = a.qkv + a.q_stride_heads + (size_t)a.n_kv * hd + (size_t)kvh * hd;
-    for (int d = tid; d < hd; d += 256) { kn[d] = ksrc[d]; vn[d] = vsrc[d]; }
+    const float* ksrc = a.qkv + a.q_stride_heads + (size_t)kvh * HD;
+    const float* vsrc = a.qkv + a.q_stride_heads + (size_t)a.n_kv * HD + (size_t)kvh * HD;
+    for (int d = tid; d < HD; d += 256) { kn[d] = ksrc[d]; vn[d] = vsrc[d]; }
   }
   __syncthreads();
   if (prep) {
     for (int h = wid; h < G; h += 4)
-      head_norm_rope(qs + h * hd, hd, a.q_norm, a.eps, a.rope, a.rope_dim, a.max_seq, pos, lane, nullptr);
-    if (has_new && wid == (G % 4)) {
-      head_norm_rope(kn, hd, a.k_norm, a.eps, a.rope, a.rope_dim, a.max_seq, pos, lane, nullptr);
-    }
+      head_norm_rope(qs + h * HD, HD, a.q_norm, a.eps, a.rope, a.rope_dim, a.max_seq, pos, lane, nullptr);
+    if (has_new && wid == (G % 4))
+      head_norm_rope(kn, HD, a.k_norm, a.eps, a.rope, a.rope_dim, a.max_seq, pos, lane, nullptr);
   }
   __syncthreads();
   if (has_new) {   // kvcache.rs:92-113 write_kv
-    float* kdst = a.k_cache + (size_t)kvh * hstride + (size_t)pos * hd;
-    float* vdst = a.v_cache + (size_t)kvh * hstride + (size_t)pos * hd;
-    for (int d = tid; d < hd; d += 256) { kdst[d] = kn[d]; vdst[d] = vn[d]; }
-  }
-  // 3. chunk into LDS
+    float* kdst = a.k_cache + (size_t)kvh * hstride + (size_t)pos * HD;
+    float* vdst = a.v_cache + (size_t)kvh * hstride + (size_t)pos * HD;
+    for (int d = tid; d < HD; d += 256) { kdst[d] = kn[d]; vdst[d] = vn[d]; }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int f = (i * 256 + tid) * 4;
-    int row = f / hd, col = f % hd;
-    if (row < np) {
-      float4 k4 = kr[i], v4 = vr[i];
-      if (p0 + row == pos) {
-        k4 = make_float4(kn[col], kn[col + 1], kn[col + 2], kn[col + 3]);
-        v4 = make_float4(vn[col], vn[col + 1], vn[col + 2], vn[col + 3]);
+    for (int i = 0; i < 8; ++i) {
+      if (p0 + i * RPI + sub == pos) {
+        kr[i] = *(const float4*)(kn + 4 * c);
+        vr[i] = *(const float4*)(vn + 4 * c);
       }
-      *(float4*)(Ks + row * KS + col) = k4;
-      *(float4*)(Vs + row * hd + col) = v4;
     }
   }
-  __syncthreads();
-  // 4. scores (ops.rs:362-374): dot * 1/sqrt(hd)
-  const float inv_sqrt = 1.0f / sqrtf((float)hd);
-  for (int idx = tid; idx < G * C; idx += 256) {
-    int h = idx / C, j = idx % C;
-    float sc_v = -INFINITY;
-    if (j < np) {
-      const float4* kq = (const float4*)(Ks + j * KS);
-      const float4* qq = (const float4*)(qs + h * hd);
-      float acc = 0.0f;
-      for (int d4 = 0; d4 < hd / 4; ++d4) {
-        float4 k4 = kq[d4], q4 = qq[d4];
-        acc = fmaf(q4.x, k4.x, acc);
-        acc = fmaf(q4.y, k4.y, acc);
-        acc = fmaf(q4.z, k4.z, acc);
-        acc = fmaf(q4.w, k4.w, acc);
+  // 3. scores (ops.rs:362-374), four heads per pass
+  const float inv_sqrt = 1.0f / sqrtf((float)HD);
+  constexpr int KSH = (LPR == 64) ? 1 : 0;
+  for (int hg = 0; hg < G; hg += 4) {
+    float v[32];
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (hg + hh < G) q4 = *(const float4*)(qs + (hg + hh) * HD + 4 * c);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float p = q4.x * kr[i].x;
+        p = fmaf(q4.y, kr[i].y, p);
+        p = fmaf(q4.z, kr[i].z, p);
+        p = fmaf(q4.w, kr[i].w, p);
+        v[hh * 8 + i] = p;
       }
-      sc_v = acc * inv_sqrt;
     }
-    sc[idx] = sc_v;
+    const float r = ReduceScatter<32, LPR / 2>::run(v, lane);
+    const int k = (lane & (LPR - 1)) >> KSH;
+    const int h = hg + (k >> 3), j = (k & 7) * RPI + sub;
+    if (h < G && (KSH == 0 || (lane & 1) == 0)) sc[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
   }
   __syncthreads();
-  // 5. per-head local softmax statistics (C <= 64)
+  // 4. per-head softmax statistics over the chunk (C <= 64)
   for (int h = wid; h < G; h += 4) {
-    float v = lane < C ? sc[h * C + lane] : -INFINITY;
-    float m = wave_max(v);
-    float e = (lane < np) ? hx_exp(v - m) : 0.0f;
+    float x = lane < C ? sc[h * C + lane] : -INFINITY;
+    float m = wave_max(x);
+    float e = (lane < np) ? hx_exp(x - m) : 0.0f;
     float l = wave_sum(e);
     if (lane < C) sc[h * C + lane] = e;
     if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
   }
   __syncthreads();
-  // 6. o = sum_j e_j v_j
+  // 5. o = sum_j e_j v_j
   const size_t pbase = ((size_t)kvh * a.max_splits + s) * G;
-  for (int idx = tid; idx < G * hd; idx += 256) {
-    int h = idx / hd, d = idx % hd;
-    float acc = 0.0f;
-    for (int j = 0; j < np; ++j) acc = fmaf(sc[h * C + j], Vs[j * hd + d], acc);
-    a.part_o[(pbase + h) * hd + d] = acc;
+  for (int hg = 0; hg < G; hg += 4) {
+    float acc[16];
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+      if (hg + hh < G) {
+        const float* eh = sc + (hg + hh) * C + sub;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float e = eh[i * RPI];
+          o0 = fmaf(e, vr[i].x, o0);
+          o1 = fmaf(e, vr[i].y, o1);
+          o2 = fmaf(e, vr[i].z, o2);
+          o3 = fmaf(e, vr[i].w, o3);
+        }
+      }
+      acc[hh * 4 + 0] = o0; acc[hh * 4 + 1] = o1; acc[hh * 4 + 2] = o2; acc[hh * 4 + 3] = o3;
+    }
+    if constexpr (LPR == 32) {
+      // the two row groups of this wave: lanes < 32 keep heads 0-1, others 2-3
+      const bool up = (lane & 32) != 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        float send = up ? acc[k] : acc[k + 8];
+        float keep = up ? acc[k + 8] : acc[k];
+        float x = keep + __shfl_xor(send, 32, 64);
+        const int kk = k + (up ? 8 : 0);
+        red[(wid * 4 + (kk >> 2)) * HD + 4 * c + (kk & 3)] = x;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) red[(wid * 4 + (k >> 2)) * HD + 4 * c + (k & 3)] = acc[k];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < 4 * HD; idx += 256) {
+      const int h = hg + idx / HD;
+      if (h < G) {
+        float o = (red[idx] + red[4 * HD + idx]) + (red[8 * HD + idx] + red[12 * HD + idx]);
+        a.part_o[(pbase + h) * HD + (idx % HD)] = o;
+      }
+    }
+    __syncthreads();
   }
   if (tid < G) {
     a.part_ml[(pbase + tid) * 2] = ml[2 * tid];
     a.part_ml[(pbase + tid) * 2 + 1] = ml[2 * tid + 1];
   }
-  // 7. last workgroup of this kv head merges the splits
-  __shared__ int is_last;
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    is_last = (atomicAdd(a.counters + kvh, 1) == n_active - 1);
+}
+
+// Merge kernel: workgroup (qh, 64-column slice).  M = max m_t, w_t =
+// exp(m_t - M), L = sum w_t l_t (lane-strided over t, then a butterfly);
+// wave g sums the splits t = g (mod 4) as an fma chain in increasing t, and
+// o = ((P0 + P1) + (P2 + P3)) / L.  Applies the qwen35 output gate and emits
+// the f32 row and/or the packed Q8_0 input of attn_output.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
+  extern __shared__ __align__(16) float wm[];
+  float* wts = wm;                         // max_splits
+  float* pw = wm + a.max_splits;           // 4 x 64
+  float* sL = pw + 256;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int qh = blockIdx.x, d = blockIdx.y * 64 + lane;
+  const int G = a.n_heads / a.n_kv, kvh = qh / G, h = qh % G;
+  constexpr int C = (256 / (HD / 4)) * 8;
+  const int seq = a.fixed_seq > 0 ? a.fixed_seq : a.state->pos + 1;
+  const int n_active = (seq + C - 1) / C;
+  const size_t hb = (size_t)kvh * a.max_splits * G + h;
+  const size_t tstride = (size_t)G * HD;
+  const float* pb = a.part_o + hb * HD + d;
+  float pv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = wid + 4 * i;
+    pv[i] = t < n_active ? pb[(size_t)t * tstride] : 0.0f;
   }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int h = wid; h < G; h += 4) {
-    const size_t hb = (size_t)kvh * a.max_splits * G + h;   // + s'*G
+  if (wid == 0) {
     float M = -INFINITY;
     for (int t = lane; t < n_active; t += 64) M = fmaxf(M, a.part_ml[(hb + (size_t)t * G) * 2]);
     M = wave_max(M);
     float L = 0.0f;
     for (int t = lane; t < n_active; t += 64) {
       float e = hx_exp(a.part_ml[(hb + (size_t)t * G) * 2] - M);
-      wts[h * a.max_splits + t] = e;
+      wts[t] = e;
       L += e * a.part_ml[(hb + (size_t)t * G) * 2 + 1];
     }
     L = wave_sum(L);
-    float invL = 1.0f / L;
-    int qh = kvh * G + h;
-    // o[d] = sum_t w_t o_t[d] in split order; the partials of 16 splits are
-    // fetched together so the loop waits on one round trip per batch
-    const size_t tstride = (size_t)G * hd;
-    for (int d0 = 0; d0 < hd; d0 += 64) {
-      int d = d0 + lane;
-      float o = 0.0f;
-      const float* pb = a.part_o + hb * hd + d;
-      for (int t0 = 0; t0 < n_active; t0 += 16) {
-        float pv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) pv[i] = (t0 + i < n_active) ? pb[(size_t)(t0 + i) * tstride] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (t0 + i < n_active) o = fmaf(wts[h * a.max_splits + t0 + i], pv[i], o);
-      }
-      o = o * invL;
-      if (a.gated) {   // qwen35.rs:1627-1629 attn_out /= 1 + exp(-gate)
-        float g = a.qkv[(size_t)qh * 2 * hd + hd + d];
-        o = o / (1.0f + hx_exp(-g));
-      }
-      if (a.out_f32) a.out_f32[(size_t)qh * hd + d] = o;
-      if (a.act_out) {
-        float am = group_max<32>(fabsf(o));
-        float scq = q8_scale(am);
-        int q = q8_round(o, scq);
-        int qsum = group_sum_i<32>(q);
-        int e = qh * hd + d;
-        int K = a.n_heads * hd;
-        a.act_out[perm_pos(a.act_fmt, e)] = (uint8_t)(int8_t)q;
-        if ((lane & 31) == 0) {
-          ((float*)(a.act_out + K))[e >> 5] = h2f(f2h(scq));
-          ((int*)(a.act_out + K + (K / 32) * 4))[e >> 5] = qsum;
-        }
-      }
-    }
+    if (lane == 0) *sL = L;
   }
   __syncthreads();
-  if (tid == 0) {
-    a.counters[kvh] = 0;
-    __threadfence();
+  float P = 0.0f;
+  for (int t0 = 0; t0 < n_active; t0 += 64) {
+    if (t0 > 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = t0 + wid + 4 * i;
+        pv[i] = t < n_active ? pb[(size_t)t * tstride] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int t = t0 + wid + 4 * i;
+      if (t < n_active) P = fmaf(wts[t], pv[i], P);
+    }
+  }
+  pw[wid * 64 + lane] = P;
+  __syncthreads();
+  if (wid != 0) return;
+  float o = (pw[lane] + pw[64 + lane]) + (pw[128 + lane] + pw[192 + lane]);
+  o = o * (1.0f / *sL);
+  if (a.gated) {   // qwen35.rs:1627-1629 attn_out /= 1 + exp(-gate)
+    float g = a.qkv[(size_t)qh * 2 * HD + HD + d];
+    o = o / (1.0f + hx_exp(-g));
+  }
+  if (a.out_f32) a.out_f32[(size_t)qh * HD + d] = o;
+  if (a.act_out) {
+    float am = group_max<32>(fabsf(o));
+    float scq = q8_scale(am);
+    int q = q8_round(o, scq);
+    int qsum = group_sum_i<32>(q);
+    int e = qh * HD + d;
+    int K = a.n_heads * HD;
+    a.act_out[perm_pos(a.act_fmt, e)] = (uint8_t)(int8_t)q;
+    if ((lane & 31) == 0) {
+      ((float*)(a.act_out + K))[e >> 5] = h2f(f2h(scq));
+      ((int*)(a.act_out + K + (K / 32) * 4))[e >> 5] = qsum;
+    }
   }
 }
 
@@ -533,11 +617,18 @@ int hh_embed_launch(int type, const uint8_t* table, int d, const StepState* st, 
 }
 
 int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
-  int G = a.n_heads / a.n_kv;
-  size_t floats = (size_t)G * a.hd + (size_t)a.chunk * (a.hd + 4) + (size_t)a.chunk * a.hd + (size_t)G * a.chunk +
-                  2 * (size_t)a.hd + 2 * G + 8 + (size_t)G * a.max_splits;
+  const int G = a.n_heads / a.n_kv;
   if (a.hd != 128 && a.hd != 256) return 1;
-  hipLaunchKernelGGL(k_attn, dim3(a.max_splits, a.n_kv), dim3(256), floats * 4, s, a);
+  if (a.chunk != 8192 / a.hd || a.n_kv * G != a.n_heads) return 1;
+  const size_t split_lds = 4 * ((size_t)G * a.hd + 2 * (size_t)a.hd + (size_t)G * a.chunk + 2 * G + 4 + 16 * (size_t)a.hd);
+  const size_t merge_lds = 4 * ((size_t)a.max_splits + 256 + 4);
+  if (a.hd == 128) {
+    hipLaunchKernelGGL(k_attn_split<128>, dim3(a.max_splits, a.n_kv), dim3(256), split_lds, s, a);
+    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_heads, 2), dim3(256), merge_lds, s, a);
+  } else {
+    hipLaunchKernelGGL(k_attn_split<256>, dim3(a.max_splits, a.n_kv), dim3(256), split_lds, s, a);
+    hipLaunchKernelGGL(k_attn_merge<256>, dim3(a.n_heads, 4), dim3(256), merge_lds, s, a);
+  }
   return ok();
 }
 

@@ -746,8 +746,26 @@ static void dev_rms_norm_wave(const float* x, const float* w, float eps, int n, 
 /* Split-sequence attention for one query head: chunks of C = 8192/hd positions,
  * per chunk max / exp / butterfly sum / sequential fma of p*v, then the chunks
  * merged with exp(m_s - M) weights. */
+/* Butterfly sum over n lanes (n a power of two <= 64), offsets n/2 .. 1. */
+static float bfly_n(const float* v, int n) {
+  float a[64], b[64];
+  memcpy(a, v, sizeof(float) * (size_t)n);
+  for (int o = n / 2; o > 0; o >>= 1) {
+    for (int i = 0; i < n; i++) b[i] = a[i] + a[i ^ o];
+    memcpy(a, b, sizeof(float) * (size_t)n);
+  }
+  return a[0];
+}
+
+/* Split-sequence attention in the device's grouping: chunks of C = 8192/hd
+ * positions; a score is the butterfly over hd/4 column slices of a 4-term
+ * fma chain; the chunk's o is summed per row group (rows i*RPI + sub) as an
+ * fma chain over i and the groups are combined pairwise; splits merge with
+ * w_t = exp(m_t - M) as four strided fma chains added pairwise.  The
+ * reference computes the same softmax-weighted sum in one pass
+ * (ops.rs:353-406). */
 static void dev_attention(const float* q, const float* k, const float* v, int seq, int hd, float* out) {
-  int C = 8192 / hd, ns = (seq + C - 1) / C;
+  const int C = 8192 / hd, LPR = hd / 4, RPI = 256 / LPR, ns = (seq + C - 1) / C;
   float inv_sqrt = 1.0f / sqrtf((float)hd);
   float* ms = (float*)malloc(sizeof(float) * (size_t)ns * (hd + 3));
   float* ls = ms + ns;
@@ -755,13 +773,18 @@ static void dev_attention(const float* q, const float* k, const float* v, int se
   float* os = wts + ns;
   for (int s = 0; s < ns; s++) {
     int p0 = s * C, np = seq - p0 < C ? seq - p0 : C;
-    float sc[64], e[64];
+    float sc[64], e[64], parts[64];
     for (int l = 0; l < 64; l++) sc[l] = -INFINITY;
     for (int j = 0; j < np; j++) {
       const float* kr = k + (size_t)(p0 + j) * hd;
-      float acc = 0.0f;
-      for (int d = 0; d < hd; d++) acc = fmaf(q[d], kr[d], acc);
-      sc[j] = acc * inv_sqrt;
+      for (int c = 0; c < LPR; c++) {
+        float p = q[4 * c] * kr[4 * c];
+        p = fmaf(q[4 * c + 1], kr[4 * c + 1], p);
+        p = fmaf(q[4 * c + 2], kr[4 * c + 2], p);
+        p = fmaf(q[4 * c + 3], kr[4 * c + 3], p);
+        parts[c] = p;
+      }
+      sc[j] = bfly_n(parts, LPR) * inv_sqrt;
     }
     float m = -INFINITY;
     for (int l = 0; l < 64; l++) m = fmaxf(m, sc[l]);
@@ -769,9 +792,23 @@ static void dev_attention(const float* q, const float* k, const float* v, int se
     ms[s] = m;
     ls[s] = bfly64(e);
     for (int d = 0; d < hd; d++) {
-      float acc = 0.0f;
-      for (int j = 0; j < np; j++) acc = fmaf(e[j], v[(size_t)(p0 + j) * hd + d], acc);
-      os[(size_t)s * hd + d] = acc;
+      float A[8] = {0};
+      for (int sub = 0; sub < RPI; sub++) {
+        float acc = 0.0f;
+        for (int i = 0; i < 8; i++) {
+          int j = i * RPI + sub;
+          if (j < np) acc = fmaf(e[j], v[(size_t)(p0 + j) * hd + d], acc);
+        }
+        A[sub] = acc;
+      }
+      float o;
+      if (RPI == 8) {
+        float X0 = A[0] + A[1], X1 = A[2] + A[3], X2 = A[4] + A[5], X3 = A[6] + A[7];
+        o = (X0 + X1) + (X2 + X3);
+      } else {
+        o = (A[0] + A[1]) + (A[2] + A[3]);
+      }
+      os[(size_t)s * hd + d] = o;
     }
   }
   float M = -INFINITY;
@@ -788,9 +825,12 @@ static void dev_attention(const float* q, const float* k, const float* v, int se
   }
   float invL = 1.0f / bfly64(lanes);
   for (int d = 0; d < hd; d++) {
-    float o = 0.0f;
-    for (int t = 0; t < ns; t++) o = fmaf(wts[t], os[(size_t)t * hd + d], o);
-    out[d] = o * invL;
+    float P[4];
+    for (int g = 0; g < 4; g++) {
+      P[g] = 0.0f;
+      for (int t = g; t < ns; t += 4) P[g] = fmaf(wts[t], os[(size_t)t * hd + d], P[g]);
+    }
+    out[d] = ((P[0] + P[1]) + (P[2] + P[3])) * invL;
   }
   free(ms);
 }

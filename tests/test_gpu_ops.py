@@ -137,7 +137,7 @@ def test_rms_norm_rope_attention(ctx, oracle):
         want[h * hd:(h + 1) * hd] = hh
     assert np.array_equal(host(qd), want)
     # attention (GQA 32/8, hd 128, seq 2049)
-    for (nh, nkv, hd, seq) in ((32, 8, 128, 2049), (16, 4, 256, 300), (16, 8, 128, 1)):
+    for (nh, nkv, hd, seq) in ((32, 8, 128, 2049), (16, 4, 256, 300), (16, 8, 128, 1), (24, 4, 256, 77)):
         ms = seq + 7
         qv = rng.standard_normal(nh * hd).astype(np.float32)
         kc = rng.standard_normal(nkv * ms * hd).astype(np.float32)
