@@ -337,27 +337,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
   const int P = p.P;
 
   if constexpr (EPI == EPI_LOGITS) {
-    StepState* st = p.state;
     // Prompt tokens other than the last need no logits (forward_batch computes
-    // only the last token's, mod.rs:1201-1218): count in, advance, leave.
-    if (st->step + 1 < st->n_prompt) {
-      __syncthreads();
-      __shared__ int last_pf;
-      if (tid == 0) {
-        __threadfence();
-        last_pf = (atomicAdd(p.counter, 1) == (int)gridDim.x - 1);
-      }
-      __syncthreads();
-      if (last_pf && tid == 0) {
-        int s = st->step;
-        st->token = (int)p.prompt[s + 1];
-        st->pos = st->pos + 1;
-        st->step = s + 1;
-        *p.counter = 0;
-        __threadfence();
-      }
-      return;
-    }
+    // only the last token's, mod.rs:1201-1218); k_head_final advances the state.
+    const StepState* st = p.state;
+    if (st->step + 1 < st->n_prompt) return;
   }
 
   // rows owned by this workgroup
@@ -472,7 +455,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
       }
     }
   } else if constexpr (EPI == EPI_LOGITS) {
-    StepState* st = p.state;
+    const StepState* st = p.state;
     const int rule = p.rule;
     const float pen = st->pen;
     const bool do_pen = !(fabsf(pen - 1.0f) < 1e-6f);
@@ -507,54 +490,73 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
       }
       __syncthreads();
     }
-    __shared__ int is_last;
     if (tid == 0) {
       p.part_val[blockIdx.x] = sv[0];
       p.part_idx[blockIdx.x] = si[0];
-      __threadfence();
-      is_last = (atomicAdd(p.counter, 1) == (int)gridDim.x - 1);
+    }
+  }
+}
+
+
+// Greedy selection over the per-workgroup (value, index) partials of the
+// EPI_LOGITS head, with the same tie rule, then the step-state advance:
+// record the token, count it into the penalty history, move to the next
+// position.  For a prompt token other than the last the head computed
+// nothing and the state advances to the next prompt token.
+__global__ __launch_bounds__(1024) void k_head_final(GemvArgs p, int n_part) {
+  __shared__ float sv[1024];
+  __shared__ int si[1024];
+  __shared__ int step0, prompt_only;
+  StepState* st = p.state;
+  const int tid = threadIdx.x;
+  const int rule = p.rule;
+  if (tid == 0) {
+    step0 = st->step;
+    prompt_only = (st->step + 1 < st->n_prompt);
+  }
+  __syncthreads();
+  const int s = step0;
+  if (prompt_only) {
+    if (tid == 0) {
+      st->token = (int)p.prompt[s + 1];
+      st->pos = st->pos + 1;
+      st->step = s + 1;
+    }
+    return;
+  }
+  float v1 = -INFINITY;
+  int i1 = (rule == 0) ? -1 : 0x7fffffff;
+  for (int b = tid; b < n_part; b += 1024) {
+    float v2 = p.part_val[b];
+    int i2 = p.part_idx[b];
+    bool take = (rule == 0) ? (v2 > v1 || (v2 == v1 && i2 > i1)) : (v2 > v1 || (v2 == v1 && i2 < i1));
+    if (take) { v1 = v2; i1 = i2; }
+  }
+  sv[tid] = v1;
+  si[tid] = i1;
+  __syncthreads();
+  for (int o = 512; o > 0; o >>= 1) {
+    if (tid < o) {
+      float v2 = sv[tid + o];
+      int i2 = si[tid + o];
+      float va = sv[tid];
+      int ia = si[tid];
+      bool take = (rule == 0) ? (v2 > va || (v2 == va && i2 > ia)) : (v2 > va || (v2 == va && i2 < ia));
+      if (take) { sv[tid] = v2; si[tid] = i2; }
     }
     __syncthreads();
-    if (is_last) {
-      __threadfence();
-      float v1 = -INFINITY;
-      int i1 = (rule == 0) ? -1 : 0x7fffffff;
-      for (int b = tid; b < (int)gridDim.x; b += 256) {
-        float v2 = __hip_atomic_load(p.part_val + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        int i2 = __hip_atomic_load(p.part_idx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        bool take = (rule == 0) ? (v2 > v1 || (v2 == v1 && i2 > i1)) : (v2 > v1 || (v2 == v1 && i2 < i1));
-        if (take) { v1 = v2; i1 = i2; }
-      }
-      sv[tid] = v1;
-      si[tid] = i1;
-      __syncthreads();
-      for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) {
-          float v2 = sv[tid + o];
-          int i2 = si[tid + o];
-          float va = sv[tid];
-          int ia = si[tid];
-          bool take = (rule == 0) ? (v2 > va || (v2 == va && i2 > ia)) : (v2 > va || (v2 == va && i2 < ia));
-          if (take) { sv[tid] = v2; si[tid] = i2; }
-        }
-        __syncthreads();
-      }
-      if (tid == 0) {
-        int tok = si[0];
-        if (tok < 0 || tok >= p.n_rows) tok = 0;
-        st->argmax = tok;
-        if (st->update) {
-          int s = st->step;
-          int gen = s + 1 - st->n_prompt;           // index of this generated token
-          if (gen >= 0 && gen < p.max_out) p.out_tokens[gen] = (uint32_t)tok;
-          p.counts[tok] += 1;                        // past_tokens.push(token)
-          st->token = tok;
-          st->pos = st->pos + 1;
-          st->step = s + 1;
-        }
-        *p.counter = 0;
-        __threadfence();
-      }
+  }
+  if (tid == 0) {
+    int tok = si[0];
+    if (tok < 0 || tok >= p.n_rows) tok = 0;
+    st->argmax = tok;
+    if (st->update) {
+      int gen = s + 1 - st->n_prompt;           // index of this generated token
+      if (gen >= 0 && gen < p.max_out) p.out_tokens[gen] = (uint32_t)tok;
+      p.counts[tok] += 1;                        // past_tokens.push(token)
+      st->token = tok;
+      st->pos = st->pos + 1;
+      st->step = s + 1;
     }
   }
 }
@@ -633,12 +635,17 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
     rows_total = a.rows_per_wg;
   }
   size_t lds = hh_gemv_lds(fmt, a.K, rows_total);
+  int rc = 1;
   switch (fmt) {
-    case FMT_Q2: return launch_p<FMT_Q2>(a, pro, epi, n_wg, lds, s);
-    case FMT_Q1: return launch_p<FMT_Q1>(a, pro, epi, n_wg, lds, s);
-    case FMT_Q8: return launch_p<FMT_Q8>(a, pro, epi, n_wg, lds, s);
+    case FMT_Q2: rc = launch_p<FMT_Q2>(a, pro, epi, n_wg, lds, s); break;
+    case FMT_Q1: rc = launch_p<FMT_Q1>(a, pro, epi, n_wg, lds, s); break;
+    case FMT_Q8: rc = launch_p<FMT_Q8>(a, pro, epi, n_wg, lds, s); break;
   }
-  return 1;
+  if (rc == 0 && epi == EPI_LOGITS) {
+    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), 0, s, a, n_wg);
+    rc = hipGetLastError() == hipSuccess ? 0 : 1;
+  }
+  return rc;
 }
 
 int hh_gemv_grid(int epi, const GemvArgs& a) {
