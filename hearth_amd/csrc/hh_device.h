@@ -144,47 +144,107 @@ HH_DEV int q8_round(float x, float scale) {
   v = fminf(fmaxf(v, -128.0f), 127.0f);
   return (v != v) ? 0 : (int)v;
 }
+// q8_round with the block's reciprocal scale from v_rcp_f32 (<= 1 ulp):
+// t = x * rcp is within 2^-15.3 of the correctly rounded x / scale for
+// |x / scale| <= 127.5, so unless t lies within 2^-14 of a half-integer both
+// round to the same integer.  Near a tie, and for non-finite t, the exact
+// division decides.
+HH_DEV int q8_round_r(float x, float scale, float rcp) {
+  const float t = x * rcp;
+  const float d = fabsf(fabsf(t - truncf(t)) - 0.5f);
+  if (!(d >= 0x1p-14f)) return q8_round(x, scale);
+  return (int)fminf(fmaxf(roundf(t), -128.0f), 127.0f);
+}
+HH_DEV float q8_rcp(float scale) { return __builtin_amdgcn_rcpf(scale); }
 // q8_0.rs:35: scale = max_abs == 0 ? 1 : max_abs / 127.
 HH_DEV float q8_scale(float amax) { return amax == 0.0f ? 1.0f : amax / 127.0f; }
 
 // ---- wave helpers (wave64) ----
-HH_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-HH_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-// Sum of squares of a K-vector (K % 1024 == 0) by a 256-lane workgroup in a
-// fixed order: lane t sums its float4s x[4t + 1024k .. +3] as
-// ss + (((x0^2 + x1^2) + x2^2) + x3^2), waves reduce by butterfly, then
-// (w0 + w1) + (w2 + w3).  Every full-width RMSNorm of the path uses this order.
-HH_DEV float block_sumsq_f4(const float* __restrict__ x, int K, float* red4) {
-  const int tid = threadIdx.x;
-  float ss = 0.0f;
-  for (int e = tid * 4; e < K; e += 1024) {
-    float4 v = *(const float4*)(x + e);
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+// Butterfly reductions run with ascending offsets 1, 2, 4, ..., 32.  Before
+// the step at offset O every aligned group of O lanes holds one value, so the
+// partner across bit O can be read with cheap lane permutes instead of LDS
+// permutes: 1 and 2 are exact xor (DPP quad_perm), 4 and 8 mirror the 8- and
+// 16-lane rows (DPP row_half_mirror / row_mirror: the mirrored lane lies in
+// the partner group), 16 is a ds_swizzle xor within 32 lanes, and 32 reads
+// lanes 0 and 32.  Callers keep the whole wave active.
+template <int O> HH_DEV int bfly_xchg(int v) {
+  if constexpr (O == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (O == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (O == 4) return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  else if constexpr (O == 8) return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  else if constexpr (O == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+  else {
+    static_assert(O == 32, "offset");
+    int lo = __builtin_amdgcn_readlane(v, 0), hi = __builtin_amdgcn_readlane(v, 32);
+    return (__lane_id() < 32) ? hi : lo;
   }
-  ss = wave_sum(ss);
-  if ((tid & 63) == 0) red4[tid >> 6] = ss;
-  __syncthreads();
-  return (red4[0] + red4[1]) + (red4[2] + red4[3]);
 }
+template <int O> HH_DEV float bfly_xchg(float v) { return __int_as_float(bfly_xchg<O>(__float_as_int(v))); }
 
-// Reductions over aligned groups of W lanes (W power of two <= 64).
+// Reductions over aligned groups of W lanes (W power of two <= 64); every
+// lane of a group ends with the group's value.
+template <int W> HH_DEV float group_sum(float v) {
+  if constexpr (W > 1) v = v + bfly_xchg<1>(v);
+  if constexpr (W > 2) v = v + bfly_xchg<2>(v);
+  if constexpr (W > 4) v = v + bfly_xchg<4>(v);
+  if constexpr (W > 8) v = v + bfly_xchg<8>(v);
+  if constexpr (W > 16) v = v + bfly_xchg<16>(v);
+  if constexpr (W > 32) v = v + bfly_xchg<32>(v);
+  return v;
+}
 template <int W> HH_DEV float group_max(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  if constexpr (W > 1) v = fmaxf(v, bfly_xchg<1>(v));
+  if constexpr (W > 2) v = fmaxf(v, bfly_xchg<2>(v));
+  if constexpr (W > 4) v = fmaxf(v, bfly_xchg<4>(v));
+  if constexpr (W > 8) v = fmaxf(v, bfly_xchg<8>(v));
+  if constexpr (W > 16) v = fmaxf(v, bfly_xchg<16>(v));
+  if constexpr (W > 32) v = fmaxf(v, bfly_xchg<32>(v));
   return v;
 }
 template <int W> HH_DEV int group_sum_i(int v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if constexpr (W > 1) v += bfly_xchg<1>(v);
+  if constexpr (W > 2) v += bfly_xchg<2>(v);
+  if constexpr (W > 4) v += bfly_xchg<4>(v);
+  if constexpr (W > 8) v += bfly_xchg<8>(v);
+  if constexpr (W > 16) v += bfly_xchg<16>(v);
+  if constexpr (W > 32) v += bfly_xchg<32>(v);
   return v;
+}
+HH_DEV float wave_sum(float v) { return group_sum<64>(v); }
+HH_DEV float wave_max(float v) { return group_max<64>(v); }
+
+// Pairwise tree over 16 values (the wave sums of a 1024-slot reduction).
+HH_DEV float tree16(const float* v) {
+  float a0 = (v[0] + v[1]) + (v[2] + v[3]), a1 = (v[4] + v[5]) + (v[6] + v[7]);
+  float a2 = (v[8] + v[9]) + (v[10] + v[11]), a3 = (v[12] + v[13]) + (v[14] + v[15]);
+  return (a0 + a1) + (a2 + a3);
+}
+
+// Sum of squares of a K-vector (K % 1024 == 0) in the fixed order every
+// full-width RMSNorm of the path uses: 1024 slots, slot t summing the float4s
+// x[4t + 4096c .. +3] in c order as ss + (((x0^2 + x1^2) + x2^2) + x3^2);
+// slots 64w .. 64w+63 reduce by wave_sum into W_w; the total is tree16(W).
+// A 256-lane workgroup runs slots t, t+256, t+512, t+768 in lane t.
+// red16: 16 floats of LDS.
+HH_DEV float block_sumsq_f4(const float* __restrict__ x, int K, float* red16) {
+  const int tid = threadIdx.x;
+  float ss[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ss[j] = 0.0f;
+    for (int e = (tid + 256 * j) * 4; e < K; e += 4096) {
+      float4 v = *(const float4*)(x + e);
+      ss[j] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ss[j] = wave_sum(ss[j]);
+  if ((tid & 63) == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red16[(tid >> 6) + 4 * j] = ss[j];
+  }
+  __syncthreads();
+  return tree16(red16);
 }
 
 // ---- counter-based seeded generator (shared definition with the CPU checker) ----

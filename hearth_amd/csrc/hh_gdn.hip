@@ -29,7 +29,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
   const int n_conv_wg = conv_dim / 256;
-  __shared__ float red[8];
+  __shared__ float red[16];
   if ((int)blockIdx.x < n_conv_wg) {
     const int ch = blockIdx.x * 256 + tid;
     const int K = a.kernel;
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void k_gdn_rec(GdnArgs a) {
     if (a.out_f32) a.out_f32[(size_t)h * hd + dd] = o;
     float am = group_max<32>(fabsf(o));
     float sc = q8_scale(am);
-    int q = q8_round(o, sc);
+    int q = q8_round_r(o, sc, q8_rcp(sc));
     int qs = group_sum_i<32>(q);
     int e = h * hd + dd;
     int Kv = a.n_v * hd;

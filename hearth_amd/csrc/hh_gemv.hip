@@ -186,70 +186,87 @@ template <int FMT> HH_DEV void put_ds(float* ds, int blk32, float d, int s) {
   ((int*)ds)[t * dss<FMT>() + SUBS + sub] = s;
 }
 
-// PRO_RMSNORM: rms_norm(x, w) then Q8_0; NCH = K / 1024 float4 per lane.
-template <int NCH> struct NormRegs { float4 x[NCH], w[NCH]; };
+// A GEMV workgroup is NT = 1024 lanes (16 waves, one workgroup per CU at
+// the decode shapes): the activation prologue is the same for every
+// workgroup, so the fewer workgroups share a CU, the less of it each CU
+// repeats, and 16 waves hide its instruction latencies.
+constexpr int NT = 1024;
 
-template <int NCH> HH_DEV void norm_issue(const GemvArgs& p, NormRegs<NCH>& r) {
+// PRO_RMSNORM: rms_norm(x, w) then Q8_0.  Lane t owns the float4s at
+// 4t + 4096c (c < NORM_CH).  Sum of squares in the order of block_sumsq_f4:
+// slot t sums its float4s in c order as ss + (((x0^2 + x1^2) + x2^2) + x3^2),
+// waves reduce by butterfly, the 16 wave sums by tree16.  All prologue loads
+// precede the weight loads, so their conditions never delay a weight.
+constexpr int NORM_CH = 2;   // K <= 8192
+struct NormRegs { float4 x[NORM_CH], w[NORM_CH]; };
+
+HH_DEV void norm_issue(const GemvArgs& p, NormRegs& r) {
   const int tid = threadIdx.x;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    r.x[c] = *(const float4*)(p.x + tid * 4 + c * 1024);
-    r.w[c] = *(const float4*)(p.norm_w + tid * 4 + c * 1024);
+  for (int c = 0; c < NORM_CH; ++c) {
+    const int e = tid * 4 + c * 4096;
+    if (e < p.K) {
+      r.x[c] = *(const float4*)(p.x + e);
+      r.w[c] = *(const float4*)(p.norm_w + e);
+    }
   }
 }
 
-template <int FMT, int NCH>
-HH_DEV void norm_store(const GemvArgs& p, const NormRegs<NCH>& r, int8_t* aq, float* ds, float* red) {
+template <int FMT>
+HH_DEV void norm_store(const GemvArgs& p, const NormRegs& r, int8_t* aq, float* ds, float* red) {
   const int tid = threadIdx.x;
-  const int K = NCH * 1024;
-  // block_sumsq_f4's order: ss + (((x0^2 + x1^2) + x2^2) + x3^2) per float4
+  const int K = p.K;
   float ss = 0.0f;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c)
-    ss += r.x[c].x * r.x[c].x + r.x[c].y * r.x[c].y + r.x[c].z * r.x[c].z + r.x[c].w * r.x[c].w;
+  for (int c = 0; c < NORM_CH; ++c)
+    if (tid * 4 + c * 4096 < K)
+      ss += r.x[c].x * r.x[c].x + r.x[c].y * r.x[c].y + r.x[c].z * r.x[c].z + r.x[c].w * r.x[c].w;
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
-  float tot = (red[0] + red[1]) + (red[2] + red[3]);
-  float inv = 1.0f / sqrtf(tot / (float)K + p.eps);   // ops.rs:22-23
+  const float tot = tree16(red);
+  const float inv = 1.0f / sqrtf(tot / (float)K + p.eps);   // ops.rs:22-23
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int e = tid * 4 + c * 1024;
+  for (int c = 0; c < NORM_CH; ++c) {
+    const int e = tid * 4 + c * 4096;
+    if (c > 0 && 4096 * c >= K) break;   // uniform: whole chunk absent
+    const bool in = e < K;
     float vv[4] = {r.x[c].x * inv * r.w[c].x, r.x[c].y * inv * r.w[c].y,   // ops.rs:29 (x * inv) * w
                    r.x[c].z * inv * r.w[c].z, r.x[c].w * inv * r.w[c].w};
     float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
     am = group_max<8>(am);
-    float sc = q8_scale(am);
+    const float sc = q8_scale(am), rc = q8_rcp(sc);
     int qs = 0;
+    uint32_t word = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      int q = q8_round(vv[i], sc);
+      int q = q8_round_r(vv[i], sc, rc);
       qs += q;
-      aq[lds_qpos(FMT, e + i)] = (int8_t)q;
+      word |= ((uint32_t)q & 0xffu) << (8 * i);
     }
     qs = group_sum_i<8>(qs);
-    if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
+    if (in) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)(word >> (8 * i));
+      if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
+    }
   }
 }
 
 // PRO_PACKED: packed activation [q K][d K/32][s K/32] from a producer kernel.
-constexpr int PK_Q = 5;   // 16-byte chunks per lane: K <= 20480
-constexpr int PK_D = 3;   // blocks per lane: K/32 <= 768
-struct PackedRegs { i32x4 q[PK_Q]; float d[PK_D]; int s[PK_D]; };
+constexpr int PK_Q = 2;   // 16-byte chunks per lane: K <= 32768
+struct PackedRegs { i32x4 q[PK_Q]; float d; int s; };
 
 HH_DEV void packed_issue(const GemvArgs& p, PackedRegs& r) {
   const int tid = threadIdx.x, K = p.K;
 #pragma unroll
   for (int i = 0; i < PK_Q; ++i) {
-    int c = tid + 256 * i;
+    int c = tid + NT * i;
     if (c < K / 16) r.q[i] = *(const i32x4*)(p.act + c * 16);
   }
-  const float* gd = (const float*)(p.act + K);
-  const int* gs = (const int*)(p.act + K + (K / 32) * 4);
-#pragma unroll
-  for (int i = 0; i < PK_D; ++i) {
-    int b = tid + 256 * i;
-    if (b < K / 32) { r.d[i] = gd[b]; r.s[i] = gs[b]; }
+  if (tid < K / 32) {
+    r.d = ((const float*)(p.act + K))[tid];
+    r.s = ((const int*)(p.act + K + (K / 32) * 4))[tid];
   }
 }
 
@@ -258,28 +275,24 @@ template <int FMT> HH_DEV void packed_store(const GemvArgs& p, const PackedRegs&
   constexpr int EL = UnitT<FMT>::EL;
 #pragma unroll
   for (int i = 0; i < PK_Q; ++i) {
-    int c = tid + 256 * i;
+    int c = tid + NT * i;
     if (c < K / 16) {
       int e = c * 16;
       *(i32x4*)(aq + (e / EL) * qstride<FMT>() + (e % EL)) = r.q[i];
     }
   }
-#pragma unroll
-  for (int i = 0; i < PK_D; ++i) {
-    int b = tid + 256 * i;
-    if (b < K / 32) put_ds<FMT>(ds, b, r.d[i], r.s[i]);
-  }
+  if (tid < K / 32) put_ds<FMT>(ds, tid, r.d, r.s);
 }
 
 // PRO_STDQ8: standard Q8_0 blocks (DotFn activation format), K <= 20480.
-constexpr int SQ_C = 20;
+constexpr int SQ_C = 5;
 struct StdRegs { uint32_t q[SQ_C]; uint32_t d[SQ_C]; };
 
 HH_DEV void std_issue(const GemvArgs& p, StdRegs& r) {
   const int tid = threadIdx.x, K = p.K;
 #pragma unroll
   for (int c = 0; c < SQ_C; ++c) {
-    int e = tid * 4 + c * 1024;
+    int e = tid * 4 + c * 4 * NT;
     if (e < K) {
       const uint8_t* blk = p.act + (size_t)(e >> 5) * 34;
       const uint16_t* q16 = (const uint16_t*)(blk + 2 + (e & 31));
@@ -293,44 +306,48 @@ template <int FMT> HH_DEV void std_store(const GemvArgs& p, const StdRegs& r, in
   const int tid = threadIdx.x, K = p.K;
 #pragma unroll
   for (int c = 0; c < SQ_C; ++c) {
-    int e = tid * 4 + c * 1024;
-    if (e < K) {
-      int qs = 0;
+    int e = tid * 4 + c * 4 * NT;
+    if (c > 0 && c * 4 * NT >= K) break;   // uniform
+    int qs = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int q = (int8_t)((r.q[c] >> (8 * i)) & 0xffu);
-        qs += q;
-        aq[lds_qpos(FMT, e + i)] = (int8_t)q;
-      }
-      qs = group_sum_i<8>(qs);
+    for (int i = 0; i < 4; ++i) qs += (int)(int8_t)((r.q[c] >> (8 * i)) & 0xffu);
+    qs = group_sum_i<8>(qs);
+    if (e < K) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)((r.q[c] >> (8 * i)) & 0xffu);
       if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(r.d[c]), qs);
     }
   }
 }
 
-template <int FMT, int PRO, int NCH> struct ActStage;
-template <int FMT, int NCH> struct ActStage<FMT, PRO_RMSNORM, NCH> {
-  NormRegs<NCH> r;
-  HH_DEV void issue(const GemvArgs& p) { norm_issue<NCH>(p, r); }
-  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT, NCH>(p, r, aq, ds, red); }
+template <int FMT, int PRO> struct ActStage;
+template <int FMT> struct ActStage<FMT, PRO_RMSNORM> {
+  NormRegs r;
+  HH_DEV void issue(const GemvArgs& p) { norm_issue(p, r); }
+  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT>(p, r, aq, ds, red); }
 };
-template <int FMT, int NCH> struct ActStage<FMT, PRO_PACKED, NCH> {
+template <int FMT> struct ActStage<FMT, PRO_PACKED> {
   PackedRegs r;
   HH_DEV void issue(const GemvArgs& p) { packed_issue(p, r); }
   HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float*) { packed_store<FMT>(p, r, aq, ds); }
 };
-template <int FMT, int NCH> struct ActStage<FMT, PRO_STDQ8, NCH> {
+template <int FMT> struct ActStage<FMT, PRO_STDQ8> {
   StdRegs r;
   HH_DEV void issue(const GemvArgs& p) { std_issue(p, r); }
   HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float*) { std_store<FMT>(p, r, aq, ds); }
 };
 
-template <int FMT, int PRO, int EPI, int NCH>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
+// NU = 1, 2, 4: every lane holds at most NU units, all loaded at once before
+// the prologue (one batch).  NU = 0: larger workgroups stream batches of
+// DEPTH units per lane, double-buffered in VGPRs.  Every weight load is
+// unconditional (lanes past the last unit re-read it): a load under a branch
+// makes the compiler count it as possibly absent, and the wait for an earlier
+// load then also waits for the weight loads issued after it.
+template <int FMT, int PRO, int EPI, int NU>
+__global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   constexpr int DW = UnitT<FMT>::DW;
   constexpr int UB = UnitT<FMT>::BYTES;
-  // units per lane per batch; two batches are in flight
-  constexpr int DEPTH = (FMT == FMT_Q1) ? 4 : 2;
+  constexpr int DEPTH = NU > 0 ? NU : 2;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int K = p.K;
@@ -343,12 +360,14 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
     if (st->step + 1 < st->n_prompt) return;
   }
 
-  // rows owned by this workgroup
-  int rows_total, r0, up_base = 0;
+  // rows owned by this workgroup.  EPI_SILU: the gate rows come in blocks
+  // of 32 (one Q8_0 block of the output); workgroup g takes blocks g, g + G,
+  // ... (G = grid size), all its gate rows first, then the matching up rows.
+  int rows_total, r0 = 0, nbw = 0;
   if constexpr (EPI == EPI_SILU) {
-    rows_total = 2 * p.rows_per_wg;             // gate rows then the matching up rows
-    r0 = blockIdx.x * p.rows_per_wg;
-    up_base = p.half_rows;
+    const int nblk = p.half_rows / 32;
+    nbw = (nblk - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    rows_total = 64 * nbw;
   } else {
     r0 = blockIdx.x * p.rows_per_wg;
     rows_total = min(p.rows_per_wg, p.n_rows - r0);
@@ -363,32 +382,37 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
   // RS = rows + 1, so the row-sum pass (one lane per row) reads consecutive words
   float* part = ds + nunits_act * dss<FMT>();
   const int RS = rows_total + 1;
-  float* red = part + 2 * P * RS;
-  float* rowsum = red + 8;
+  float* red = part + 2 * P * RS;   // 16 wave partials
+  float* rowsum = red + 16;
 
   auto unit_addr = [&](int lu) -> const uint8_t* {
     int rl = lu / P, t = lu - rl * P;
     int grow;
-    if constexpr (EPI == EPI_SILU) grow = (rl < p.rows_per_wg) ? r0 + rl : up_base + r0 + (rl - p.rows_per_wg);
-    else grow = r0 + rl;
+    if constexpr (EPI == EPI_SILU) {
+      const int gl = rl < 32 * nbw ? rl : rl - 32 * nbw;   // local gate row
+      grow = ((int)blockIdx.x + (gl >> 5) * (int)gridDim.x) * 32 + (gl & 31);
+      if (rl >= 32 * nbw) grow += p.half_rows;
+    } else {
+      grow = r0 + rl;
+    }
     return p.w + ((size_t)grow * P + t) * UB;
   };
 
-  const int NI = (U + 255) / 256;
+  const int NI = (U + NT - 1) / NT;
   const int NB = (NI + DEPTH - 1) / DEPTH;
-  uint32_t wa[DEPTH][DW], wb[DEPTH][DW];
+  uint32_t wa[DEPTH][DW], wb[NU > 0 ? 1 : DEPTH][DW];
 
   auto load_batch = [&](uint32_t (&wr)[DEPTH][DW], int b) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      int lu = (b * DEPTH + d) * 256 + tid;
-      if (lu < U) load_unit<FMT>(wr[d], unit_addr(lu));
+      int lu = min((b * DEPTH + d) * NT + tid, U - 1);
+      load_unit<FMT>(wr[d], unit_addr(lu));
     }
   };
   auto comp_batch = [&](const uint32_t (&wr)[DEPTH][DW], int b) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      int lu = (b * DEPTH + d) * 256 + tid;
+      int lu = (b * DEPTH + d) * NT + tid;
       if (lu < U) {
         int rl = lu / P, t = lu - rl * P;
         float pr[2];
@@ -400,38 +424,57 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
     }
   };
 
-  ActStage<FMT, PRO, NCH> act;
+  ActStage<FMT, PRO> act;
   act.issue(p);                      // activation first (in-order retirement)
-  if (NB > 0) load_batch(wa, 0);     // then the first weight batch
-  if (NB > 1) load_batch(wb, 1);     // and the second
-  act.store(p, aq, ds, red);
-  __syncthreads();
-
-  for (int b = 0; b < NB; b += 2) {
+  if constexpr (NU > 0) {
+    load_batch(wa, 0);               // the whole share of this lane
+    act.store(p, aq, ds, red);
+    __syncthreads();
+    comp_batch(wa, 0);
+  } else {
+    load_batch(wa, 0);
+    load_batch(wb, 1);
+    act.store(p, aq, ds, red);
+    __syncthreads();
+    int b = 0;
+    for (; b + 2 < NB; b += 2) {
+      comp_batch(wa, b);
+      load_batch(wa, b + 2);
+      comp_batch(wb, b + 1);
+      load_batch(wb, b + 3);
+    }
     comp_batch(wa, b);
-    if (b + 2 < NB) load_batch(wa, b + 2);
     if (b + 1 < NB) comp_batch(wb, b + 1);
-    if (b + 3 < NB) load_batch(wb, b + 3);
   }
   __syncthreads();
 
-  // per-row sums over the block products in block order (the scalar loop)
-  for (int r = tid; r < rows_total; r += 256) {
+  // per-row sums over the block products in block order (the scalar loop);
+  // 16 products are fetched per round trip, the additions stay sequential
+  const int NPR = 2 * P;
+  for (int r = tid; r < rows_total; r += NT) {
     float s = 0.0f;
-    for (int j = 0; j < 2 * P; ++j) s += part[j * RS + r];
+    int j = 0;
+    for (; j + 16 <= NPR; j += 16) {
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = part[(j + i) * RS + r];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s += v[i];
+    }
+    for (; j < NPR; ++j) s += part[j * RS + r];
     rowsum[r] = s;
   }
   __syncthreads();
 
   if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
-    for (int r = tid; r < rows_total; r += 256) {
+    for (int r = tid; r < rows_total; r += NT) {
       if constexpr (EPI == EPI_STORE) p.y[r0 + r] = rowsum[r];
       else p.y[r0 + r] = p.y[r0 + r] + rowsum[r];
     }
   } else if constexpr (EPI == EPI_SILU) {
     // ops.rs:240-253 silu then mul_elem (mod.rs:758-763), then Q8_0 (q8_0.rs:20-51)
-    const int R2 = p.rows_per_wg;   // multiple of 32
-    for (int i0 = 0; i0 < R2; i0 += 256) {
+    const int R2 = 32 * nbw;
+    for (int i0 = 0; i0 < R2; i0 += NT) {
       int i = i0 + tid;
       float h = 0.0f;
       if (i < R2) {
@@ -441,10 +484,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
       }
       float am = group_max<32>(fabsf(h));
       float sc = q8_scale(am);
-      int q = q8_round(h, sc);
+      int q = q8_round_r(h, sc, q8_rcp(sc));
       int qs = group_sum_i<32>(q);
       if (i < R2) {
-        int e = r0 + i;
+        int e = ((int)blockIdx.x + (i >> 5) * (int)gridDim.x) * 32 + (i & 31);
         p.act_out[perm_pos(p.act_out_fmt, e)] = (uint8_t)(int8_t)q;
         if ((i & 31) == 0) {
           float* od = (float*)(p.act_out + p.act_out_k);
@@ -461,7 +504,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
     const bool do_pen = !(fabsf(pen - 1.0f) < 1e-6f);
     float bv = -INFINITY;
     int bi = (rule == 0) ? -1 : 0x7fffffff;
-    for (int r = tid; r < rows_total; r += 256) {
+    for (int r = tid; r < rows_total; r += NT) {
       float v = rowsum[r];
       int gr = r0 + r;
       if (p.y) p.y[gr] = v;
@@ -474,12 +517,12 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
       if (better) { bv = v; bi = gr; }
     }
     // workgroup reduction
-    __shared__ float sv[256];
-    __shared__ int si[256];
+    __shared__ float sv[NT];
+    __shared__ int si[NT];
     sv[tid] = bv;
     si[tid] = bi;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
+    for (int o = NT / 2; o > 0; o >>= 1) {
       if (tid < o) {
         float v2 = sv[tid + o];
         int i2 = si[tid + o];
@@ -561,39 +604,40 @@ __global__ __launch_bounds__(1024) void k_head_final(GemvArgs p, int n_part) {
   }
 }
 
-template <int FMT, int PRO, int EPI, int NCH>
+template <int FMT, int PRO, int EPI, int NU>
 int launch_t(const GemvArgs& a, int n_wg, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((k_gemv<FMT, PRO, EPI, NCH>), dim3(n_wg), dim3(256), lds, s, a);
+  hipLaunchKernelGGL((k_gemv<FMT, PRO, EPI, NU>), dim3(n_wg), dim3(NT), lds, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
-template <int FMT, int PRO, int NCH>
-int launch_e(const GemvArgs& a, int epi, int n_wg, size_t lds, hipStream_t s) {
-  switch (epi) {
-    case EPI_STORE: return launch_t<FMT, PRO, EPI_STORE, NCH>(a, n_wg, lds, s);
-    case EPI_ADD: return launch_t<FMT, PRO, EPI_ADD, NCH>(a, n_wg, lds, s);
-    case EPI_SILU: return launch_t<FMT, PRO, EPI_SILU, NCH>(a, n_wg, lds, s);
-    case EPI_LOGITS: return launch_t<FMT, PRO, EPI_LOGITS, NCH>(a, n_wg, lds, s);
+template <int FMT, int PRO, int EPI>
+int launch_u(const GemvArgs& a, int nu, int n_wg, size_t lds, hipStream_t s) {
+  switch (nu) {
+    case 1: return launch_t<FMT, PRO, EPI, 1>(a, n_wg, lds, s);
+    case 2: return launch_t<FMT, PRO, EPI, 2>(a, n_wg, lds, s);
+    case 4: return launch_t<FMT, PRO, EPI, 4>(a, n_wg, lds, s);
+    default: return launch_t<FMT, PRO, EPI, 0>(a, n_wg, lds, s);
   }
-  return 1;
 }
 
+// Prologue/epilogue pairs of the decode step (and the STDQ8 operator).
 template <int FMT>
-int launch_p(const GemvArgs& a, int pro, int epi, int n_wg, size_t lds, hipStream_t s) {
+int launch_p(const GemvArgs& a, int pro, int epi, int nu, int n_wg, size_t lds, hipStream_t s) {
   switch (pro) {
     case PRO_PACKED:
-      if (a.K > PK_Q * 4096 || a.K / 32 > PK_D * 256) return 1;
-      return launch_e<FMT, PRO_PACKED, 0>(a, epi, n_wg, lds, s);
+      if (a.K > PK_Q * 16 * NT) return 1;
+      if (epi == EPI_ADD) return launch_u<FMT, PRO_PACKED, EPI_ADD>(a, nu, n_wg, lds, s);
+      if (epi == EPI_STORE) return launch_u<FMT, PRO_PACKED, EPI_STORE>(a, nu, n_wg, lds, s);
+      return 1;
     case PRO_STDQ8:
-      if (a.K > SQ_C * 1024) return 1;
-      return launch_e<FMT, PRO_STDQ8, 0>(a, epi, n_wg, lds, s);
+      if (a.K > SQ_C * 4 * NT) return 1;
+      if (epi == EPI_STORE) return launch_u<FMT, PRO_STDQ8, EPI_STORE>(a, nu, n_wg, lds, s);
+      return 1;
     case PRO_RMSNORM:
-      switch (a.K) {   // NCH = K / 1024 float4 per lane
-        case 1024: return launch_e<FMT, PRO_RMSNORM, 1>(a, epi, n_wg, lds, s);
-        case 2048: return launch_e<FMT, PRO_RMSNORM, 2>(a, epi, n_wg, lds, s);
-        case 4096: return launch_e<FMT, PRO_RMSNORM, 4>(a, epi, n_wg, lds, s);
-        case 5120: return launch_e<FMT, PRO_RMSNORM, 5>(a, epi, n_wg, lds, s);
-      }
+      if (a.K % 1024 != 0 || a.K > NORM_CH * 4 * NT) return 1;
+      if (epi == EPI_STORE) return launch_u<FMT, PRO_RMSNORM, EPI_STORE>(a, nu, n_wg, lds, s);
+      if (epi == EPI_SILU) return launch_u<FMT, PRO_RMSNORM, EPI_SILU>(a, nu, n_wg, lds, s);
+      if (epi == EPI_LOGITS) return launch_u<FMT, PRO_RMSNORM, EPI_LOGITS>(a, nu, n_wg, lds, s);
       return 1;
   }
   return 1;
@@ -618,7 +662,7 @@ size_t hh_gemv_lds(int fmt, int K, int rows_total_per_wg) {
   int P = K / el;
   size_t qb = (size_t)(K / el) * (el + 16);
   size_t dsb = (size_t)(K / el) * (fmt == FMT_Q8 ? 8 : 20) * 4;
-  size_t b = qb + dsb + (size_t)(rows_total_per_wg + 1) * P * 8 + 8 * 4 + (size_t)rows_total_per_wg * 4;
+  size_t b = qb + dsb + (size_t)(rows_total_per_wg + 1) * P * 8 + 16 * 4 + (size_t)rows_total_per_wg * 4;
   return (b + 15) & ~(size_t)15;
 }
 
@@ -628,18 +672,22 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   a.P = a.K / el;
   int n_wg, rows_total;
   if (epi == EPI_SILU) {
-    n_wg = a.half_rows / a.rows_per_wg;
-    rows_total = 2 * a.rows_per_wg;
+    if (a.half_rows % 32 != 0) return 1;
+    const int nblk = a.half_rows / 32;
+    n_wg = std::min(nblk, 256);
+    rows_total = 64 * ((nblk + n_wg - 1) / n_wg);   // the largest share
   } else {
     n_wg = (a.n_rows + a.rows_per_wg - 1) / a.rows_per_wg;
     rows_total = a.rows_per_wg;
   }
   size_t lds = hh_gemv_lds(fmt, a.K, rows_total);
+  const int ni = (rows_total * a.P + NT - 1) / NT;   // units per lane
+  const int nu = ni <= 1 ? 1 : ni <= 2 ? 2 : ni <= 4 ? 4 : 0;
   int rc = 1;
   switch (fmt) {
-    case FMT_Q2: rc = launch_p<FMT_Q2>(a, pro, epi, n_wg, lds, s); break;
-    case FMT_Q1: rc = launch_p<FMT_Q1>(a, pro, epi, n_wg, lds, s); break;
-    case FMT_Q8: rc = launch_p<FMT_Q8>(a, pro, epi, n_wg, lds, s); break;
+    case FMT_Q2: rc = launch_p<FMT_Q2>(a, pro, epi, nu, n_wg, lds, s); break;
+    case FMT_Q1: rc = launch_p<FMT_Q1>(a, pro, epi, nu, n_wg, lds, s); break;
+    case FMT_Q8: rc = launch_p<FMT_Q8>(a, pro, epi, nu, n_wg, lds, s); break;
   }
   if (rc == 0 && epi == EPI_LOGITS) {
     hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), 0, s, a, n_wg);
@@ -649,6 +697,6 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
 }
 
 int hh_gemv_grid(int epi, const GemvArgs& a) {
-  if (epi == EPI_SILU) return a.half_rows / a.rows_per_wg;
+  if (epi == EPI_SILU) return std::min(a.half_rows / 32, 256);
   return (a.n_rows + a.rows_per_wg - 1) / a.rows_per_wg;
 }

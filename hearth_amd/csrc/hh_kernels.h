@@ -8,7 +8,7 @@ struct GemvArgs {
   int n_rows;           // rows (EPI_SILU: unused; half_rows gives the gate count)
   int K;                // n_cols
   int P;                // units per row (set by the launcher)
-  int rows_per_wg;      // rows per workgroup (EPI_SILU: gate rows per workgroup)
+  int rows_per_wg;      // rows per workgroup (EPI_SILU: unused, blocks of 32 gate rows)
   int half_rows;        // EPI_SILU: row offset of the up half
   // prologue inputs
   const float* x;       // PRO_RMSNORM: f32 vector

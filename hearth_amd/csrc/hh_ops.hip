@@ -20,7 +20,7 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, i
   float v = idx < n ? x[idx] : 0.0f;
   float am = group_max<32>(fabsf(v));
   float sc = q8_scale(am);
-  int q = idx < n ? q8_round(v, sc) : 0;
+  int q = idx < n ? q8_round_r(v, sc, q8_rcp(sc)) : 0;
   uint8_t* o = out + b * 34;
   o[2 + lane] = (uint8_t)(int8_t)q;
   if (lane == 0) {
@@ -124,34 +124,37 @@ __global__ __launch_bounds__(256) void k_embed(int type, const uint8_t* __restri
 // (max-rescaled sums), applies the qwen35 gate, and emits the packed Q8_0
 // input of attn_output.
 // ---------------------------------------------------------------------------
-HH_DEV void head_norm_rope(float* v, int hd, const float* nw, float eps, const float* rope, int rope_dim,
-                           int max_seq, int pos, int lane, float* tmp_pair) {
-  // v: LDS vector of hd floats, processed by one wave
-  if (nw) {
-    float ss = 0.0f;
-    for (int d = lane; d < hd; d += 64) ss += v[d] * v[d];
-    ss = wave_sum(ss);
-    float inv = 1.0f / sqrtf(ss / (float)hd + eps);
-    for (int d = lane; d < hd; d += 64) v[d] = v[d] * inv * nw[d];
+// A lane's float4 column slice x[4c .. 4c+3] of one head (c < LPR = HD/4;
+// every LPR-lane group holds the whole head).  Per-head RMSNorm
+// (mod.rs:551-578): ss_c = ((x0^2 + x1^2) + x2^2) + x3^2, summed over the
+// group by an ascending butterfly; out = (x * inv) * w.  NeoX RoPE on the
+// first rope_dim dims (ops.rs:140-164): the partner element i +- rope_dim/2
+// sits rope_dim/8 lanes away.
+template <int LPR>
+HH_DEV float4 slice_norm(float4 x, float4 w, float eps) {
+  float ss = x.x * x.x + x.y * x.y;
+  ss = ss + x.z * x.z;
+  ss = ss + x.w * x.w;
+  ss = group_sum<LPR>(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)(4 * LPR) + eps);
+  return make_float4(x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w);
+}
+
+// sn/cs: sin/cos of the slice's rotation index (c4 mod half); lanes with
+// 4c >= rope_dim keep x.
+HH_DEV float4 slice_rope(float4 x, float4 sn, float4 cs, int c4, int rope_dim) {
+  const int half = rope_dim / 2, X = half / 4;
+  float4 y;   // partner slice (all lanes exchange; the wave stays converged)
+  y.x = __shfl_xor(x.x, X, 64); y.y = __shfl_xor(x.y, X, 64);
+  y.z = __shfl_xor(x.z, X, 64); y.w = __shfl_xor(x.w, X, 64);
+  if (c4 < half) {          // x0 = x, x1 = partner: x0*cos - x1*sin
+    return make_float4(x.x * cs.x - y.x * sn.x, x.y * cs.y - y.y * sn.y,
+                       x.z * cs.z - y.z * sn.z, x.w * cs.w - y.w * sn.w);
+  } else if (c4 < rope_dim) {   // x0 = partner, x1 = x: x0*sin + x1*cos
+    return make_float4(y.x * sn.x + x.x * cs.x, y.y * sn.y + x.y * cs.y,
+                       y.z * sn.z + x.z * cs.z, y.w * sn.w + x.w * cs.w);
   }
-  if (rope) {
-    int half = rope_dim / 2;
-    const float* base = rope + (size_t)(pos % max_seq) * half * 2;
-    float r0[4], r1[4];
-    int cnt = 0;
-    for (int i = lane; i < half; i += 64, ++cnt) {
-      float s = base[i], c = base[half + i];
-      float x0 = v[i], x1 = v[i + half];
-      r0[cnt] = x0 * c - x1 * s;
-      r1[cnt] = x0 * s + x1 * c;
-    }
-    cnt = 0;
-    for (int i = lane; i < half; i += 64, ++cnt) {
-      v[i] = r0[cnt];
-      v[i + half] = r1[cnt];
-    }
-  }
-  (void)tmp_pair;
+  return x;
 }
 
 // Butterfly sum of NV values held by each lane of an aligned LPR-lane group,
@@ -182,19 +185,31 @@ template <int N, int O> struct ReduceScatter {
 };
 
 // Split kernel: workgroup (s, kvh) owns positions [s*C, s*C + C) of kv head
-// kvh for its G query heads.  Thread t holds one float4 column slice
-// (c = t % LPR) of rows j = i*RPI + t/LPR, i < 8, of K and V in registers,
-// so the chunk is read from HBM exactly once and never staged through LDS.
+// kvh (C = 8192/hd) for its G query heads, with ATTN_NT lanes.  Thread t
+// holds one float4 column slice (c = t % LPR) of rows j = i*RPI + t/LPR,
+// i < NR, of K and V in registers, so the chunk is read from HBM exactly
+// once and never staged through LDS.
 //  * score(h, j) = (butterfly over the LPR lanes of the row of the 4-term
 //    fma chain q.k) * 1/sqrt(hd)
 //  * e = exp(score - m), m and l = sum e by a 64-lane butterfly
 //  * o(h, d): per row group `sub` an fma chain over i; hd 128: the two row
-//    groups of a wave are added, then waves as (w0 + w1) + (w2 + w3);
-//    hd 256: (w0 + w1) + (w2 + w3) directly.
+//    groups of a wave are added; then the NW wave values by pairwise_tree.
 // Writes the unnormalised partial o and (m, l) of every (split, head).
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
-  constexpr int LPR = HD / 4, RPI = 256 / LPR, C = RPI * 8;
+constexpr int ATTN_NT = 512;
+
+// ((v0 + v1) + (v2 + v3)) + ... over N = 2^k values.
+template <int N> HH_DEV float pairwise_tree(float* t) {
+#pragma unroll
+  for (int w = N; w > 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w / 2; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+  return t[0];
+}
+
+template <int HD, int NTA>
+__global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
+  constexpr int LPR = HD / 4, RPI = NTA / LPR, C = 8192 / HD, NR = C / RPI, NW = NTA / 64;
+  static_assert(NR * RPI == C && NR >= 1, "geometry");
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int s = blockIdx.x, kvh = blockIdx.y;
@@ -211,20 +226,46 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   const int p0 = s * C, np = min(C, seq - p0);
   const bool has_new = prep && pos >= p0 && pos < p0 + np;
   const int sub = tid / LPR, c = tid % LPR;
-  float* qs = sm;                 // G*HD
-  float* kn = qs + G * HD;        // HD
-  float* vn = kn + HD;            // HD
-  float* sc = vn + HD;            // G*C
+  float* sc = sm;                 // G*C
   float* ml = sc + G * C;         // 2*G (+pad)
-  float* red = ml + 2 * G + 4;    // 4 waves * 4 heads * HD
+  float* red = ml + 2 * G + 4;    // NW waves * 4 heads * HD
   const size_t hstride = (size_t)a.max_seq * HD;
   const float* kg = a.k_cache + (size_t)kvh * hstride + 4 * c;
   const float* vg = a.v_cache + (size_t)kvh * hstride + 4 * c;
 
-  // 1. issue this chunk's K/V loads
-  float4 kr[8], vr[8];
+  // 1. the small loads first (vector loads return in issue order): this
+  // lane's slice of every q head and of the new k/v, the norm weights and the
+  // RoPE row
+  constexpr int GMAX = 8;
+  float4 q4[GMAX], kn4 = make_float4(0.f, 0.f, 0.f, 0.f), vn4 = kn4;
+  float4 nq4 = kn4, nk4 = kn4, sn4 = kn4, cs4 = kn4;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int h = 0; h < GMAX; ++h) {
+    q4[h] = kn4;
+    if (h < G) {
+      const int qh = kvh * G + h;
+      q4[h] = *(const float4*)(a.qkv + (a.gated ? (size_t)qh * 2 * HD : (size_t)qh * HD) + 4 * c);
+    }
+  }
+  if (has_new) {
+    kn4 = *(const float4*)(a.qkv + a.q_stride_heads + (size_t)kvh * HD + 4 * c);
+    vn4 = *(const float4*)(a.qkv + a.q_stride_heads + (size_t)a.n_kv * HD + (size_t)kvh * HD + 4 * c);
+  }
+  if (prep) {
+    if (a.q_norm) nq4 = *(const float4*)(a.q_norm + 4 * c);
+    if (a.k_norm) nk4 = *(const float4*)(a.k_norm + 4 * c);
+    if (a.rope && 4 * c < a.rope_dim) {
+      const int half = a.rope_dim / 2, ib = (4 * c < half) ? 4 * c : 4 * c - half;
+      const float* base = a.rope + (size_t)(pos % a.max_seq) * half * 2;
+      sn4 = *(const float4*)(base + ib);
+      cs4 = *(const float4*)(base + half + ib);
+    }
+  }
+
+  // 2. this chunk's K/V
+  float4 kr[NR], vr[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
     const int j = i * RPI + sub;
     kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     vr[i] = kr[i];
@@ -233,63 +274,57 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
     }
   }
-  // 2. q heads (and the new k/v): raw -> LDS, then norm + rope, one wave per head
-  for (int h = 0; h < G; ++h) {
-    const int qh = kvh * G + h;
-    const float* src = a.qkv + (a.gated ? (size_t)qh * 2 * HD : (size_t)qh * HD);
-    for (int d = tid; d < HD; d += 256) qs[h * HD + d] = src[d];
-  }
-  if (has_new) {
-    const float* ksrc = a.qkv + a.q_stride_heads + (size_t)kvh * HD;
-    const float* vsrc = a.qkv + a.q_stride_heads + (size_t)a.n_kv * HD + (size_t)kvh * HD;
-    for (int d = tid; d < HD; d += 256) { kn[d] = ksrc[d]; vn[d] = vsrc[d]; }
-  }
-  __syncthreads();
+  // 3. q heads and the new k: per-head norm + rope on the lane's slice
   if (prep) {
-    for (int h = wid; h < G; h += 4)
-      head_norm_rope(qs + h * HD, HD, a.q_norm, a.eps, a.rope, a.rope_dim, a.max_seq, pos, lane, nullptr);
-    if (has_new && wid == (G % 4))
-      head_norm_rope(kn, HD, a.k_norm, a.eps, a.rope, a.rope_dim, a.max_seq, pos, lane, nullptr);
-  }
-  __syncthreads();
-  if (has_new) {   // kvcache.rs:92-113 write_kv
-    float* kdst = a.k_cache + (size_t)kvh * hstride + (size_t)pos * HD;
-    float* vdst = a.v_cache + (size_t)kvh * hstride + (size_t)pos * HD;
-    for (int d = tid; d < HD; d += 256) { kdst[d] = kn[d]; vdst[d] = vn[d]; }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (p0 + i * RPI + sub == pos) {
-        kr[i] = *(const float4*)(kn + 4 * c);
-        vr[i] = *(const float4*)(vn + 4 * c);
+    for (int h = 0; h < GMAX; ++h) {
+      if (h < G) {
+        if (a.q_norm) q4[h] = slice_norm<LPR>(q4[h], nq4, a.eps);
+        if (a.rope) q4[h] = slice_rope(q4[h], sn4, cs4, 4 * c, a.rope_dim);
+      }
+    }
+    if (has_new) {   // uniform over the workgroup
+      if (a.k_norm) kn4 = slice_norm<LPR>(kn4, nk4, a.eps);
+      if (a.rope) kn4 = slice_rope(kn4, sn4, cs4, 4 * c, a.rope_dim);
+      // kvcache.rs:92-113 write_kv, then the row joins this chunk
+      if (sub == 0) {
+        *(float4*)(a.k_cache + (size_t)kvh * hstride + (size_t)pos * HD + 4 * c) = kn4;
+        *(float4*)(a.v_cache + (size_t)kvh * hstride + (size_t)pos * HD + 4 * c) = vn4;
+      }
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        if (p0 + i * RPI + sub == pos) { kr[i] = kn4; vr[i] = vn4; }
       }
     }
   }
-  // 3. scores (ops.rs:362-374), four heads per pass
+  // 4. scores (ops.rs:362-374), four heads per pass
   const float inv_sqrt = 1.0f / sqrtf((float)HD);
-  constexpr int KSH = (LPR == 64) ? 1 : 0;
-  for (int hg = 0; hg < G; hg += 4) {
-    float v[32];
+  constexpr int NV = 4 * NR;                          // values per lane per pass
+  constexpr int KSH = (LPR == 64 ? 6 : 5) - (NV == 32 ? 5 : NV == 16 ? 4 : 3);   // log2(LPR / NV)
+#pragma unroll
+  for (int hg = 0; hg < GMAX; hg += 4) {
+    if (hg >= G) break;
+    float v[NV];
 #pragma unroll
     for (int hh = 0; hh < 4; ++hh) {
-      float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (hg + hh < G) q4 = *(const float4*)(qs + (hg + hh) * HD + 4 * c);
+      const float4 qq = q4[hg + hh];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float p = q4.x * kr[i].x;
-        p = fmaf(q4.y, kr[i].y, p);
-        p = fmaf(q4.z, kr[i].z, p);
-        p = fmaf(q4.w, kr[i].w, p);
-        v[hh * 8 + i] = p;
+      for (int i = 0; i < NR; ++i) {
+        float p = qq.x * kr[i].x;
+        p = fmaf(qq.y, kr[i].y, p);
+        p = fmaf(qq.z, kr[i].z, p);
+        p = fmaf(qq.w, kr[i].w, p);
+        v[hh * NR + i] = p;
       }
     }
-    const float r = ReduceScatter<32, LPR / 2>::run(v, lane);
+    const float r = ReduceScatter<NV, LPR / 2>::run(v, lane);
     const int k = (lane & (LPR - 1)) >> KSH;
-    const int h = hg + (k >> 3), j = (k & 7) * RPI + sub;
-    if (h < G && (KSH == 0 || (lane & 1) == 0)) sc[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
+    const int h = hg + k / NR, j = (k % NR) * RPI + sub;
+    if (h < G && (lane & ((1 << KSH) - 1)) == 0) sc[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
   }
   __syncthreads();
-  // 4. per-head softmax statistics over the chunk (C <= 64)
-  for (int h = wid; h < G; h += 4) {
+  // 5. per-head softmax statistics over the chunk (C <= 64)
+  for (int h = wid; h < G; h += NW) {
     float x = lane < C ? sc[h * C + lane] : -INFINITY;
     float m = wave_max(x);
     float e = (lane < np) ? hx_exp(x - m) : 0.0f;
@@ -298,7 +333,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
     if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
   }
   __syncthreads();
-  // 5. o = sum_j e_j v_j
+  // 6. o = sum_j e_j v_j
   const size_t pbase = ((size_t)kvh * a.max_splits + s) * G;
   for (int hg = 0; hg < G; hg += 4) {
     float acc[16];
@@ -308,7 +343,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       if (hg + hh < G) {
         const float* eh = sc + (hg + hh) * C + sub;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NR; ++i) {
           const float e = eh[i * RPI];
           o0 = fmaf(e, vr[i].x, o0);
           o1 = fmaf(e, vr[i].y, o1);
@@ -334,11 +369,13 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       for (int k = 0; k < 16; ++k) red[(wid * 4 + (k >> 2)) * HD + 4 * c + (k & 3)] = acc[k];
     }
     __syncthreads();
-    for (int idx = tid; idx < 4 * HD; idx += 256) {
+    for (int idx = tid; idx < 4 * HD; idx += NTA) {
       const int h = hg + idx / HD;
       if (h < G) {
-        float o = (red[idx] + red[4 * HD + idx]) + (red[8 * HD + idx] + red[12 * HD + idx]);
-        a.part_o[(pbase + h) * HD + (idx % HD)] = o;
+        float t[NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) t[w] = red[w * 4 * HD + idx];
+        a.part_o[(pbase + h) * HD + (idx % HD)] = pairwise_tree<NW>(t);
       }
     }
     __syncthreads();
@@ -417,7 +454,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   if (a.act_out) {
     float am = group_max<32>(fabsf(o));
     float scq = q8_scale(am);
-    int q = q8_round(o, scq);
+    int q = q8_round_r(o, scq, q8_rcp(scq));
     int qsum = group_sum_i<32>(q);
     int e = qh * HD + d;
     int K = a.n_heads * HD;
@@ -619,14 +656,14 @@ int hh_embed_launch(int type, const uint8_t* table, int d, const StepState* st, 
 int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
   const int G = a.n_heads / a.n_kv;
   if (a.hd != 128 && a.hd != 256) return 1;
-  if (a.chunk != 8192 / a.hd || a.n_kv * G != a.n_heads) return 1;
-  const size_t split_lds = 4 * ((size_t)G * a.hd + 2 * (size_t)a.hd + (size_t)G * a.chunk + 2 * G + 4 + 16 * (size_t)a.hd);
+  if (a.chunk != 8192 / a.hd || a.n_kv * G != a.n_heads || G > 8) return 1;
+  const size_t split_lds = 4 * ((size_t)G * a.chunk + 2 * G + 4 + (ATTN_NT / 64) * 4 * (size_t)a.hd);
   const size_t merge_lds = 4 * ((size_t)a.max_splits + 256 + 4);
   if (a.hd == 128) {
-    hipLaunchKernelGGL(k_attn_split<128>, dim3(a.max_splits, a.n_kv), dim3(256), split_lds, s, a);
+    hipLaunchKernelGGL((k_attn_split<128, ATTN_NT>), dim3(a.max_splits, a.n_kv), dim3(ATTN_NT), split_lds, s, a);
     hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_heads, 2), dim3(256), merge_lds, s, a);
   } else {
-    hipLaunchKernelGGL(k_attn_split<256>, dim3(a.max_splits, a.n_kv), dim3(256), split_lds, s, a);
+    hipLaunchKernelGGL((k_attn_split<256, ATTN_NT>), dim3(a.max_splits, a.n_kv), dim3(ATTN_NT), split_lds, s, a);
     hipLaunchKernelGGL(k_attn_merge<256>, dim3(a.n_heads, 4), dim3(256), merge_lds, s, a);
   }
   return ok();

@@ -225,13 +225,13 @@ void declare(hh_model* m) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Rows per GEMV workgroup: about 512 units (1-2 per lane) per workgroup, halved
-// until the launch has at least 512 workgroups (2 per CU) or one row each.
+// Rows per GEMV workgroup (1024 lanes): enough for one workgroup per CU
+// (256), capped so the transposed block products part[2P x (rows+1)] stay
+// within 64 KB of LDS.
 int gemv_rows_for(int n_rows, int P) {
-  int rows = 1;
-  while (rows * 2 * P <= 512 && rows < 64) rows *= 2;
-  while (rows > 1 && (n_rows + rows - 1) / rows < 512) rows /= 2;
-  return rows;
+  int rows = (n_rows + 255) / 256;
+  int cap = std::max(1, (64 * 1024) / (8 * P) - 1);
+  return std::max(1, std::min(rows, cap));
 }
 
 int enqueue_step(hh_model* m, hipStream_t s, int only_layer = -1, unsigned stages = ~0u);
@@ -718,6 +718,16 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   m->attn_chunk = 8192 / hd;
   m->attn_splits = (c.max_seq + m->attn_chunk - 1) / m->attn_chunk;
   int G = c.n_heads / c.n_kv_heads;
+  // launch geometry of the GEMVs
+  {
+    int el = hh_unit_el(wf);
+    int n_in_max = std::max((c.attn_out_gate ? 2 : 1) * nq + 2 * nkv, c.arch == 1 ? conv_dim + vdim : 0);
+    m->rows_in = gemv_rows_for(n_in_max, c.d_model / el);
+    m->rows_gu = 32;
+    m->rows_out = gemv_rows_for(c.d_model, std::max(nq, vdim) / el);
+    m->rows_down = gemv_rows_for(c.d_model, c.d_ffn / el);
+    m->rows_head = gemv_rows_for(c.vocab, c.d_model / hh_unit_el(hh_fmt_of(c.head_type)));
+  }
   int head_wg = (c.vocab + m->rows_head - 1) / m->rows_head;
   m->max_out = c.max_seq + 8;
   HIP_TRY(hipMalloc(&m->hidden, sizeof(float) * c.d_model));
@@ -740,16 +750,6 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   HIP_TRY(hipMemset(m->state, 0, sizeof(StepState)));
   HIP_TRY(hipEventCreate(&m->ev0));
   HIP_TRY(hipEventCreate(&m->ev1));
-  // launch geometry: ~256-1024 units of work per workgroup
-  {
-    int el = hh_unit_el(wf);
-    int n_in_max = std::max((c.attn_out_gate ? 2 : 1) * nq + 2 * nkv, c.arch == 1 ? conv_dim + vdim : 0);
-    m->rows_in = gemv_rows_for(n_in_max, c.d_model / el);
-    m->rows_gu = 32;
-    m->rows_out = gemv_rows_for(c.d_model, std::max(nq, vdim) / el);
-    m->rows_down = gemv_rows_for(c.d_model, c.d_ffn / el);
-    m->rows_head = 64;
-  }
   HIP_TRY(hipDeviceSynchronize());
   int rc = capture(m);
   if (rc) { std::string msg = g_err; hh_model_destroy(m); return fail(rc, "graph capture: " + msg); }

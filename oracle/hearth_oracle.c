@@ -694,13 +694,15 @@ void ho_synth_tensor(int type, uint64_t seed, const char* name, int64_t rows, in
 /* The same mathematics as the reference-order functions above, with the fp32
  * additions grouped as the HIP kernels group them, so the two implementations
  * can be compared bit for bit.  Wave reductions are butterflies over 64 lanes
- * (lane i adds lane i^o for o = 32..1); the 256-lane vector sum of squares is
- * lane-strided float4 partials, per-wave butterflies, then (w0+w1)+(w2+w3). */
+ * (lane i adds lane i^o for o = 1..32); the vector sum of squares is 1024
+ * slot-strided float4 partials, per-wave butterflies, then a 16-way pairwise
+ * tree. */
 
 static float bfly64(const float* v) {
+  /* the device's wave_sum: butterfly with ascending offsets 1, 2, ..., 32 */
   float a[64], b[64];
   memcpy(a, v, sizeof a);
-  for (int o = 32; o > 0; o >>= 1) {
+  for (int o = 1; o < 64; o <<= 1) {
     for (int i = 0; i < 64; i++) b[i] = a[i] + a[i ^ o];
     memcpy(a, b, sizeof a);
   }
@@ -708,10 +710,12 @@ static float bfly64(const float* v) {
 }
 
 static float dev_sumsq_block(const float* x, int64_t K) {
-  float lanes[256], w[4];
-  for (int t = 0; t < 256; t++) {
+  /* 1024 slots: slot t sums the float4s at 4t + 4096c in c order; slots
+   * 64w..64w+63 butterfly into W_w; the 16 W_w add as a pairwise tree. */
+  float lanes[1024], w[16];
+  for (int t = 0; t < 1024; t++) {
     float ss = 0.0f;
-    for (int64_t e = 4 * t; e < K; e += 1024) {
+    for (int64_t e = 4 * t; e < K; e += 4096) {
       float q = x[e] * x[e] + x[e + 1] * x[e + 1];
       q = q + x[e + 2] * x[e + 2];
       q = q + x[e + 3] * x[e + 3];
@@ -719,8 +723,10 @@ static float dev_sumsq_block(const float* x, int64_t K) {
     }
     lanes[t] = ss;
   }
-  for (int k = 0; k < 4; k++) w[k] = bfly64(lanes + 64 * k);
-  return (w[0] + w[1]) + (w[2] + w[3]);
+  for (int k = 0; k < 16; k++) w[k] = bfly64(lanes + 64 * k);
+  float a0 = (w[0] + w[1]) + (w[2] + w[3]), a1 = (w[4] + w[5]) + (w[6] + w[7]);
+  float a2 = (w[8] + w[9]) + (w[10] + w[11]), a3 = (w[12] + w[13]) + (w[14] + w[15]);
+  return (a0 + a1) + (a2 + a3);
 }
 
 static void dev_rms_norm_block(const float* x, const float* w, float eps, int64_t K, float* out) {
@@ -743,6 +749,25 @@ static void dev_rms_norm_wave(const float* x, const float* w, float eps, int n, 
   for (int i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
 }
 
+/* Attention head RMSNorm as the split kernel computes it on hd/4 lanes, each
+ * holding a float4 slice: ss_c = ((x0^2 + x1^2) + x2^2) + x3^2, then an
+ * ascending butterfly over the hd/4 lanes. */
+static void dev_rms_norm_slices(const float* x, const float* w, float eps, int n, float* out) {
+  float a[64], b[64];
+  const int L = n / 4;
+  for (int c = 0; c < L; c++) {
+    float q = x[4 * c] * x[4 * c] + x[4 * c + 1] * x[4 * c + 1];
+    q = q + x[4 * c + 2] * x[4 * c + 2];
+    a[c] = q + x[4 * c + 3] * x[4 * c + 3];
+  }
+  for (int o = 1; o < L; o <<= 1) {
+    for (int i = 0; i < L; i++) b[i] = a[i] + a[i ^ o];
+    memcpy(a, b, sizeof(float) * (size_t)L);
+  }
+  float inv = 1.0f / sqrtf(a[0] / (float)n + eps);
+  for (int i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+}
+
 /* Split-sequence attention for one query head: chunks of C = 8192/hd positions,
  * per chunk max / exp / butterfly sum / sequential fma of p*v, then the chunks
  * merged with exp(m_s - M) weights. */
@@ -757,6 +782,9 @@ static float bfly_n(const float* v, int n) {
   return a[0];
 }
 
+/* Lanes per workgroup of the device's attention split kernel (ATTN_NT). */
+#define DEV_ATTN_NT 512
+
 /* Split-sequence attention in the device's grouping: chunks of C = 8192/hd
  * positions; a score is the butterfly over hd/4 column slices of a 4-term
  * fma chain; the chunk's o is summed per row group (rows i*RPI + sub) as an
@@ -765,7 +793,8 @@ static float bfly_n(const float* v, int n) {
  * reference computes the same softmax-weighted sum in one pass
  * (ops.rs:353-406). */
 static void dev_attention(const float* q, const float* k, const float* v, int seq, int hd, float* out) {
-  const int C = 8192 / hd, LPR = hd / 4, RPI = 256 / LPR, ns = (seq + C - 1) / C;
+  const int C = 8192 / hd, LPR = hd / 4, RPI = DEV_ATTN_NT / LPR, NR = C / RPI, NW = DEV_ATTN_NT / 64;
+  const int ns = (seq + C - 1) / C;
   float inv_sqrt = 1.0f / sqrtf((float)hd);
   float* ms = (float*)malloc(sizeof(float) * (size_t)ns * (hd + 3));
   float* ls = ms + ns;
@@ -792,23 +821,19 @@ static void dev_attention(const float* q, const float* k, const float* v, int se
     ms[s] = m;
     ls[s] = bfly64(e);
     for (int d = 0; d < hd; d++) {
-      float A[8] = {0};
+      float A[64] = {0}, X[32];
       for (int sub = 0; sub < RPI; sub++) {
         float acc = 0.0f;
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < NR; i++) {
           int j = i * RPI + sub;
           if (j < np) acc = fmaf(e[j], v[(size_t)(p0 + j) * hd + d], acc);
         }
         A[sub] = acc;
       }
-      float o;
-      if (RPI == 8) {
-        float X0 = A[0] + A[1], X1 = A[2] + A[3], X2 = A[4] + A[5], X3 = A[6] + A[7];
-        o = (X0 + X1) + (X2 + X3);
-      } else {
-        o = (A[0] + A[1]) + (A[2] + A[3]);
-      }
-      os[(size_t)s * hd + d] = o;
+      for (int w = 0; w < NW; w++) X[w] = (LPR == 32) ? A[2 * w] + A[2 * w + 1] : A[w];
+      for (int w = NW; w > 1; w >>= 1)
+        for (int i = 0; i < w / 2; i++) X[i] = X[2 * i] + X[2 * i + 1];
+      os[(size_t)s * hd + d] = X[0];
     }
   }
   float M = -INFINITY;
@@ -1092,6 +1117,10 @@ static void norm_head(const ho_model* m, const float* x, const float* w, int n, 
   if (m->order) dev_rms_norm_wave(x, w, m->cfg.eps, n, out);
   else ho_rms_norm(x, w, m->cfg.eps, n, out);
 }
+static void norm_head_attn(const ho_model* m, const float* x, const float* w, int n, float* out) {
+  if (m->order) dev_rms_norm_slices(x, w, m->cfg.eps, n, out);
+  else ho_rms_norm(x, w, m->cfg.eps, n, out);
+}
 
 void ho_model_set_threads(ho_model* m, int n_threads, int arm) {
   m->n_threads = n_threads < 1 ? 1 : n_threads;
@@ -1127,13 +1156,13 @@ static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
     if (ly->attn_q_norm) {
       for (int h = 0; h < nh; h++) {
         memcpy(m->tmp, m->q + h * hd, sizeof(float) * hd);
-        norm_head(m, m->tmp, (const float*)ly->attn_q_norm->data, hd, m->q + h * hd);
+        norm_head_attn(m, m->tmp, (const float*)ly->attn_q_norm->data, hd, m->q + h * hd);
       }
     }
     if (ly->attn_k_norm) {
       for (int h = 0; h < nkvh; h++) {
         memcpy(m->tmp, m->k + h * hd, sizeof(float) * hd);
-        norm_head(m, m->tmp, (const float*)ly->attn_k_norm->data, hd, m->k + h * hd);
+        norm_head_attn(m, m->tmp, (const float*)ly->attn_k_norm->data, hd, m->k + h * hd);
       }
     }
     for (int h = 0; h < nh; h++) ho_rope_apply(m->rope, c->max_seq, m->rope_dim, m->q + h * hd, pos);
@@ -1316,11 +1345,11 @@ static void attn_layer_q35(ho_model* m, int pos, layer_t* ly) {
     memmove(m->q + h * hd, qg + (size_t)h * 2 * hd, sizeof(float) * hd);
   }
   for (int h = 0; h < nh; h++) {
-    norm_head(m, m->q + h * hd, (const float*)ly->attn_q_norm->data, hd, m->tmp);
+    norm_head_attn(m, m->q + h * hd, (const float*)ly->attn_q_norm->data, hd, m->tmp);
     memcpy(m->q + h * hd, m->tmp, sizeof(float) * hd);
   }
   for (int h = 0; h < nkvh; h++) {
-    norm_head(m, m->k + h * hd, (const float*)ly->attn_k_norm->data, hd, m->tmp);
+    norm_head_attn(m, m->k + h * hd, (const float*)ly->attn_k_norm->data, hd, m->tmp);
     memcpy(m->k + h * hd, m->tmp, sizeof(float) * hd);
   }
   for (int h = 0; h < nh; h++) ho_rope_apply(m->rope, c->max_seq, m->rope_dim, m->q + h * hd, pos);

@@ -39,6 +39,28 @@ def test_quantize_bit_exact(ctx, oracle, n):
     assert np.array_equal(host(out), oracle.quantize_q8_0(x))
 
 
+def test_quantize_near_ties(ctx, oracle):
+    """Values whose quotient x / scale sits on or next to a rounding tie: the
+    device's reciprocal fast path must defer to the exact division there."""
+    rng = np.random.default_rng(77)
+    nb = 8192
+    amax = rng.uniform(1e-3, 100, nb).astype(np.float32)
+    amax[:64] = 127.0                                  # scale exactly 1
+    s = np.where(amax == 0, 1, amax / np.float32(127)).astype(np.float32)
+    k = rng.integers(-127, 127, (nb, 31)).astype(np.float32)
+    frac = rng.choice(np.float32([0.5, 0.5, 0.4999999, 0.5000001, 0.25]), (nb, 31))
+    x = np.empty((nb, 32), np.float32)
+    x[:, 0] = amax * rng.choice([-1, 1], nb)
+    x[:, 1:] = ((k + frac) * s[:, None]).astype(np.float32)
+    ulp = np.spacing(x[:, 1:]) * rng.integers(-3, 4, (nb, 31))
+    x[nb // 2:, 1:] += ulp[nb // 2:].astype(np.float32)   # neighbours of the ties
+    x[:, 1:] = np.clip(x[:, 1:], -np.abs(x[:, :1]), np.abs(x[:, :1]))
+    x = x.reshape(-1)
+    out = torch.zeros(nb * 34, dtype=torch.uint8, device="cuda")
+    ctx.quantize_q8_0(dev(x), x.size, out)
+    assert np.array_equal(host(out), oracle.quantize_q8_0(x))
+
+
 @pytest.mark.parametrize("t", [8, 41, 42, 43, 142])
 def test_dequantize_bit_exact(ctx, oracle, t):
     n = 128 * 256
