@@ -25,6 +25,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per launch of the fused gate+up GEMV from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE on this kernel (x 1.9999 and x 1.0 from a 512 MiB copy's counts):
+# profiles/decode_8b_q2_hbm_traffic.txt.  Re-measure when the kernel changes.
+GATE_UP_TRAFFIC_BYTES = 27_208_000
 METRIC = "decode tok/s @bs1, 8B Q2_0 2k ctx; Q1/Q2 GEMV HBM GB/s vs peak"
 
 
@@ -139,7 +143,7 @@ def main():
                      "frac": round(step_gbs / PEAK_HBM_GBS, 4)},
         "roofline": {"bound": "hbm", "kernel": "k_gemv<Q2,RMSNORM,SILU> (fused gate+up, layer 0)",
                      "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
                      "avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": b["gate_up"]},
         "stage_ms": {k: round(v, 5) for k, v in stage.items()},
         "first_tokens": [int(t) for t in toks[:8]],

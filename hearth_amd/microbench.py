@@ -5,6 +5,8 @@ ring larger than 512 MB (twice the 256 MB last-level cache), so the traffic is
 HBM; bytes per launch = N*(K/128)*block_bytes + (K/32)*34 + 4N.
 
     python -m hearth_amd.microbench [--reps 1000] [--json]
+    python -m hearth_amd.microbench --copy-mb 512    (plain device copy of known
+        size: the calibration run for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)
 """
 import argparse
 import json
@@ -55,11 +57,29 @@ def run(reps: int = 1000, ring_bytes: int = 600 << 20, seed: int = 1):
     return out
 
 
+def copy_calibration(mb: int, reps: int = 4) -> None:
+    """reps device-to-device copies of mb MiB (torch copy kernel); each reads
+    and writes exactly mb MiB."""
+    import torch
+    n = mb << 20
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copied {mb} MiB x {reps}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=1000)
     ap.add_argument("--json", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0)
     a = ap.parse_args()
+    if a.copy_mb:
+        copy_calibration(a.copy_mb)
+        return
     res = run(a.reps)
     if a.json:
         print(json.dumps(res))
