@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = ["hh_gemv.hip", "hh_ops.hip", "hh_gdn.hip", "hh_runtime.hip"]
+SOURCES = ["hh_gemv.hip", "hh_gemm.hip", "hh_ops.hip", "hh_gdn.hip", "hh_runtime.hip"]
 LIB = os.path.join(HERE, "libhearth_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -1,0 +1,241 @@
+// hh_gemm.hip — batched (prefill) quantized GEMM on int8 MFMA for gfx950.
+//
+// Semantics: out[s*n + r] = dot_fn(w + r*row_bytes, x + s*q8_stride, K) for
+// every token s < seq_len and row r < n: par_dot_rows_batched with DotFn /
+// DotFn2 (pool.rs:40-80, :568-618; matmul.rs:580-674), whose paired kernels
+// are bit-identical to the single-token dot (q2_0.rs:936-986).  Here too:
+// every 32-element sub-block dot is an exact int32 from
+// v_mfma_i32_16x16x32_i8, and the fp32 combine follows the scalar kernels
+// (q2_0.rs:537-574, q1_0g128.rs:1113-1152, q8_0.rs:154-171):
+//   Q2/Q1: block_acc = (((0 + i0*da0) + i1*da1) + i2*da2) + i3*da3;
+//          sum += block_acc * dw          (128-weight blocks, 4 sub-blocks)
+//   Q8:    sum += ((float)i * dw) * da     (32-weight blocks)
+// so each output equals the decode GEMV's bit for bit.
+//
+// Tiling: a 512-lane workgroup owns 128 tokens x 64 rows; wave w owns tokens
+// [16w, 16w+16) and all 64 rows as four 16x16 MFMA tiles.  Per 128-column
+// step the workgroup stages the activation bytes and scales of its 64 tokens
+// and the weight blocks of its 64 rows in LDS, the weight codes widened to
+// int8 (code - 1, or +-1 per sign bit) once as they are stored
+// (double-buffered: the next step's global loads are issued before this
+// step's MFMAs).  Operand layouts (checked on the device): A lane l = row l%16,
+// k = 8*(l/16) .. +8; B lane l = column l%16, same k; C lane l = column l%16,
+// rows 4*(l/16) .. +4.
+#include "hh_kernels.h"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int NTG = 512;       // lanes per workgroup (8 waves, two per SIMD)
+constexpr int TM = 128;        // tokens per workgroup
+constexpr int TN = 64;         // rows per workgroup
+constexpr int KS = 128;        // columns per step
+constexpr int AROW = KS + 8;   // LDS bytes per token / weight row (padding breaks bank conflicts)
+
+// Global words of one step: activations 128 tokens x 136 B (34 u32; token rows
+// are 8-byte aligned because K % 128 == 0); weights Q2 64 x 34 B (17 u16, row
+// starts are only 2-byte aligned), Q1 64 x 18 B (9 u16), Q8 64 x 136 B (34 u32).
+constexpr int A_WORDS = TM * 34;
+template <int FMT> HH_DEV constexpr int w_units() { return FMT == FMT_Q2 ? 17 : FMT == FMT_Q1 ? 9 : 34; }
+template <int FMT> HH_DEV constexpr int w_regs() { return (TN * w_units<FMT>() + NTG - 1) / NTG; }
+constexpr int A_REGS = (A_WORDS + NTG - 1) / NTG;   // 9
+
+struct Stage {
+  int8_t a[TM * AROW];     // activations, int8
+  int8_t w[TN * AROW];     // weights widened to int8 (code - 1, or +-1)
+  float da[TM * 4];        // activation scale per (token, sub-block)
+  float dw[TN * 4];        // weight scale per row (Q2/Q1: [0]; Q8: per sub-block)
+};
+
+template <int FMT> struct Regs {
+  uint32_t a[A_REGS];
+  uint32_t w[w_regs<FMT>()];
+};
+
+template <int FMT>
+HH_DEV void stage_load(Regs<FMT>& R, const uint8_t* __restrict__ w, const uint8_t* __restrict__ x, int n, int seq,
+                       int K, int r0, int s0, int kb) {
+  const int tid = threadIdx.x;
+  const size_t q8_stride = (size_t)K / 32 * 34;
+#pragma unroll
+  for (int i = 0; i < A_REGS; ++i) {
+    const int idx = tid + NTG * i;
+    R.a[i] = 0;
+    if (idx < A_WORDS) {
+      const int t = idx / 34, wd = idx % 34;
+      if (s0 + t < seq) R.a[i] = *(const uint32_t*)(x + (size_t)(s0 + t) * q8_stride + (size_t)kb * 136 + 4 * wd);
+    }
+  }
+  constexpr int WU = w_units<FMT>();
+#pragma unroll
+  for (int i = 0; i < w_regs<FMT>(); ++i) {
+    const int idx = tid + NTG * i;
+    R.w[i] = 0;
+    if (idx < TN * WU) {
+      const int rr = idx / WU, u = idx % WU, r = r0 + rr;
+      if (r < n) {
+        if constexpr (FMT == FMT_Q8) {
+          const size_t row_bytes = (size_t)K / 32 * 34;
+          R.w[i] = *(const uint32_t*)(w + (size_t)r * row_bytes + (size_t)kb * 136 + 4 * u);
+        } else {
+          constexpr int BB = FMT == FMT_Q2 ? 34 : 18;
+          const size_t row_bytes = (size_t)K / 128 * BB;
+          R.w[i] = *(const uint16_t*)(w + (size_t)r * row_bytes + (size_t)kb * BB + 2 * u);
+        }
+      }
+    }
+  }
+}
+
+// Q2_0 codes (8 per u16, LSB first) -> 8 int8 (code - 1): spread the four
+// 2-bit fields of a byte to byte lanes, then (c + 0x7f) ^ 0x80 per lane.
+HH_DEV uint32_t q2_spread4(uint32_t y) {
+  uint32_t z = (y | (y << 6) | (y << 12) | (y << 18)) & 0x03030303u;
+  return (z + 0x7f7f7f7fu) ^ 0x80808080u;
+}
+// Q1_0 sign bits (4 in y, LSB first) -> 4 int8 (+1 / -1): bit j to byte lane
+// j, then (2b + 0x7f) ^ 0x80 per lane (0 -> 0xff, 1 -> 0x01, no carries).
+HH_DEV uint32_t q1_spread4(uint32_t y) {
+  uint32_t z = (y | (y << 7) | (y << 14) | (y << 21)) & 0x01010101u;
+  return ((z << 1) + 0x7f7f7f7fu) ^ 0x80808080u;
+}
+
+template <int FMT>
+HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
+  const int tid = threadIdx.x;
+  // activations: u32 word wd of token t covers bytes 4wd..4wd+3 of four
+  // [f16 d][32 q] blocks; its two halves are each a scale or two data bytes
+#pragma unroll
+  for (int i = 0; i < A_REGS; ++i) {
+    const int idx = tid + NTG * i;
+    if (idx < A_WORDS) {
+      const int t = idx / 34, wd = idx % 34;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int byte = 4 * wd + 2 * h, blk = byte / 34, off = byte % 34;
+        const uint32_t v = (R.a[i] >> (16 * h)) & 0xffffu;
+        if (off == 0) st.da[t * 4 + blk] = h2f(v);
+        else *(uint16_t*)(st.a + t * AROW + blk * 32 + off - 2) = (uint16_t)v;
+      }
+    }
+  }
+  constexpr int WU = w_units<FMT>();
+#pragma unroll
+  for (int i = 0; i < w_regs<FMT>(); ++i) {
+    const int idx = tid + NTG * i;
+    if (idx < TN * WU) {
+      const int rr = idx / WU, u = idx % WU;
+      const uint32_t v = R.w[i];
+      if constexpr (FMT == FMT_Q2) {
+        if (u == 0) st.dw[rr * 4] = h2f(v);
+        else {   // codes of elements 8(u-1) .. 8(u-1)+7
+          uint2 q = make_uint2(q2_spread4(v & 0xffu), q2_spread4(v >> 8));
+          *(uint2*)(st.w + rr * AROW + 8 * (u - 1)) = q;
+        }
+      } else if constexpr (FMT == FMT_Q1) {
+        if (u == 0) st.dw[rr * 4] = h2f(v);
+        else {   // bits of elements 16(u-1) .. +15
+          uint4 q = make_uint4(q1_spread4(v & 0xfu), q1_spread4((v >> 4) & 0xfu),
+                               q1_spread4((v >> 8) & 0xfu), q1_spread4((v >> 12) & 0xfu));
+          *(uint4*)(st.w + rr * AROW + 16 * (u - 1)) = q;
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int byte = 4 * u + 2 * h, blk = byte / 34, off = byte % 34;
+          const uint32_t hv = (v >> (16 * h)) & 0xffffu;
+          if (off == 0) st.dw[rr * 4 + blk] = h2f(hv);
+          else *(uint16_t*)(st.w + rr * AROW + blk * 32 + off - 2) = (uint16_t)hv;
+        }
+      }
+    }
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, const uint8_t* __restrict__ x,
+                                              float* __restrict__ out, int n, int K, int seq) {
+#pragma clang fp contract(off)
+  __shared__ Stage st[2];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int r0 = blockIdx.x * TN, s0 = blockIdx.y * TM;
+  const int nsteps = K / KS;
+  float sum[4][4], bacc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { sum[t][r] = 0.0f; bacc[t][r] = 0.0f; }
+
+  Regs<FMT> R;
+  stage_load<FMT>(R, w, x, n, seq, K, r0, s0, 0);
+  stage_store<FMT>(st[0], R);
+  __syncthreads();
+  const int arow = 16 * wid + (lane & 15);   // A operand token (within the tile)
+  const int kg = 8 * (lane >> 4);            // k offset within a sub-block
+  const int tok0 = 16 * wid + 4 * (lane >> 4);
+  for (int kb = 0; kb < nsteps; ++kb) {
+    const int cur = kb & 1;
+    const bool more = kb + 1 < nsteps;
+    if (more) stage_load<FMT>(R, w, x, n, seq, K, r0, s0, kb + 1);
+    const Stage& S = st[cur];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      const long a = *(const long*)(S.a + arow * AROW + sub * 32 + kg);
+      float da[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) da[r] = S.da[(tok0 + r) * 4 + sub];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int col = 16 * t + (lane & 15);
+        const long b = *(const long*)(S.w + col * AROW + sub * 32 + kg);
+        v4i c = {0, 0, 0, 0};
+        c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+        if constexpr (FMT == FMT_Q8) {
+          const float dw = S.dw[col * 4 + sub];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sum[t][r] += ((float)c[r] * dw) * da[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bacc[t][r] += (float)c[r] * da[r];
+        }
+      }
+    }
+    if constexpr (FMT != FMT_Q8) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float dw = S.dw[(16 * t + (lane & 15)) * 4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sum[t][r] += bacc[t][r] * dw;
+          bacc[t][r] = 0.0f;
+        }
+      }
+    }
+    if (more) stage_store<FMT>(st[cur ^ 1], R);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int r = r0 + 16 * t + (lane & 15);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int s = s0 + tok0 + q;
+      if (r < n && s < seq) out[(size_t)s * n + r] = sum[t][q];
+    }
+  }
+}
+
+}  // namespace
+
+int hh_gemm_launch(int fmt, const uint8_t* w, int n, int K, const uint8_t* x, int seq, float* out, hipStream_t s) {
+  if (K % KS != 0 || n <= 0 || seq <= 0) return 1;
+  dim3 grid((n + TN - 1) / TN, (seq + TM - 1) / TM);
+  switch (fmt) {
+    case FMT_Q2: hipLaunchKernelGGL(k_gemm<FMT_Q2>, grid, dim3(NTG), 0, s, w, x, out, n, K, seq); break;
+    case FMT_Q1: hipLaunchKernelGGL(k_gemm<FMT_Q1>, grid, dim3(NTG), 0, s, w, x, out, n, K, seq); break;
+    case FMT_Q8: hipLaunchKernelGGL(k_gemm<FMT_Q8>, grid, dim3(NTG), 0, s, w, x, out, n, K, seq); break;
+    default: return 1;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}

@@ -70,6 +70,9 @@ struct AttnArgs {
 };
 int hh_attn_launch(const AttnArgs& a, hipStream_t s);
 
+// Batched Q8_0 GEMM on int8 MFMA (prefill): out[s*n + r], K % 128 == 0.
+int hh_gemm_launch(int fmt, const uint8_t* w, int n, int K, const uint8_t* x, int seq, float* out, hipStream_t s);
+
 int hh_quantize_launch(const float* x, int64_t n, uint8_t* out, hipStream_t s);
 int hh_dequant_launch(int type, const void* w, int64_t n, float* out, hipStream_t s);
 int hh_rmsnorm_launch(const float* x, const float* w, float eps, int64_t rows, int64_t n, float* out,

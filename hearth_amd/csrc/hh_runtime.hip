@@ -502,6 +502,19 @@ int hh_gemv_q8(hh_ctx* c, int type, const void* w, int64_t n_rows, int64_t n_col
   return HH_OK;
 }
 
+int hh_gemm_q8(hh_ctx* c, int type, const void* w, int64_t n_rows, int64_t n_cols, const uint8_t* xq8,
+               int64_t seq_len, float* out) {
+  if (!c || !w || !xq8 || !out) return fail(HH_ERR_INVALID, "null argument");
+  int fmt = hh_fmt_of(type);
+  if (fmt < 0) return fail(HH_ERR_DTYPE, "unsupported weight dtype for the Q8_0 GEMM");
+  if (n_cols <= 0 || n_cols % 128 != 0) return fail(HH_ERR_DIM, "n_cols must be a positive multiple of 128");
+  if (n_rows <= 0 || n_rows > (1ll << 30) || seq_len <= 0 || seq_len > (1ll << 24))
+    return fail(HH_ERR_DIM, "bad n_rows or seq_len");
+  if ((n_rows + 63) / 64 > 2147483647ll || (seq_len + 63) / 64 > 65535) return fail(HH_ERR_DIM, "grid too large");
+  KTRY(hh_gemm_launch(fmt, (const uint8_t*)w, (int)n_rows, (int)n_cols, xq8, (int)seq_len, out, c->stream));
+  return HH_OK;
+}
+
 int hh_rms_norm(hh_ctx* c, const float* x, const float* w, float eps, int64_t rows, int64_t n, float* out) {
   if (!c || !x || !w || !out) return fail(HH_ERR_INVALID, "null argument");
   if (n <= 0 || rows < 0) return fail(HH_ERR_DIM, "bad shape");

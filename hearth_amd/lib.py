@@ -128,6 +128,8 @@ _EXPORTS = {
     "hh_quantize_q8_0": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
     "hh_dequantize": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int64, C.c_void_p]),
     "hh_gemv_q8": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]),
+    "hh_gemm_q8": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p, C.c_int64,
+                             C.c_void_p]),
     "hh_rms_norm": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_float, C.c_int64, C.c_int64, C.c_void_p]),
     "hh_rope": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int]),
     "hh_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
@@ -236,6 +238,10 @@ class Ctx:
 
     def gemv_q8(self, ggml_type: int, w, n_rows: int, n_cols: int, x_q8, y) -> None:
         _check(self.lib.hh_gemv_q8(self.h, ggml_type, _ptr(w), n_rows, n_cols, _ptr(x_q8), _ptr(y)))
+
+    def gemm_q8(self, ggml_type: int, w, n_rows: int, n_cols: int, x_q8, seq_len: int, out) -> None:
+        """Batched GEMM (prefill): out[s*n_rows + r] for seq_len Q8_0 token rows."""
+        _check(self.lib.hh_gemm_q8(self.h, ggml_type, _ptr(w), n_rows, n_cols, _ptr(x_q8), seq_len, _ptr(out)))
 
     def rms_norm(self, x, w, eps: float, rows: int, n: int, out) -> None:
         _check(self.lib.hh_rms_norm(self.h, _ptr(x), _ptr(w), eps, rows, n, _ptr(out)))

@@ -7,6 +7,8 @@ HBM; bytes per launch = N*(K/128)*block_bytes + (K/32)*34 + 4N.
     python -m hearth_amd.microbench [--reps 1000] [--json]
     python -m hearth_amd.microbench --copy-mb 512    (plain device copy of known
         size: the calibration run for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)
+    python -m hearth_amd.microbench --prefill        (batched int8-MFMA GEMM at the
+        27B and 8B FFN shapes, 2048 tokens, against the dense int8 MFMA peak)
 """
 import argparse
 import json
@@ -57,6 +59,51 @@ def run(reps: int = 1000, ring_bytes: int = 600 << 20, seed: int = 1):
     return out
 
 
+PEAK_INT8_TOPS = 5000.0
+PREFILL_SHAPES = [  # (label, ggml type, rows N, cols K)
+    ("27B ffn gate+up PQ2_0", 142, 2 * 17408, 5120),
+    ("27B ffn down PQ2_0", 142, 5120, 17408),
+    ("8B ffn gate+up Q2_0", 42, 2 * 12288, 4096),
+    ("1.7B ffn gate+up Q1_0", 41, 2 * 6144, 2048),
+]
+
+
+def prefill(tokens: int = 2048, reps: int = 5, seed: int = 3):
+    """Batched GEMM time per call and int8 TOPS (2*tokens*N*K / time)."""
+    import torch
+    from hearth_amd import Ctx, row_bytes
+    ctx = Ctx(0)
+    rng = np.random.default_rng(seed)
+    out = []
+    for label, t, n, k in PREFILL_SHAPES:
+        wb = n * row_bytes(t, k)
+        w = torch.randint(0, 256, (wb,), dtype=torch.uint8, device="cuda")
+        bb = 18 if t in (41, 43) else 34
+        sc = torch.tensor(np.frombuffer(np.float16(0.01).tobytes(), np.uint8), device="cuda")
+        view = w.view(-1, bb)
+        view[:, 0] = sc[0]
+        view[:, 1] = sc[1]
+        xq = torch.randint(-127, 128, (tokens * (k // 32), 34), dtype=torch.int8, device="cuda").view(torch.uint8)
+        s2 = torch.tensor(np.frombuffer(np.float16(0.02).tobytes(), np.uint8), device="cuda")
+        xq[:, 0] = s2[0]
+        xq[:, 1] = s2[1]
+        y = torch.zeros(tokens * n, dtype=torch.float32, device="cuda")
+        ctx.gemm_q8(t, w, n, k, xq, tokens, y)
+        ctx.sync()
+        ctx.event(0)
+        for _ in range(reps):
+            ctx.gemm_q8(t, w, n, k, xq, tokens, y)
+        ctx.event(1)
+        ms = ctx.elapsed_ms(0, 1) / reps
+        tops = 2.0 * tokens * n * k / (ms * 1e-3) / 1e12
+        out.append({"shape": label, "tokens": tokens, "n": n, "k": k, "ms": round(ms, 4),
+                    "int8_TOPS": round(tops, 1), "frac_peak": round(tops / PEAK_INT8_TOPS, 4)})
+        del w, xq, y
+        torch.cuda.empty_cache()
+    ctx.close()
+    return out
+
+
 def copy_calibration(mb: int, reps: int = 4) -> None:
     """reps device-to-device copies of mb MiB (torch copy kernel); each reads
     and writes exactly mb MiB."""
@@ -76,7 +123,14 @@ def main():
     ap.add_argument("--reps", type=int, default=1000)
     ap.add_argument("--json", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0)
+    ap.add_argument("--prefill", action="store_true")
     a = ap.parse_args()
+    if a.prefill:
+        for r in prefill():
+            print(json.dumps(r) if a.json else
+                  f"{r['shape']:<24} {r['tokens']} x {r['n']} x {r['k']}: {r['ms']:8.3f} ms  "
+                  f"{r['int8_TOPS']:7.1f} TOPS ({100 * r['frac_peak']:.1f}% of {PEAK_INT8_TOPS:.0f})")
+        return
     if a.copy_mb:
         copy_calibration(a.copy_mb)
         return

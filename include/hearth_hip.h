@@ -94,6 +94,16 @@ int hh_dequantize(hh_ctx* ctx, int ggml_type, const void* w, int64_t n, float* o
 int hh_gemv_q8(hh_ctx* ctx, int ggml_type, const void* w, int64_t n_rows, int64_t n_cols,
                const uint8_t* x_q8, float* y);
 
+/* Batched quantized GEMM for prefill: out[s*n_rows + r] = dot_fn(w + r*row_bytes,
+ * x_q8 + s*(n_cols/32)*34, n_cols) for every token s < seq_len.  Replaces
+ * ThreadPool::par_dot_rows_batched with DotFn / DotFn2 (pool.rs:40-80, :568-618;
+ * matmul.rs:580-674 matmul_batch).  Runs on int8 MFMA; each output is bit-identical
+ * to hh_gemv_q8 on that token, as the reference's paired kernels are to its
+ * single-token dot (q2_0.rs:936-986).  x_q8: seq_len rows of n_cols/32 standard
+ * Q8_0 blocks.  n_cols: a positive multiple of 128. */
+int hh_gemm_q8(hh_ctx* ctx, int ggml_type, const void* w, int64_t n_rows, int64_t n_cols,
+               const uint8_t* x_q8, int64_t seq_len, float* out);
+
 /* ops.rs:8-35 rms_norm over n_rows independent rows of width n. */
 int hh_rms_norm(hh_ctx* ctx, const float* x, const float* weight, float eps, int64_t n_rows,
                 int64_t n, float* out);

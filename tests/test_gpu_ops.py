@@ -200,3 +200,34 @@ def test_argmax_rules(ctx, oracle):
     xc = x.copy()
     want = lib.ho_sample_greedy_dense(xc.ctypes.data, x.size, past.ctypes.data, 4, 1.1)
     assert int(host(out)[0]) == want == 20
+
+
+@pytest.mark.parametrize("t", [41, 42, 8])
+@pytest.mark.parametrize("n,k,seq", [(200, 512, 70), (2048, 2048, 16), (64, 5120, 1), (130, 1024, 129)])
+def test_gemm_bit_exact_vs_per_token_dot(ctx, oracle, t, n, k, seq):
+    """Batched MFMA GEMM == the scalar DotFn on every token (the reference's paired
+    kernels are bit-identical to its single-token dot, q2_0.rs:936-986)."""
+    print(f"gemm t={t} n={n} k={k} seq={seq}", flush=True)
+    rng = np.random.default_rng(n + k + seq + t)
+    w = oracle.synth_tensor(t, 9, "w", n, k, 0.02, 0.0)
+    x = rng.standard_normal(seq * k).astype(np.float32) * rng.uniform(0.1, 5)
+    xq = np.concatenate([oracle.quantize_q8_0(x[s * k:(s + 1) * k]) for s in range(seq)])
+    out = torch.zeros(seq * n, dtype=torch.float32, device="cuda")
+    ctx.gemm_q8(t, dev(w), n, k, dev(xq), seq, out)
+    got = host(out).reshape(seq, n)
+    qs = k // 32 * 34
+    for s in range(seq):
+        want = oracle.gemv(t, w, n, k, xq[s * qs:(s + 1) * qs])
+        assert np.array_equal(got[s], want), s
+
+
+def test_gemm_errors(ctx):
+    from hearth_amd import HHError
+    w = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    y = torch.zeros(64, dtype=torch.float32, device="cuda")
+    with pytest.raises(HHError) as e:
+        ctx.gemm_q8(42, w, 4, 100, w, 2, y)
+    assert e.value.status == 3
+    with pytest.raises(HHError) as e:
+        ctx.gemm_q8(2, w, 4, 128, w, 2, y)
+    assert e.value.status == 2
