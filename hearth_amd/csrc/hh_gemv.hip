@@ -604,6 +604,110 @@ __global__ __launch_bounds__(1024) void k_head_final(GemvArgs p, int n_part) {
   }
 }
 
+
+// LM head (EPI_LOGITS): output_norm + Q8_0 of the hidden state, then every
+// vocab row's dot, the repetition penalty and the argmax partials
+// (sampler lib.rs:26-40, :167-175; qwen35.rs:1735-1745).  One workgroup per
+// CU stages the activation once; then each wave streams whole rows on its
+// own (rows gw, gw + W, ... for global wave gw of W), double-buffered in
+// VGPRs, with no further workgroup barrier.  Lane l holds the row's units
+// l + 64u (u < U); the row value is q_l = sum_u (p_2t + p_2t+1) over its
+// units' block products, then an ascending butterfly over the 64 lanes.
+template <int FMT, int U>
+__global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
+  constexpr int DW = UnitT<FMT>::DW;
+  constexpr int UB = UnitT<FMT>::BYTES;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const StepState* st = p.state;
+  if (st->step + 1 < st->n_prompt) return;   // k_head_final advances the prompt
+  const int K = p.K, P = p.P, n = p.n_rows;
+  const int nunits_act = K / UnitT<FMT>::EL;
+  int8_t* aq = (int8_t*)smem;
+  float* ds = (float*)(smem + nunits_act * qstride<FMT>());
+  float* red = ds + nunits_act * dss<FMT>();     // 16
+  float* bvs = red + 16;                         // 16 wave bests
+  int* bis = (int*)(bvs + 16);
+
+  const int gw = blockIdx.x * (NT / 64) + wv, W = gridDim.x * (NT / 64);
+  auto load_row = [&](uint32_t (&wr)[U][DW], int r) {
+    r = min(r, n - 1);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = min(lane + 64 * u, P - 1);
+      load_unit<FMT>(wr[u], p.w + ((size_t)r * P + t) * UB);
+    }
+  };
+  const int rule = p.rule;
+  const float pen = st->pen;
+  const bool do_pen = rule == 0 && !(fabsf(pen - 1.0f) < 1e-6f);
+  float bv = -INFINITY;
+  int bi = (rule == 0) ? -1 : 0x7fffffff;
+  auto row = [&](const uint32_t (&wr)[U][DW], int r) {
+    float q = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = lane + 64 * u;
+      if (t < P) {
+        float pr[2];
+        const float* ud = ds + t * dss<FMT>();
+        unit_dot<FMT>(wr[u], aq + t * qstride<FMT>(), ud, (const int*)(ud + UnitT<FMT>::SUBS), pr);
+        q = q + (pr[0] + pr[1]);
+      }
+    }
+    float v = group_sum<64>(q);
+    if (lane == 0) {
+      if (p.y) p.y[r] = v;
+      if (do_pen) {
+        const int c = p.counts[r];
+        for (int k = 0; k < c; ++k) v = (v > 0.0f) ? v / pen : v * pen;   // lib.rs:26-40
+      }
+      bool better = (rule == 0) ? (v > bv || (v == bv && r > bi)) : (v > bv || (v == bv && r < bi));
+      if (v != v) better = false;
+      if (better) { bv = v; bi = r; }
+    }
+  };
+
+  ActStage<FMT, PRO_RMSNORM> act;
+  act.issue(p);
+  uint32_t wa[U][DW], wb[U][DW];
+  load_row(wa, gw);
+  act.store(p, aq, ds, red);
+  __syncthreads();
+  for (int r = gw; r < n; r += 2 * W) {
+    load_row(wb, r + W);
+    row(wa, r);
+    load_row(wa, r + 2 * W);
+    if (r + W < n) row(wb, r + W);
+  }
+  if (lane == 0) { bvs[wv] = bv; bis[wv] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    float v1 = bvs[0];
+    int i1 = bis[0];
+    for (int w = 1; w < NT / 64; ++w) {
+      const float v2 = bvs[w];
+      const int i2 = bis[w];
+      const bool take = (rule == 0) ? (v2 > v1 || (v2 == v1 && i2 > i1)) : (v2 > v1 || (v2 == v1 && i2 < i1));
+      if (take) { v1 = v2; i1 = i2; }
+    }
+    p.part_val[blockIdx.x] = v1;
+    p.part_idx[blockIdx.x] = i1;
+  }
+}
+
+template <int FMT>
+int launch_head(GemvArgs a, hipStream_t s, int* n_wg_out) {
+  const int n_wg = std::max(1, std::min(256, (a.n_rows + NT / 64 - 1) / (NT / 64)));
+  const int nunits = a.K / UnitT<FMT>::EL;
+  const size_t lds = (size_t)nunits * (UnitT<FMT>::EL + 16) + (size_t)nunits * (FMT == FMT_Q8 ? 8 : 20) * 4 + 48 * 4;
+  if (a.P <= 64) hipLaunchKernelGGL((k_head<FMT, 1>), dim3(n_wg), dim3(NT), lds, s, a);
+  else if (a.P <= 128) hipLaunchKernelGGL((k_head<FMT, 2>), dim3(n_wg), dim3(NT), lds, s, a);
+  else return 1;
+  *n_wg_out = n_wg;
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
 template <int FMT, int PRO, int EPI, int NU>
 int launch_t(const GemvArgs& a, int n_wg, size_t lds, hipStream_t s) {
   hipLaunchKernelGGL((k_gemv<FMT, PRO, EPI, NU>), dim3(n_wg), dim3(NT), lds, s, a);
@@ -637,7 +741,6 @@ int launch_p(const GemvArgs& a, int pro, int epi, int nu, int n_wg, size_t lds, 
       if (a.K % 1024 != 0 || a.K > NORM_CH * 4 * NT) return 1;
       if (epi == EPI_STORE) return launch_u<FMT, PRO_RMSNORM, EPI_STORE>(a, nu, n_wg, lds, s);
       if (epi == EPI_SILU) return launch_u<FMT, PRO_RMSNORM, EPI_SILU>(a, nu, n_wg, lds, s);
-      if (epi == EPI_LOGITS) return launch_u<FMT, PRO_RMSNORM, EPI_LOGITS>(a, nu, n_wg, lds, s);
       return 1;
   }
   return 1;
@@ -671,6 +774,18 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   if (a.K % el != 0) return 1;
   a.P = a.K / el;
   int n_wg, rows_total;
+  if (epi == EPI_LOGITS) {   // persistent row-streaming head + finalize
+    if (pro != PRO_RMSNORM || a.K % 1024 != 0 || a.K > NORM_CH * 4 * NT) return 1;
+    int rc = 1;
+    switch (fmt) {
+      case FMT_Q2: rc = launch_head<FMT_Q2>(a, s, &n_wg); break;
+      case FMT_Q1: rc = launch_head<FMT_Q1>(a, s, &n_wg); break;
+      case FMT_Q8: rc = launch_head<FMT_Q8>(a, s, &n_wg); break;
+    }
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), 0, s, a, n_wg);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+  }
   if (epi == EPI_SILU) {
     if (a.half_rows % 32 != 0) return 1;
     const int nblk = a.half_rows / 32;

@@ -741,7 +741,7 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
     m->rows_down = gemv_rows_for(c.d_model, c.d_ffn / el);
     m->rows_head = gemv_rows_for(c.vocab, c.d_model / hh_unit_el(hh_fmt_of(c.head_type)));
   }
-  int head_wg = (c.vocab + m->rows_head - 1) / m->rows_head;
+  int head_wg = std::max(256, (c.vocab + m->rows_head - 1) / m->rows_head);
   m->max_out = c.max_seq + 8;
   HIP_TRY(hipMalloc(&m->hidden, sizeof(float) * c.d_model));
   HIP_TRY(hipMalloc(&m->proj, sizeof(float) * wide));

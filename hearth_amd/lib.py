@@ -185,16 +185,26 @@ def _check(rc: int) -> None:
 
 
 def _ptr(x) -> int:
-    """Device pointer of a torch tensor (or an int address)."""
+    """Device pointer of a torch tensor (or an int address).
+
+    The library runs on its own stream, so torch's pending work on a tensor
+    (an async fill or copy on torch's current stream) is waited for first."""
     if isinstance(x, int):
         return x
     if x is None:
         return 0
+    if getattr(x, "is_cuda", False):
+        import torch
+        torch.cuda.current_stream(x.device).synchronize()
     return x.data_ptr()
 
 
 class Ctx:
-    """One device context with its own HIP stream."""
+    """One device context with its own HIP stream.
+
+    Operator calls are asynchronous on that stream; torch work queued on a
+    tensor before a call is waited for, but reading a result with torch needs
+    ctx.sync() (or torch.cuda.synchronize()) first."""
 
     def __init__(self, device: int = 0):
         import weakref

@@ -1135,6 +1135,41 @@ static void mm(ho_model* m, const tensor_t* w, const float* x, float* out) {
   ho_gemv(w->type, w->data, w->rows, w->cols, m->q8, out, m->n_threads, m->arm);
 }
 
+/* The device's LM-head row value: lane l (of 64) holds the units t = l + 64u
+ * (two blocks each, u increasing) and sums q = q + (p_2t + p_2t+1) of their
+ * scalar block products; the lanes combine by bfly64. */
+static void dev_head_gemv(int type, const uint8_t* w, int64_t rows, int64_t K, const uint8_t* a, float* out,
+                          int threads) {
+  const int el = (type == 8) ? 32 : 128;
+  const size_t bb = ho_row_bytes(type, el), abb = (size_t)(el / 32) * 34, rb = ho_row_bytes(type, K);
+  const int64_t P = K / (2 * el);
+  float (*dot)(const uint8_t*, const uint8_t*, int64_t) =
+      type == 8 ? ho_dot_q8_0_q8_0 : (type == 41 || type == 43) ? ho_dot_q1_0_q8_0 : ho_dot_q2_0_q8_0;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t r = 0; r < rows; r++) {
+    const uint8_t* wr = w + (size_t)r * rb;
+    float lanes[64];
+    for (int l = 0; l < 64; l++) {
+      float q = 0.0f;
+      for (int64_t t = l; t < P; t += 64) {
+        float p0 = dot(wr + (size_t)(2 * t) * bb, a + (size_t)(2 * t) * abb, el);
+        float p1 = dot(wr + (size_t)(2 * t + 1) * bb, a + (size_t)(2 * t + 1) * abb, el);
+        q = q + (p0 + p1);
+      }
+      lanes[l] = q;
+    }
+    out[r] = bfly64(lanes);
+  }
+}
+
+/* LM head in the model's order. */
+static void head_mm(ho_model* m, const float* x, float* logits) {
+  const tensor_t* w = m->output;
+  ho_quantize_q8_0(x, w->cols, m->q8);
+  if (m->order) dev_head_gemv(w->type, w->data, w->rows, w->cols, m->q8, logits, m->n_threads);
+  else ho_gemv(w->type, w->data, w->rows, w->cols, m->q8, logits, m->n_threads, m->arm);
+}
+
 /* qwen35.rs:1809-1815 */
 static float softplus(float x) { return x > 20.0f ? x : ho_log(1.0f + ho_exp(x)); }
 
@@ -1198,8 +1233,7 @@ static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
     for (int i = 0; i < d; i++) m->hidden[i] += m->tmp[i];
   }
   norm_d(m, m->hidden, (const float*)m->output_norm->data, d, m->normed);
-  ho_quantize_q8_0(m->normed, d, m->q8);
-  ho_gemv(m->output->type, m->output->data, m->output->rows, d, m->q8, logits, m->n_threads, m->arm);
+  head_mm(m, m->normed, logits);
   (void)nq;
   return 0;
 }
@@ -1413,7 +1447,7 @@ static int forward_hybrid(ho_model* m, uint32_t token, int pos, float* logits) {
     for (int i = 0; i < d; i++) m->hidden[i] += m->attn_out[i];
   }
   norm_d(m, m->hidden, (const float*)m->output_norm->data, d, m->normed);
-  mm(m, m->output, m->normed, logits);
+  head_mm(m, m->normed, logits);
   return 0;
 }
 

@@ -59,10 +59,12 @@ def test_golden_gpu_ops(ctx):
     x = G["q8_x"]
     out = torch.zeros(G["q8_bytes"].size, dtype=torch.uint8, device="cuda")
     ctx.quantize_q8_0(dev(x), x.size, out)
+    ctx.sync()
     assert np.array_equal(out.cpu().numpy(), G["q8_bytes"])
     for name, t in (("q1", 41), ("q2", 42), ("q8", 8)):
         y = torch.zeros(N, dtype=torch.float32, device="cuda")
         ctx.gemv_q8(t, dev(G[f"gemv_{name}_w"]), N, K, dev(G[f"gemv_{name}_a"]), y)
+        ctx.sync()
         assert np.array_equal(y.cpu().numpy(), G[f"gemv_{name}_y"]), name
 
 
