@@ -76,6 +76,31 @@ def cpu_baseline(model, cfg, seed, kv_seed, tok0, budget_s: float):
                       f"{'AVX2 LUT' if avx2 else 'scalar'} Q2_0 arm, {threads} threads, {el:.1f} s"}
 
 
+PEAK_INT8_TOPS = 5000.0
+
+
+def prefill_leg(m, cfg, n_tok: int) -> dict:
+    """forward_batch of an n_tok seeded prompt at positions 0.. (overwrites the
+    synthetic KV; runs after the decode measurement).  The layer GEMMs run on
+    int8 MFMA; attention and the row kernels on the vector units."""
+    rng = np.random.default_rng(7)
+    toks = rng.integers(0, cfg.vocab, n_tok).tolist()
+    m.prefill(toks[:64], 0)                       # warm-up (scratch, code)
+    m.prefill(toks, 0)
+    ms = m.last_prefill_ms()
+    d, hd = cfg.d_model, cfg.head_dim
+    n_in = (cfg.n_heads + 2 * cfg.n_kv_heads) * hd
+    weights = cfg.n_layers * (n_in * d + d * cfg.n_heads * hd + 2 * cfg.d_ffn * d + d * cfg.d_ffn)
+    gemm_ops = 2.0 * n_tok * weights
+    tops = gemm_ops / (ms * 1e-3) / 1e12
+    print(f"[bench] prefill {n_tok} tokens: {ms:.2f} ms ({n_tok / (ms * 1e-3):.0f} tok/s)", file=sys.stderr, flush=True)
+    return {"tokens": n_tok, "ms": round(ms, 3), "tok_per_s": round(n_tok / (ms * 1e-3), 1),
+            "gemm_int8_ops": gemm_ops, "int8_TOPS_over_whole_prefill": round(tops, 1),
+            "mfma_frac": round(tops / PEAK_INT8_TOPS, 4), "peak_int8_TOPS": PEAK_INT8_TOPS,
+            "note": "int8 ops of the layer GEMMs only, divided by the whole prefill time (attention and row "
+                    "kernels included); dense-model forward_batch, bit-identical to token-by-token decode"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -84,6 +109,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=0, help="override layer count (debug only)")
+    ap.add_argument("--prefill-tokens", type=int, default=2048,
+                    help="batched-prefill leg after the decode measurement (0 = skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs one GPU per process: bench.py measures --gpus 1 only; "
@@ -148,6 +175,8 @@ def main():
         "stage_ms": {k: round(v, 5) for k, v in stage.items()},
         "first_tokens": [int(t) for t in toks[:8]],
     }
+    if args.prefill_tokens > 0:
+        out["prefill"] = prefill_leg(m, cfg, args.prefill_tokens)
     if not args.no_cpu:
         try:
             out["cpu_baseline"] = cpu_baseline(m, cfg, seed, kv_seed, tok0, args.cpu_budget)

@@ -88,28 +88,28 @@ __global__ void k_rope(float* x, int n_heads, int hd, int rope_dim, const float*
   xh[i + half] = x0 * s + x1 * c;
 }
 
-// mod.rs:483-504: hidden = dequantize(token_embd row), token from the step state.
+// mod.rs:483-504: element i of the dequantized token_embd row of token tok.
+HH_DEV float embed_value(int type, const uint8_t* __restrict__ table, int d, int tok, int i) {
+  if (type == 8) {
+    const uint8_t* blk = table + (size_t)tok * (d / 32) * 34 + (size_t)(i / 32) * 34;
+    return h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) * (float)(int8_t)blk[2 + (i % 32)];
+  } else if (type == 42 || type == 142) {
+    const uint8_t* blk = table + (size_t)tok * (d / 128) * 34 + (size_t)(i / 128) * 34;
+    int e = i % 128;
+    int code = (blk[2 + e / 4] >> (2 * (e % 4))) & 3;
+    return (float)(code - 1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  }
+  const uint8_t* blk = table + (size_t)tok * (d / 128) * 18 + (size_t)(i / 128) * 18;
+  int e = i % 128;
+  int bit = (blk[2 + e / 8] >> (e % 8)) & 1;
+  return (float)(bit ? 1 : -1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+}
+
+// hidden = dequantize(token_embd row), token from the step state.
 __global__ __launch_bounds__(256) void k_embed(int type, const uint8_t* __restrict__ table, int d,
                                                const StepState* __restrict__ st, float* __restrict__ hidden) {
-  int tok = st->token;
-  for (int i = threadIdx.x; i < d; i += 256) {
-    float v;
-    if (type == 8) {
-      const uint8_t* blk = table + (size_t)tok * (d / 32) * 34 + (size_t)(i / 32) * 34;
-      v = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) * (float)(int8_t)blk[2 + (i % 32)];
-    } else if (type == 42 || type == 142) {
-      const uint8_t* blk = table + (size_t)tok * (d / 128) * 34 + (size_t)(i / 128) * 34;
-      int e = i % 128;
-      int code = (blk[2 + e / 4] >> (2 * (e % 4))) & 3;
-      v = (float)(code - 1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    } else {
-      const uint8_t* blk = table + (size_t)tok * (d / 128) * 18 + (size_t)(i / 128) * 18;
-      int e = i % 128;
-      int bit = (blk[2 + e / 8] >> (e % 8)) & 1;
-      v = (float)(bit ? 1 : -1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    }
-    hidden[i] = v;
-  }
+  const int tok = st->token;
+  for (int i = threadIdx.x; i < d; i += 256) hidden[i] = embed_value(type, table, d, tok, i);
 }
 
 // ---------------------------------------------------------------------------
@@ -467,6 +467,322 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Batched prefill (forward_batch, mod.rs:899-1221) pieces.  Each restates, per
+// token row, the arithmetic of the decode step's fused kernels, so a prompt
+// prefilled here leaves the same KV cache and residual stream as one fed token
+// by token.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_embed_rows(int type, const uint8_t* __restrict__ table, int d,
+                                                    const uint32_t* __restrict__ toks, float* __restrict__ H) {
+  const int s = blockIdx.x;
+  const int tok = (int)toks[s];
+  for (int i = threadIdx.x; i < d; i += 256) H[(size_t)s * d + i] = embed_value(type, table, d, tok, i);
+}
+
+// rms_norm(x_s, w) then Q8_0 into standard blocks, row s = blockIdx.x: the
+// GEMV prologue's arithmetic (block_sumsq_f4 order, (x * inv) * w, per-block
+// scale from the max of |v|, reciprocal rounding with the exact tie fallback).
+__global__ __launch_bounds__(256) void k_norm_q8_rows(const float* __restrict__ X, const float* __restrict__ w,
+                                                      float eps, int K, uint8_t* __restrict__ out) {
+  __shared__ float red16[16];
+  const int s = blockIdx.x, tid = threadIdx.x;
+  const float* x = X + (size_t)s * K;
+  uint8_t* o = out + (size_t)s * (K / 32) * 34;
+  const float tot = block_sumsq_f4(x, K, red16);
+  const float inv = 1.0f / sqrtf(tot / (float)K + eps);   // ops.rs:22-23
+  for (int e = tid * 4; e < K; e += 1024) {
+    const float4 xv = *(const float4*)(x + e), wv = *(const float4*)(w + e);
+    float vv[4] = {xv.x * inv * wv.x, xv.y * inv * wv.y, xv.z * inv * wv.z, xv.w * inv * wv.w};
+    float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+    am = group_max<8>(am);
+    const float sc = q8_scale(am), rc = q8_rcp(sc);
+    uint8_t* blk = o + (size_t)(e >> 5) * 34;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) blk[2 + ((e + i) & 31)] = (uint8_t)(int8_t)q8_round_r(vv[i], sc, rc);
+    if ((tid & 7) == 0) {
+      const uint32_t h = f2h(sc);
+      blk[0] = (uint8_t)(h & 0xff);
+      blk[1] = (uint8_t)(h >> 8);
+    }
+  }
+}
+
+// silu(g) * u of the [gate; up] rows of token s, then Q8_0 into standard
+// blocks: the SILU epilogue's arithmetic (ops.rs:240-253, q8_0.rs:20-51).
+__global__ __launch_bounds__(256) void k_silu_q8_rows(const float* __restrict__ GU, int F, uint8_t* __restrict__ out) {
+  const int s = blockIdx.x, tid = threadIdx.x;
+  const float* g = GU + (size_t)s * 2 * F;
+  uint8_t* o = out + (size_t)s * (F / 32) * 34;
+  for (int i = tid; i < F; i += 256) {   // F % 256 == 0: whole waves
+    const float gv = g[i];
+    const float sg = gv / (1.0f + hx_exp(-gv));
+    const float h = sg * g[F + i];
+    const float am = group_max<32>(fabsf(h));
+    const float sc = q8_scale(am);
+    const int q = q8_round_r(h, sc, q8_rcp(sc));
+    uint8_t* blk = o + (size_t)(i >> 5) * 34;
+    blk[2 + (i & 31)] = (uint8_t)(int8_t)q;
+    if ((i & 31) == 0) {
+      const uint32_t hb = f2h(sc);
+      blk[0] = (uint8_t)(hb & 0xff);
+      blk[1] = (uint8_t)(hb >> 8);
+    }
+  }
+}
+
+__global__ void k_add_rows(float* __restrict__ H, const float* __restrict__ T, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) H[i] = H[i] + T[i];   // mod.rs:718-720, :776-778
+}
+
+// Per token s (blockIdx.x) and kv head (blockIdx.y): the G query heads' and
+// the key's per-head RMSNorm + RoPE on float4 slices of LPR lanes (the split
+// kernel's slice_norm / slice_rope), K and V written at pos0 + s, the
+// rotated q kept for the attention pass.  One LPR-lane group per head.
+template <int HD>
+__global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QKV, int n_in, int n_heads, int n_kv,
+                                                    const float* __restrict__ q_norm, const float* __restrict__ k_norm,
+                                                    float eps, const float* __restrict__ rope, int rope_dim,
+                                                    int max_seq, int pos0, float* __restrict__ k_cache,
+                                                    float* __restrict__ v_cache, float* __restrict__ QB) {
+  constexpr int LPR = HD / 4;
+  const int s = blockIdx.x, kvh = blockIdx.y, G = n_heads / n_kv;
+  const int grp = threadIdx.x / LPR, c = threadIdx.x % LPR;
+  const int pos = pos0 + s;
+  const float* row = QKV + (size_t)s * n_in;
+  if (grp > G) return;   // whole LPR-lane groups
+  const bool is_k = grp == G;
+  const int qh = kvh * G + grp;
+  float4 x = is_k ? *(const float4*)(row + (size_t)n_heads * HD + (size_t)kvh * HD + 4 * c)
+                  : *(const float4*)(row + (size_t)qh * HD + 4 * c);
+  const float* nw = is_k ? k_norm : q_norm;
+  if (nw) x = slice_norm<LPR>(x, *(const float4*)(nw + 4 * c), eps);
+  if (rope) {
+    float4 sn = make_float4(0.f, 0.f, 0.f, 0.f), cs = sn;
+    if (4 * c < rope_dim) {
+      const int half = rope_dim / 2, ib = (4 * c < half) ? 4 * c : 4 * c - half;
+      const float* base = rope + (size_t)(pos % max_seq) * half * 2;
+      sn = *(const float4*)(base + ib);
+      cs = *(const float4*)(base + half + ib);
+    }
+    x = slice_rope(x, sn, cs, 4 * c, rope_dim);
+  }
+  if (is_k) {
+    const size_t off = ((size_t)kvh * max_seq + pos) * HD + 4 * c;
+    *(float4*)(k_cache + off) = x;
+    *(float4*)(v_cache + off) = *(const float4*)(row + (size_t)(n_heads + n_kv) * HD + (size_t)kvh * HD + 4 * c);
+  } else {
+    *(float4*)(QB + (size_t)s * n_heads * HD + (size_t)qh * HD + 4 * c) = x;
+  }
+}
+
+// Prefill attention, split pass: workgroup (chunk c, kv head, token tile)
+// holds K/V rows of chunk c in registers exactly as k_attn_split does and
+// runs the decode arithmetic (scores, chunk softmax, P.V and their reduction
+// order) once per token of the tile whose position reaches the chunk.
+// Partials: PO[((sl*n_kv + kvh)*n_chunks + c)*G + h][HD], PML likewise x2.
+template <int HD, int NTA>
+__global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restrict__ QB, const float* __restrict__ k_cache,
+                                                            const float* __restrict__ v_cache, int n_heads, int n_kv,
+                                                            int max_seq, int pos0, int S, int t0, int TT, int n_chunks,
+                                                            float* __restrict__ PO, float* __restrict__ PML) {
+  constexpr int LPR = HD / 4, RPI = NTA / LPR, C = 8192 / HD, NR = C / RPI, NW = NTA / 64;
+  constexpr int GMAX = 8;
+  extern __shared__ __align__(16) float sm[];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c = blockIdx.x, kvh = blockIdx.y, G = n_heads / n_kv;
+  const int sl0 = blockIdx.z * TT, sl1 = min(sl0 + TT, S - t0);   // tile-launch-relative tokens
+  const int p0 = c * C;
+  const int np_max = min(C, pos0 + t0 + sl1 - p0);
+  if (sl0 >= sl1 || np_max <= 0) return;
+  const int sub = tid / LPR, cc = tid % LPR;
+  float* sc = sm;                 // G*C
+  float* ml = sc + G * C;         // 2*G (+pad)
+  float* red = ml + 2 * G + 4;    // NW waves * 4 heads * HD
+  const size_t hstride = (size_t)max_seq * HD;
+  const float* kg = k_cache + (size_t)kvh * hstride + 4 * cc;
+  const float* vg = v_cache + (size_t)kvh * hstride + 4 * cc;
+  float4 kr[NR], vr[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int j = i * RPI + sub;
+    kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    vr[i] = kr[i];
+    if (j < np_max) {
+      kr[i] = *(const float4*)(kg + (size_t)(p0 + j) * HD);
+      vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
+    }
+  }
+  const float inv_sqrt = 1.0f / sqrtf((float)HD);
+  constexpr int NV = 4 * NR;
+  constexpr int KSH = (LPR == 64 ? 6 : 5) - (NV == 32 ? 5 : NV == 16 ? 4 : 3);
+  for (int sl = sl0; sl < sl1; ++sl) {
+    const int s = t0 + sl, seq = pos0 + s + 1;
+    if (p0 >= seq) continue;
+    const int np = min(C, seq - p0);
+    float4 q4[GMAX];
+#pragma unroll
+    for (int h = 0; h < GMAX; ++h) {
+      q4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (h < G) q4[h] = *(const float4*)(QB + (size_t)s * n_heads * HD + (size_t)(kvh * G + h) * HD + 4 * cc);
+    }
+#pragma unroll
+    for (int hg = 0; hg < GMAX; hg += 4) {
+      if (hg >= G) break;
+      float v[NV];
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        const float4 qq = q4[hg + hh];
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+          float pp = qq.x * kr[i].x;
+          pp = fmaf(qq.y, kr[i].y, pp);
+          pp = fmaf(qq.z, kr[i].z, pp);
+          pp = fmaf(qq.w, kr[i].w, pp);
+          v[hh * NR + i] = pp;
+        }
+      }
+      const float r = ReduceScatter<NV, LPR / 2>::run(v, lane);
+      const int k = (lane & (LPR - 1)) >> KSH;
+      const int h = hg + k / NR, j = (k % NR) * RPI + sub;
+      if (h < G && (lane & ((1 << KSH) - 1)) == 0) sc[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
+    }
+    __syncthreads();
+    for (int h = wid; h < G; h += NW) {
+      float x = lane < C ? sc[h * C + lane] : -INFINITY;
+      float m = wave_max(x);
+      float e = (lane < np) ? hx_exp(x - m) : 0.0f;
+      float l = wave_sum(e);
+      if (lane < C) sc[h * C + lane] = e;
+      if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
+    }
+    __syncthreads();
+    const size_t pbase = ((size_t)(sl * n_kv + kvh) * n_chunks + c) * G;
+    for (int hg = 0; hg < G; hg += 4) {
+      float acc[16];
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+        if (hg + hh < G) {
+          const float* eh = sc + (hg + hh) * C + sub;
+#pragma unroll
+          for (int i = 0; i < NR; ++i) {
+            const float e = eh[i * RPI];
+            o0 = fmaf(e, vr[i].x, o0);
+            o1 = fmaf(e, vr[i].y, o1);
+            o2 = fmaf(e, vr[i].z, o2);
+            o3 = fmaf(e, vr[i].w, o3);
+          }
+        }
+        acc[hh * 4 + 0] = o0; acc[hh * 4 + 1] = o1; acc[hh * 4 + 2] = o2; acc[hh * 4 + 3] = o3;
+      }
+      if constexpr (LPR == 32) {
+        const bool up = (lane & 32) != 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          float send = up ? acc[k] : acc[k + 8];
+          float keep = up ? acc[k + 8] : acc[k];
+          float x = keep + __shfl_xor(send, 32, 64);
+          const int kk = k + (up ? 8 : 0);
+          red[(wid * 4 + (kk >> 2)) * HD + 4 * cc + (kk & 3)] = x;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) red[(wid * 4 + (k >> 2)) * HD + 4 * cc + (k & 3)] = acc[k];
+      }
+      __syncthreads();
+      for (int idx = tid; idx < 4 * HD; idx += NTA) {
+        const int h = hg + idx / HD;
+        if (h < G) {
+          float t[NW];
+#pragma unroll
+          for (int w = 0; w < NW; ++w) t[w] = red[w * 4 * HD + idx];
+          PO[(pbase + h) * HD + (idx % HD)] = pairwise_tree<NW>(t);
+        }
+      }
+      __syncthreads();
+    }
+    if (tid < G) {
+      PML[(pbase + tid) * 2] = ml[2 * tid];
+      PML[(pbase + tid) * 2 + 1] = ml[2 * tid + 1];
+    }
+  }
+}
+
+// Prefill attention, merge pass: k_attn_merge's arithmetic for token t0 + sl
+// (blockIdx.x = sl * n_heads + qh), writing the Q8_0 row of attn_output's
+// input in standard blocks.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restrict__ PO, const float* __restrict__ PML,
+                                                            int n_heads, int n_kv, int n_chunks, int pos0, int t0,
+                                                            uint8_t* __restrict__ Y) {
+  extern __shared__ __align__(16) float wm[];
+  float* wts = wm;                         // n_chunks
+  float* pw = wm + n_chunks;               // 4 x 64
+  float* sL = pw + 256;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int sl = blockIdx.x / n_heads, qh = blockIdx.x % n_heads, d = blockIdx.y * 64 + lane;
+  const int G = n_heads / n_kv, kvh = qh / G, h = qh % G;
+  constexpr int C = 8192 / HD;
+  const int s = t0 + sl, seq = pos0 + s + 1;
+  const int n_active = (seq + C - 1) / C;
+  const size_t hb = (size_t)(sl * n_kv + kvh) * n_chunks * G + h;
+  const size_t tstride = (size_t)G * HD;
+  const float* pb = PO + hb * HD + d;
+  float pv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = wid + 4 * i;
+    pv[i] = t < n_active ? pb[(size_t)t * tstride] : 0.0f;
+  }
+  if (wid == 0) {
+    float M = -INFINITY;
+    for (int t = lane; t < n_active; t += 64) M = fmaxf(M, PML[(hb + (size_t)t * G) * 2]);
+    M = wave_max(M);
+    float L = 0.0f;
+    for (int t = lane; t < n_active; t += 64) {
+      float e = hx_exp(PML[(hb + (size_t)t * G) * 2] - M);
+      wts[t] = e;
+      L += e * PML[(hb + (size_t)t * G) * 2 + 1];
+    }
+    L = wave_sum(L);
+    if (lane == 0) *sL = L;
+  }
+  __syncthreads();
+  float P = 0.0f;
+  for (int tt0 = 0; tt0 < n_active; tt0 += 64) {
+    if (tt0 > 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = tt0 + wid + 4 * i;
+        pv[i] = t < n_active ? pb[(size_t)t * tstride] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int t = tt0 + wid + 4 * i;
+      if (t < n_active) P = fmaf(wts[t], pv[i], P);
+    }
+  }
+  pw[wid * 64 + lane] = P;
+  __syncthreads();
+  if (wid != 0) return;
+  float o = (pw[lane] + pw[64 + lane]) + (pw[128 + lane] + pw[192 + lane]);
+  o = o * (1.0f / *sL);
+  const float am = group_max<32>(fabsf(o));
+  const float scq = q8_scale(am);
+  const int q = q8_round_r(o, scq, q8_rcp(scq));
+  const int e = qh * HD + d, K = n_heads * HD;
+  uint8_t* blk = Y + (size_t)s * (K / 32) * 34 + (size_t)(e >> 5) * 34;
+  blk[2 + (e & 31)] = (uint8_t)(int8_t)q;
+  if ((lane & 31) == 0) {
+    const uint32_t hbits = f2h(scq);
+    blk[0] = (uint8_t)(hbits & 0xff);
+    blk[1] = (uint8_t)(hbits >> 8);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Greedy selection over a logits vector (standalone operator).
 // ---------------------------------------------------------------------------
 HH_DEV bool better(int rule, float v2, int i2, float v1, int i1) {
@@ -715,3 +1031,66 @@ int hh_kv_synth_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq, f
   hipLaunchKernelGGL(k_kv_synth, dim3(nblk(total, 256)), dim3(256), 0, s, key, n_pos, n_kv, hd, max_seq, cs, cache);
   return ok();
 }
+
+int hh_embed_rows_launch(int type, const uint8_t* table, int d, const uint32_t* toks, int S, float* H, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed_rows, dim3(S), dim3(256), 0, s, type, table, d, toks, H);
+  return ok();
+}
+
+int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int S, uint8_t* out, hipStream_t s) {
+  if (K % 1024 != 0) return 1;
+  hipLaunchKernelGGL(k_norm_q8_rows, dim3(S), dim3(256), 0, s, X, w, eps, K, out);
+  return ok();
+}
+
+int hh_silu_q8_rows_launch(const float* GU, int F, int S, uint8_t* out, hipStream_t s) {
+  if (F % 256 != 0) return 1;
+  hipLaunchKernelGGL(k_silu_q8_rows, dim3(S), dim3(256), 0, s, GU, F, out);
+  return ok();
+}
+
+int hh_add_rows_launch(float* H, const float* T, int64_t n, hipStream_t s) {
+  hipLaunchKernelGGL(k_add_rows, dim3(nblk(n, 256)), dim3(256), 0, s, H, T, n);
+  return ok();
+}
+
+int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_kv, const float* q_norm,
+                         const float* k_norm, float eps, const float* rope, int rope_dim, int max_seq, int pos0, int S,
+                         float* k_cache, float* v_cache, float* QB, hipStream_t s) {
+  const int G = n_heads / n_kv;
+  if (hd == 128 && G + 1 <= 512 / 32)
+    hipLaunchKernelGGL(k_prefill_qk<128>, dim3(S, n_kv), dim3(512), 0, s, QKV, n_in, n_heads, n_kv, q_norm, k_norm,
+                       eps, rope, rope_dim, max_seq, pos0, k_cache, v_cache, QB);
+  else if (hd == 256 && G + 1 <= 512 / 64)
+    hipLaunchKernelGGL(k_prefill_qk<256>, dim3(S, n_kv), dim3(512), 0, s, QKV, n_in, n_heads, n_kv, q_norm, k_norm,
+                       eps, rope, rope_dim, max_seq, pos0, k_cache, v_cache, QB);
+  else
+    return 1;
+  return ok();
+}
+
+// Attention for tokens [t0, t0 + n) of a prefill; PO/PML hold n tokens' partials.
+int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
+                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML, uint8_t* Y,
+                           hipStream_t s) {
+  const int G = n_heads / n_kv, TT = 16;
+  if (G > 8 || n_kv * G != n_heads) return 1;
+  const size_t split_lds = 4 * ((size_t)G * (8192 / hd) + 2 * G + 4 + (ATTN_NT / 64) * 4 * (size_t)hd);
+  const size_t merge_lds = 4 * ((size_t)n_chunks + 256 + 4);
+  dim3 g1(n_chunks, n_kv, (n + TT - 1) / TT), g2(n * n_heads, hd / 64);
+  if (hd == 128) {
+    hipLaunchKernelGGL((k_attn_prefill_split<128, ATTN_NT>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, v_cache,
+                       n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML);
+    hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
+                       t0, Y);
+  } else if (hd == 256) {
+    hipLaunchKernelGGL((k_attn_prefill_split<256, ATTN_NT>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, v_cache,
+                       n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML);
+    hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
+                       t0, Y);
+  } else {
+    return 1;
+  }
+  return ok();
+}
+

@@ -158,11 +158,15 @@ struct hh_model {
   // graph
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
-  hipEvent_t ev0 = nullptr, ev1 = nullptr;
-  double last_decode_ms = 0.0;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr, ev2 = nullptr, evp = nullptr;
+  double last_decode_ms = 0.0, last_prefill_ms = 0.0;
   int cancel = 0;
   // launch geometry
   int rows_in = 16, rows_out = 16, rows_gu = 32, rows_down = 16, rows_head = 64;
+  // batched prefill scratch (grown on demand); HH_BATCHED_PREFILL=0 feeds prompts token by token
+  uint8_t* pf_buf = nullptr;
+  size_t pf_cap = 0;
+  int batched_prefill = 1;
 };
 
 namespace {
@@ -375,6 +379,70 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
   h.part_idx = m->head_pi;
   h.counter = m->counters;
   if (want(6, -1)) KTRY(hh_gemv_launch(hh_fmt_of(c.head_type), HH_PRO_RMSNORM, HH_EPI_LOGITS, h, s));
+  return HH_OK;
+}
+
+
+
+// Batched prefill of a dense model (forward_batch, mod.rs:899-1221): tokens
+// toks[0..S) at positions pos0.. through every layer with the int8-MFMA GEMM
+// and row kernels that restate the decode step's arithmetic, writing the KV
+// cache; no logits (mod.rs:1201-1218 computes only the last token's, which the
+// caller runs through the decode step).
+int prefill_dense(hh_model* m, const uint32_t* toks, int S, int pos0) {
+  const hh_model_config& c = m->cfg;
+  hipStream_t s = m->ctx->stream;
+  const int d = c.d_model, hd = c.head_dim, nq = c.n_heads * hd, F = c.d_ffn;
+  const int n_in = nq + 2 * c.n_kv_heads * hd;
+  const int wt = c.wtype;
+  const int TA = 128;                              // attention tokens per pass
+  const int n_chunks = m->attn_splits, G = c.n_heads / c.n_kv_heads;
+  auto q8b = [](long long K) { return (size_t)(K / 32) * 34; };
+  // scratch layout
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
+  const size_t oH = take((size_t)S * d * 4), oX = take((size_t)S * q8b(std::max(d, F))),
+               oQKV = take((size_t)S * n_in * 4), oQB = take((size_t)S * nq * 4), oA = take((size_t)S * q8b(nq)),
+               oT = take((size_t)S * d * 4), oGU = take((size_t)S * 2 * F * 4),
+               oPO = take((size_t)TA * c.n_kv_heads * n_chunks * G * hd * 4),
+               oPML = take((size_t)TA * c.n_kv_heads * n_chunks * G * 2 * 4);
+  if (off > m->pf_cap) {
+    if (m->pf_buf) HIP_TRY(hipFree(m->pf_buf));
+    m->pf_buf = nullptr;
+    m->pf_cap = 0;
+    if (hipMalloc(&m->pf_buf, off) != hipSuccess) return fail(HH_ERR_OOM, "prefill scratch allocation failed");
+    m->pf_cap = off;
+  }
+  uint8_t* B = m->pf_buf;
+  float* H = (float*)(B + oH);
+  uint8_t* X = B + oX;
+  float* QKV = (float*)(B + oQKV);
+  float* QB = (float*)(B + oQB);
+  uint8_t* A = B + oA;
+  float* T = (float*)(B + oT);
+  float* GU = (float*)(B + oGU);
+  float* PO = (float*)(B + oPO);
+  float* PML = (float*)(B + oPML);
+  KTRY(hh_embed_rows_launch(c.head_type, m->token_embd->d, d, toks, S, H, s));
+  for (int li = 0; li < c.n_layers; ++li) {
+    Layer& L = m->layers[li];
+    KTRY(hh_norm_q8_rows_launch(H, L.attn_norm, c.eps, d, S, X, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_in, n_in, d, X, S, QKV, s));
+    KTRY(hh_prefill_qk_launch(hd, QKV, n_in, c.n_heads, c.n_kv_heads, c.qk_norm ? L.q_norm : nullptr,
+                              c.qk_norm ? L.k_norm : nullptr, c.eps, m->rope, m->rope_dim, c.max_seq, pos0, S,
+                              L.k_cache, L.v_cache, QB, s));
+    for (int t0 = 0; t0 < S; t0 += TA)
+      KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, c.max_seq, pos0, t0,
+                                  std::min(TA, S - t0), n_chunks, PO, PML, A, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_out, d, nq, A, S, T, s));
+    KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
+    KTRY(hh_norm_q8_rows_launch(H, L.ffn_norm, c.eps, d, S, X, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_gu, 2 * F, d, X, S, GU, s));
+    KTRY(hh_silu_q8_rows_launch(GU, F, S, X, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_down, d, F, X, S, T, s));
+    KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
+  }
+  (void)wt;
   return HH_OK;
 }
 
@@ -763,6 +831,12 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   HIP_TRY(hipMemset(m->state, 0, sizeof(StepState)));
   HIP_TRY(hipEventCreate(&m->ev0));
   HIP_TRY(hipEventCreate(&m->ev1));
+  HIP_TRY(hipEventCreate(&m->ev2));
+  HIP_TRY(hipEventCreate(&m->evp));
+  {
+    const char* e = getenv("HH_BATCHED_PREFILL");
+    m->batched_prefill = (e && e[0] == '0') ? 0 : 1;
+  }
   HIP_TRY(hipDeviceSynchronize());
   int rc = capture(m);
   if (rc) { std::string msg = g_err; hh_model_destroy(m); return fail(rc, "graph capture: " + msg); }
@@ -783,6 +857,9 @@ int hh_model_destroy(hh_model* m) {
     if (p) hipFree(p);
   if (m->ev0) hipEventDestroy(m->ev0);
   if (m->ev1) hipEventDestroy(m->ev1);
+  if (m->ev2) hipEventDestroy(m->ev2);
+  if (m->evp) hipEventDestroy(m->evp);
+  if (m->pf_buf) hipFree(m->pf_buf);
   delete m;
   return HH_OK;
 }
@@ -905,6 +982,7 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
     if (prompt[i] >= (uint32_t)m->cfg.vocab) return fail(HH_ERR_RANGE, "prompt token out of range");
   if (m->cancel) return fail(HH_ERR_CANCELLED, "Cancelled");
   hipStream_t s = m->ctx->stream;
+  HIP_TRY(hipEventRecord(m->evp, s));
   HIP_TRY(hipMemcpyAsync(m->prompt, prompt, sizeof(uint32_t) * n_prompt, hipMemcpyHostToDevice, s));
   // past_tokens = [last prompt token] (mod.rs:2879); counts start from it
   KTRY(hh_fill_i32_launch(m->counts, m->cfg.vocab, 0, s));
@@ -917,8 +995,19 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
   st.update = 1;
   st.pen = pen;
   HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
-  // prompt steps (the last one yields the first generated token)
-  for (int i = 0; i < n_prompt; ++i) HIP_TRY(hipGraphLaunch(m->gexec, s));
+  // prompt: dense models prefill all but the last token in one batched pass;
+  // the last prompt token runs the decode step, which yields the first
+  // generated token.  Hybrids feed the prompt token by token (qwen35.rs:1693-1700).
+  int fed = 0;
+  if (m->cfg.arch == 0 && m->batched_prefill && n_prompt >= 2) {
+    KTRY(prefill_dense(m, m->prompt, n_prompt - 1, start_pos));
+    fed = n_prompt - 1;
+    st.pos = start_pos + fed;
+    st.step = fed;
+    st.token = (int)prompt[fed];
+    HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
+  }
+  for (int i = fed; i < n_prompt; ++i) HIP_TRY(hipGraphLaunch(m->gexec, s));
   HIP_TRY(hipEventRecord(m->ev0, s));
   // decode steps: forward each generated token (the last forward only when its logits are wanted)
   int steps = n_gen - 1 + (last_logits ? 1 : 0);
@@ -932,6 +1021,8 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
   float ms = 0.0f;
   HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
   m->last_decode_ms = ms;
+  HIP_TRY(hipEventElapsedTime(&ms, m->evp, m->ev0));
+  m->last_prefill_ms = ms;
   return HH_OK;
 }
 
@@ -971,6 +1062,36 @@ int hh_model_time_stages(hh_model* m, int layer, int iters, double* out_ms, int 
   }
   HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
   HIP_TRY(hipStreamSynchronize(s));
+  return HH_OK;
+}
+
+int hh_model_prefill(hh_model* m, const uint32_t* tokens, int n, int start_pos) {
+  if (!m || !tokens) return fail(HH_ERR_INVALID, "null argument");
+  if (n <= 0) return fail(HH_ERR_INVALID, "Empty prompt");
+  if (m->cfg.arch != 0) return fail(HH_ERR_INVALID, "batched prefill covers the dense architecture only");
+  if (start_pos < 0 || start_pos + n > m->cfg.max_seq) return fail(HH_ERR_RANGE, "sequence exceeds max_seq");
+  for (int i = 0; i < n; ++i)
+    if (tokens[i] >= (uint32_t)m->cfg.vocab) return fail(HH_ERR_RANGE, "prompt token out of range");
+  if (m->cancel) return fail(HH_ERR_CANCELLED, "Cancelled");
+  hipStream_t s = m->ctx->stream;
+  uint32_t* dt = nullptr;
+  HIP_TRY(hipMalloc(&dt, sizeof(uint32_t) * n));
+  HIP_TRY(hipMemcpyAsync(dt, tokens, sizeof(uint32_t) * n, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipEventRecord(m->evp, s));
+  int rc = prefill_dense(m, dt, n, start_pos);
+  HIP_TRY(hipEventRecord(m->ev2, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  hipFree(dt);
+  if (rc) return rc;
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, m->evp, m->ev2));
+  m->last_prefill_ms = ms;
+  return HH_OK;
+}
+
+int hh_model_last_prefill_ms(hh_model* m, double* ms) {
+  if (!m || !ms) return fail(HH_ERR_INVALID, "null argument");
+  *ms = m->last_prefill_ms;
   return HH_OK;
 }
 

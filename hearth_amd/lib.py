@@ -153,6 +153,8 @@ _EXPORTS = {
                                      C.c_void_p]),
     "hh_model_last_decode_ms": (C.c_int, [C.c_void_p, C.POINTER(C.c_double)]),
     "hh_model_time_stages": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int]),
+    "hh_model_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
+    "hh_model_last_prefill_ms": (C.c_int, [C.c_void_p, C.POINTER(C.c_double)]),
 }
 
 
@@ -348,6 +350,16 @@ class Model:
         out = np.zeros(7, dtype=np.float64)
         _check(self.lib.hh_model_time_stages(self.h, layer, iters, out.ctypes.data, 7))
         return dict(zip(self.STAGES, out.tolist()))
+
+    def prefill(self, tokens: Sequence[int], start_pos: int = 0) -> None:
+        """Batched prefill (dense): K/V for tokens at start_pos.., no logits."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
+        _check(self.lib.hh_model_prefill(self.h, t.ctypes.data, len(t), start_pos))
+
+    def last_prefill_ms(self) -> float:
+        v = C.c_double()
+        _check(self.lib.hh_model_last_prefill_ms(self.h, C.byref(v)))
+        return v.value
 
     def last_decode_ms(self) -> float:
         v = C.c_double()

@@ -181,6 +181,20 @@ int hh_model_forward(hh_model* m, uint32_t token, int pos, float* logits_host,
 int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int start_pos, int n_gen,
                       float repeat_pen, uint32_t* out_tokens, float* last_logits_host);
 
+/* Batched prefill of a dense model (LlamaModel::forward_batch, mod.rs:899-1221):
+ * runs tokens[0..n) at positions start_pos.. through every layer with the
+ * int8-MFMA GEMM (hh_gemm_q8) and writes their K/V; computes no logits (the
+ * reference computes only the last token's, mod.rs:1201-1218: feed that token
+ * to hh_model_forward).  Each layer's arithmetic restates the decode step's, so
+ * the cache equals the one token-by-token decoding leaves.  hh_model_generate
+ * uses it for all prompt tokens but the last on dense models. */
+int hh_model_prefill(hh_model* m, const uint32_t* tokens, int n, int start_pos);
+
+/* Device time (ms) of the last prefill: hh_model_prefill, or the prompt phase of
+ * hh_model_generate (batched prefill plus the last prompt token's step, which
+ * yields the first generated token). */
+int hh_model_last_prefill_ms(hh_model* m, double* ms);
+
 /* Timing of the last hh_model_generate call, device clock (hipEvents): total ms
  * over the generated-token steps only (prefill excluded). */
 int hh_model_last_decode_ms(hh_model* m, double* ms);

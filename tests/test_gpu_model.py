@@ -142,3 +142,64 @@ def test_upload_roundtrip(ctx, oracle):
         m.upload(name, t, ne0, ne1, o.tensor(name))
     lg, _ = m.forward(5, 0)
     assert rel(lg, o.forward(5, 0)) < 1e-3
+
+
+def _model_with_env(ctx, cfg, seed, env):
+    import os
+    from hearth_amd import Model
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        m = Model(ctx, cfg)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    m.synthesize(seed)
+    return m
+
+
+@pytest.mark.parametrize("cfg,n_prompt", [(TINY, 9), (TINY.replace(wtype=GGML_Q1_0), 40),
+                                          (CONFIGS["8b-q2"].replace(n_layers=2, max_seq=640), 300)],
+                         ids=["dense-q2", "dense-q1", "8b-2layer-300"])
+def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
+    """forward_batch on the MFMA GEMM leaves the same KV cache as feeding the
+    prompt one token at a time: the first generated token's logits and the next
+    tokens are identical, and match the device-order oracle."""
+    print(f"prefill {cfg.d_model} {cfg.n_layers} n={n_prompt}", flush=True)
+    prompt = [oracle.synth_token(11, i, cfg.vocab) for i in range(n_prompt)]
+    mb = _model_with_env(ctx, cfg, 13, {"HH_BATCHED_PREFILL": "1"})
+    mt = _model_with_env(ctx, cfg, 13, {"HH_BATCHED_PREFILL": "0"})
+    tb, lb = mb.generate(prompt, 8, repeat_pen=1.1, want_logits=True)
+    tt, lt = mt.generate(prompt, 8, repeat_pen=1.1, want_logits=True)
+    assert list(tb) == list(tt)
+    assert np.array_equal(lb, lt)
+    if n_prompt <= 40:
+        o = oracle.OracleModel(cfg, seed=13, threads=16, order=oracle.OracleModel.DEVICE)
+        tw, lw = o.generate(prompt, 8, repeat_pen=1.1, want_logits=True)
+        assert list(tb) == list(tw)
+        assert np.array_equal(lb, lw)
+        o.close()
+    mb.close()
+    mt.close()
+
+
+def test_prefill_then_forward(ctx):
+    """hh_model_prefill(prompt[:-1]) then hh_model_forward(last token) equals
+    generate's first step."""
+    cfg = TINY
+    from hearth_amd import Model
+    prompt = [5, 77, 1023, 4000, 12, 9]
+    m = _model_with_env(ctx, cfg, 4, {"HH_BATCHED_PREFILL": "1"})
+    m.prefill(prompt[:-1], 0)
+    lg, am = m.forward(prompt[-1], len(prompt) - 1)
+    m2 = _model_with_env(ctx, cfg, 4, {"HH_BATCHED_PREFILL": "0"})
+    for p, t in enumerate(prompt[:-1]):
+        m2.forward(t, p)
+    lg2, am2 = m2.forward(prompt[-1], len(prompt) - 1)
+    assert np.array_equal(lg, lg2) and am == am2
+    assert m.last_prefill_ms() > 0
+    m.close()
+    m2.close()
