@@ -14,11 +14,13 @@
 //
 // Tiling: a 512-lane workgroup owns 128 tokens x 64 rows; wave w owns tokens
 // [16w, 16w+16) and all 64 rows as four 16x16 MFMA tiles.  Per 128-column
-// step the workgroup stages the activation bytes and scales of its 64 tokens
+// step the workgroup stages the activation bytes and scales of its 128 tokens
 // and the weight blocks of its 64 rows in LDS, the weight codes widened to
 // int8 (code - 1, or +-1 per sign bit) once as they are stored
 // (double-buffered: the next step's global loads are issued before this
-// step's MFMAs).  Operand layouts (checked on the device): A lane l = row l%16,
+// step's MFMAs).  Activations come split (int8 rows + f32 block scales), so
+// staging is plain 16-byte copies; the standard Q8_0 layout of the operator
+// entry point is split by k_q8_split first.  Operand layouts (checked on the device): A lane l = row l%16,
 // k = 8*(l/16) .. +8; B lane l = column l%16, same k; C lane l = column l%16,
 // rows 4*(l/16) .. +4.
 #include "hh_kernels.h"
@@ -31,62 +33,17 @@ constexpr int NTG = 512;       // lanes per workgroup (8 waves, two per SIMD)
 constexpr int TM = 128;        // tokens per workgroup
 constexpr int TN = 64;         // rows per workgroup
 constexpr int KS = 128;        // columns per step
-constexpr int AROW = KS + 8;   // LDS bytes per token / weight row (padding breaks bank conflicts)
+constexpr int AROW = KS + 16;  // LDS bytes per token / weight row (16-byte aligned, staggered banks)
 
-// Global words of one step: activations 128 tokens x 136 B (34 u32; token rows
-// are 8-byte aligned because K % 128 == 0); weights Q2 64 x 34 B (17 u16, row
-// starts are only 2-byte aligned), Q1 64 x 18 B (9 u16), Q8 64 x 136 B (34 u32).
-constexpr int A_WORDS = TM * 34;
-template <int FMT> HH_DEV constexpr int w_units() { return FMT == FMT_Q2 ? 17 : FMT == FMT_Q1 ? 9 : 34; }
-template <int FMT> HH_DEV constexpr int w_regs() { return (TN * w_units<FMT>() + NTG - 1) / NTG; }
-constexpr int A_REGS = (A_WORDS + NTG - 1) / NTG;   // 9
-
+// Activations arrive split: xq = int8 [seq][K], xd = f32 [seq][K/32] (the
+// Q8_0 scale of each 32-block).  Per step a lane copies two 16-byte pieces of
+// the 128 x 128 int8 tile and one scale; weight roles are wave-uniform.
 struct Stage {
   int8_t a[TM * AROW];     // activations, int8
   int8_t w[TN * AROW];     // weights widened to int8 (code - 1, or +-1)
   float da[TM * 4];        // activation scale per (token, sub-block)
   float dw[TN * 4];        // weight scale per row (Q2/Q1: [0]; Q8: per sub-block)
 };
-
-template <int FMT> struct Regs {
-  uint32_t a[A_REGS];
-  uint32_t w[w_regs<FMT>()];
-};
-
-template <int FMT>
-HH_DEV void stage_load(Regs<FMT>& R, const uint8_t* __restrict__ w, const uint8_t* __restrict__ x, int n, int seq,
-                       int K, int r0, int s0, int kb) {
-  const int tid = threadIdx.x;
-  const size_t q8_stride = (size_t)K / 32 * 34;
-#pragma unroll
-  for (int i = 0; i < A_REGS; ++i) {
-    const int idx = tid + NTG * i;
-    R.a[i] = 0;
-    if (idx < A_WORDS) {
-      const int t = idx / 34, wd = idx % 34;
-      if (s0 + t < seq) R.a[i] = *(const uint32_t*)(x + (size_t)(s0 + t) * q8_stride + (size_t)kb * 136 + 4 * wd);
-    }
-  }
-  constexpr int WU = w_units<FMT>();
-#pragma unroll
-  for (int i = 0; i < w_regs<FMT>(); ++i) {
-    const int idx = tid + NTG * i;
-    R.w[i] = 0;
-    if (idx < TN * WU) {
-      const int rr = idx / WU, u = idx % WU, r = r0 + rr;
-      if (r < n) {
-        if constexpr (FMT == FMT_Q8) {
-          const size_t row_bytes = (size_t)K / 32 * 34;
-          R.w[i] = *(const uint32_t*)(w + (size_t)r * row_bytes + (size_t)kb * 136 + 4 * u);
-        } else {
-          constexpr int BB = FMT == FMT_Q2 ? 34 : 18;
-          const size_t row_bytes = (size_t)K / 128 * BB;
-          R.w[i] = *(const uint16_t*)(w + (size_t)r * row_bytes + (size_t)kb * BB + 2 * u);
-        }
-      }
-    }
-  }
-}
 
 // Q2_0 codes (8 per u16, LSB first) -> 8 int8 (code - 1): spread the four
 // 2-bit fields of a byte to byte lanes, then (c + 0x7f) ^ 0x80 per lane.
@@ -101,61 +58,85 @@ HH_DEV uint32_t q1_spread4(uint32_t y) {
   return ((z << 1) + 0x7f7f7f7fu) ^ 0x80808080u;
 }
 
+template <int FMT> HH_DEV constexpr int w_code_units() { return FMT == FMT_Q2 ? 16 : FMT == FMT_Q1 ? 8 : 64; }
+template <int FMT> HH_DEV constexpr int w_regs() { return (TN * w_code_units<FMT>() + NTG - 1) / NTG; }
+template <int FMT> HH_DEV constexpr int w_scales() { return FMT == FMT_Q8 ? 4 : 1; }   // per row per step
+
+template <int FMT> struct Regs {
+  uint4 a[2];
+  float ad;
+  uint32_t w[w_regs<FMT>()];
+  uint32_t ws;
+};
+
 template <int FMT>
-HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
+HH_DEV void stage_load(Regs<FMT>& R, const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
+                       const float* __restrict__ xd, int n, int seq, int K, int r0, int s0, int kb) {
   const int tid = threadIdx.x;
-  // activations: u32 word wd of token t covers bytes 4wd..4wd+3 of four
-  // [f16 d][32 q] blocks; its two halves are each a scale or two data bytes
 #pragma unroll
-  for (int i = 0; i < A_REGS; ++i) {
-    const int idx = tid + NTG * i;
-    if (idx < A_WORDS) {
-      const int t = idx / 34, wd = idx % 34;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int byte = 4 * wd + 2 * h, blk = byte / 34, off = byte % 34;
-        const uint32_t v = (R.a[i] >> (16 * h)) & 0xffffu;
-        if (off == 0) st.da[t * 4 + blk] = h2f(v);
-        else *(uint16_t*)(st.a + t * AROW + blk * 32 + off - 2) = (uint16_t)v;
-      }
-    }
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + NTG * i, t = idx >> 3, piece = idx & 7;
+    const int sidx = min(s0 + t, seq - 1);
+    R.a[i] = *(const uint4*)(xq + (size_t)sidx * K + (size_t)kb * KS + 16 * piece);
   }
-  constexpr int WU = w_units<FMT>();
+  {
+    const int t = tid >> 2, sub = tid & 3;
+    const int sidx = min(s0 + t, seq - 1);
+    R.ad = xd[(size_t)sidx * (K / 32) + kb * 4 + sub];
+  }
+  constexpr int CU = w_code_units<FMT>();
+  const size_t row_bytes = (size_t)K / (FMT == FMT_Q8 ? 32 : 128) * (FMT == FMT_Q8 ? 34 : FMT == FMT_Q2 ? 34 : 18);
+  const size_t step_bytes = FMT == FMT_Q8 ? 136 : FMT == FMT_Q2 ? 34 : 18;
 #pragma unroll
   for (int i = 0; i < w_regs<FMT>(); ++i) {
-    const int idx = tid + NTG * i;
-    if (idx < TN * WU) {
-      const int rr = idx / WU, u = idx % WU;
-      const uint32_t v = R.w[i];
-      if constexpr (FMT == FMT_Q2) {
-        if (u == 0) st.dw[rr * 4] = h2f(v);
-        else {   // codes of elements 8(u-1) .. 8(u-1)+7
-          uint2 q = make_uint2(q2_spread4(v & 0xffu), q2_spread4(v >> 8));
-          *(uint2*)(st.w + rr * AROW + 8 * (u - 1)) = q;
-        }
-      } else if constexpr (FMT == FMT_Q1) {
-        if (u == 0) st.dw[rr * 4] = h2f(v);
-        else {   // bits of elements 16(u-1) .. +15
-          uint4 q = make_uint4(q1_spread4(v & 0xfu), q1_spread4((v >> 4) & 0xfu),
-                               q1_spread4((v >> 8) & 0xfu), q1_spread4((v >> 12) & 0xfu));
-          *(uint4*)(st.w + rr * AROW + 16 * (u - 1)) = q;
-        }
-      } else {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int byte = 4 * u + 2 * h, blk = byte / 34, off = byte % 34;
-          const uint32_t hv = (v >> (16 * h)) & 0xffffu;
-          if (off == 0) st.dw[rr * 4 + blk] = h2f(hv);
-          else *(uint16_t*)(st.w + rr * AROW + blk * 32 + off - 2) = (uint16_t)hv;
-        }
-      }
-    }
+    const int idx = min(tid + NTG * i, TN * CU - 1);
+    const int rr = idx / CU, u = idx % CU, r = min(r0 + rr, n - 1);
+    const uint8_t* base = w + (size_t)r * row_bytes + (size_t)kb * step_bytes;
+    if constexpr (FMT == FMT_Q8) R.w[i] = *(const uint16_t*)(base + (u / 16) * 34 + 2 + 2 * (u % 16));
+    else R.w[i] = *(const uint16_t*)(base + 2 + 2 * u);
+  }
+  if (tid < TN * w_scales<FMT>()) {   // waves 0 (Q2/Q1) or 0-3 (Q8): uniform
+    const int rr = tid / w_scales<FMT>(), b = tid % w_scales<FMT>(), r = min(r0 + rr, n - 1);
+    R.ws = *(const uint16_t*)(w + (size_t)r * row_bytes + (size_t)kb * step_bytes + 34 * b);
   }
 }
 
 template <int FMT>
-__global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, const uint8_t* __restrict__ x,
-                                              float* __restrict__ out, int n, int K, int seq) {
+HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + NTG * i, t = idx >> 3, piece = idx & 7;
+    *(uint4*)(st.a + t * AROW + 16 * piece) = R.a[i];
+  }
+  st.da[tid] = R.ad;                                // [t][sub], t = tid / 4
+  constexpr int CU = w_code_units<FMT>();
+#pragma unroll
+  for (int i = 0; i < w_regs<FMT>(); ++i) {
+    const int idx = tid + NTG * i;
+    if (idx < TN * CU) {   // Q2: 1024, Q1: 512, Q8: 4096 = whole multiples of 512
+      const int rr = idx / CU, u = idx % CU;
+      const uint32_t v = R.w[i];
+      if constexpr (FMT == FMT_Q2) {
+        *(uint2*)(st.w + rr * AROW + 8 * u) = make_uint2(q2_spread4(v & 0xffu), q2_spread4(v >> 8));
+      } else if constexpr (FMT == FMT_Q1) {
+        *(uint4*)(st.w + rr * AROW + 16 * u) = make_uint4(q1_spread4(v & 0xfu), q1_spread4((v >> 4) & 0xfu),
+                                                          q1_spread4((v >> 8) & 0xfu), q1_spread4((v >> 12) & 0xfu));
+      } else {
+        *(uint16_t*)(st.w + rr * AROW + 32 * (u / 16) + 2 * (u % 16)) = (uint16_t)v;
+      }
+    }
+  }
+  if (tid < TN * w_scales<FMT>()) {
+    const int rr = tid / w_scales<FMT>(), b = tid % w_scales<FMT>();
+    st.dw[rr * 4 + b] = h2f(R.ws);
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
+                                              const float* __restrict__ xd, float* __restrict__ out, int n, int K,
+                                              int seq) {
 #pragma clang fp contract(off)
   __shared__ Stage st[2];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -168,7 +149,7 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
     for (int r = 0; r < 4; ++r) { sum[t][r] = 0.0f; bacc[t][r] = 0.0f; }
 
   Regs<FMT> R;
-  stage_load<FMT>(R, w, x, n, seq, K, r0, s0, 0);
+  stage_load<FMT>(R, w, xq, xd, n, seq, K, r0, s0, 0);
   stage_store<FMT>(st[0], R);
   __syncthreads();
   const int arow = 16 * wid + (lane & 15);   // A operand token (within the tile)
@@ -177,7 +158,7 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
   for (int kb = 0; kb < nsteps; ++kb) {
     const int cur = kb & 1;
     const bool more = kb + 1 < nsteps;
-    if (more) stage_load<FMT>(R, w, x, n, seq, K, r0, s0, kb + 1);
+    if (more) stage_load<FMT>(R, w, xq, xd, n, seq, K, r0, s0, kb + 1);
     const Stage& S = st[cur];
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
@@ -226,16 +207,34 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
   }
 }
 
+// Standard Q8_0 rows -> split layout (int8 [seq][K], f32 scales [seq][K/32]).
+__global__ void k_q8_split(const uint8_t* __restrict__ x, int64_t nblocks, int8_t* __restrict__ xq,
+                           float* __restrict__ xd) {
+  const int64_t b = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int l = threadIdx.x & 31;
+  if (b >= nblocks) return;
+  const uint8_t* blk = x + b * 34;
+  xq[b * 32 + l] = (int8_t)blk[2 + l];
+  if (l == 0) xd[b] = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+}
+
 }  // namespace
 
-int hh_gemm_launch(int fmt, const uint8_t* w, int n, int K, const uint8_t* x, int seq, float* out, hipStream_t s) {
+int hh_gemm_launch(int fmt, const uint8_t* w, int n, int K, const int8_t* xq, const float* xd, int seq, float* out,
+                   hipStream_t s) {
   if (K % KS != 0 || n <= 0 || seq <= 0) return 1;
   dim3 grid((n + TN - 1) / TN, (seq + TM - 1) / TM);
   switch (fmt) {
-    case FMT_Q2: hipLaunchKernelGGL(k_gemm<FMT_Q2>, grid, dim3(NTG), 0, s, w, x, out, n, K, seq); break;
-    case FMT_Q1: hipLaunchKernelGGL(k_gemm<FMT_Q1>, grid, dim3(NTG), 0, s, w, x, out, n, K, seq); break;
-    case FMT_Q8: hipLaunchKernelGGL(k_gemm<FMT_Q8>, grid, dim3(NTG), 0, s, w, x, out, n, K, seq); break;
+    case FMT_Q2: hipLaunchKernelGGL(k_gemm<FMT_Q2>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
+    case FMT_Q1: hipLaunchKernelGGL(k_gemm<FMT_Q1>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
+    case FMT_Q8: hipLaunchKernelGGL(k_gemm<FMT_Q8>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
     default: return 1;
   }
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+int hh_q8_split_launch(const uint8_t* x, int64_t nblocks, int8_t* xq, float* xd, hipStream_t s) {
+  if (nblocks <= 0) return 0;
+  hipLaunchKernelGGL(k_q8_split, dim3((unsigned)((nblocks + 7) / 8)), dim3(256), 0, s, x, nblocks, xq, xd);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }

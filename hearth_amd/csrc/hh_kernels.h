@@ -72,18 +72,23 @@ int hh_attn_launch(const AttnArgs& a, hipStream_t s);
 
 // Batched prefill row kernels (hh_ops.hip).
 int hh_embed_rows_launch(int type, const uint8_t* table, int d, const uint32_t* toks, int S, float* H, hipStream_t s);
-int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int S, uint8_t* out, hipStream_t s);
-int hh_silu_q8_rows_launch(const float* GU, int F, int S, uint8_t* out, hipStream_t s);
+// Row Q8_0 outputs use the GEMM's split layout: int8 xq[S][K], f32 scales xd[S][K/32].
+int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int S, int8_t* xq, float* xd,
+                           hipStream_t s);
+int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, hipStream_t s);
 int hh_add_rows_launch(float* H, const float* T, int64_t n, hipStream_t s);
 int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_kv, const float* q_norm,
                          const float* k_norm, float eps, const float* rope, int rope_dim, int max_seq, int pos0, int S,
                          float* k_cache, float* v_cache, float* QB, hipStream_t s);
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
-                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML, uint8_t* Y,
-                           hipStream_t s);
+                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML, int8_t* yq,
+                           float* yd, hipStream_t s);
 
-// Batched Q8_0 GEMM on int8 MFMA (prefill): out[s*n + r], K % 128 == 0.
-int hh_gemm_launch(int fmt, const uint8_t* w, int n, int K, const uint8_t* x, int seq, float* out, hipStream_t s);
+// Batched Q8_0 GEMM on int8 MFMA (prefill): out[s*n + r], K % 128 == 0, activations
+// split (int8 xq[seq][K], f32 xd[seq][K/32]); hh_q8_split_launch converts standard Q8_0 rows.
+int hh_gemm_launch(int fmt, const uint8_t* w, int n, int K, const int8_t* xq, const float* xd, int seq, float* out,
+                   hipStream_t s);
+int hh_q8_split_launch(const uint8_t* x, int64_t nblocks, int8_t* xq, float* xd, hipStream_t s);
 
 int hh_quantize_launch(const float* x, int64_t n, uint8_t* out, hipStream_t s);
 int hh_dequant_launch(int type, const void* w, int64_t n, float* out, hipStream_t s);

@@ -479,15 +479,15 @@ __global__ __launch_bounds__(256) void k_embed_rows(int type, const uint8_t* __r
   for (int i = threadIdx.x; i < d; i += 256) H[(size_t)s * d + i] = embed_value(type, table, d, tok, i);
 }
 
-// rms_norm(x_s, w) then Q8_0 into standard blocks, row s = blockIdx.x: the
-// GEMV prologue's arithmetic (block_sumsq_f4 order, (x * inv) * w, per-block
-// scale from the max of |v|, reciprocal rounding with the exact tie fallback).
+// rms_norm(x_s, w) then Q8_0 of row s = blockIdx.x into the GEMM's split
+// layout (int8 xq[s][K], f32 block scales xd[s][K/32]): the GEMV prologue's
+// arithmetic (block_sumsq_f4 order, (x * inv) * w, per-block scale from the max
+// of |v|, reciprocal rounding with the exact tie fallback).
 __global__ __launch_bounds__(256) void k_norm_q8_rows(const float* __restrict__ X, const float* __restrict__ w,
-                                                      float eps, int K, uint8_t* __restrict__ out) {
+                                                      float eps, int K, int8_t* __restrict__ xq, float* __restrict__ xd) {
   __shared__ float red16[16];
   const int s = blockIdx.x, tid = threadIdx.x;
   const float* x = X + (size_t)s * K;
-  uint8_t* o = out + (size_t)s * (K / 32) * 34;
   const float tot = block_sumsq_f4(x, K, red16);
   const float inv = 1.0f / sqrtf(tot / (float)K + eps);   // ops.rs:22-23
   for (int e = tid * 4; e < K; e += 1024) {
@@ -496,23 +496,20 @@ __global__ __launch_bounds__(256) void k_norm_q8_rows(const float* __restrict__ 
     float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
     am = group_max<8>(am);
     const float sc = q8_scale(am), rc = q8_rcp(sc);
-    uint8_t* blk = o + (size_t)(e >> 5) * 34;
+    uint32_t word = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) blk[2 + ((e + i) & 31)] = (uint8_t)(int8_t)q8_round_r(vv[i], sc, rc);
-    if ((tid & 7) == 0) {
-      const uint32_t h = f2h(sc);
-      blk[0] = (uint8_t)(h & 0xff);
-      blk[1] = (uint8_t)(h >> 8);
-    }
+    for (int i = 0; i < 4; ++i) word |= ((uint32_t)q8_round_r(vv[i], sc, rc) & 0xffu) << (8 * i);
+    *(uint32_t*)(xq + (size_t)s * K + e) = word;
+    if ((tid & 7) == 0) xd[(size_t)s * (K / 32) + (e >> 5)] = h2f(f2h(sc));
   }
 }
 
-// silu(g) * u of the [gate; up] rows of token s, then Q8_0 into standard
-// blocks: the SILU epilogue's arithmetic (ops.rs:240-253, q8_0.rs:20-51).
-__global__ __launch_bounds__(256) void k_silu_q8_rows(const float* __restrict__ GU, int F, uint8_t* __restrict__ out) {
+// silu(g) * u of the [gate; up] rows of token s, then Q8_0 into the split
+// layout: the SILU epilogue's arithmetic (ops.rs:240-253, q8_0.rs:20-51).
+__global__ __launch_bounds__(256) void k_silu_q8_rows(const float* __restrict__ GU, int F, int8_t* __restrict__ xq,
+                                                      float* __restrict__ xd) {
   const int s = blockIdx.x, tid = threadIdx.x;
   const float* g = GU + (size_t)s * 2 * F;
-  uint8_t* o = out + (size_t)s * (F / 32) * 34;
   for (int i = tid; i < F; i += 256) {   // F % 256 == 0: whole waves
     const float gv = g[i];
     const float sg = gv / (1.0f + hx_exp(-gv));
@@ -520,13 +517,8 @@ __global__ __launch_bounds__(256) void k_silu_q8_rows(const float* __restrict__ 
     const float am = group_max<32>(fabsf(h));
     const float sc = q8_scale(am);
     const int q = q8_round_r(h, sc, q8_rcp(sc));
-    uint8_t* blk = o + (size_t)(i >> 5) * 34;
-    blk[2 + (i & 31)] = (uint8_t)(int8_t)q;
-    if ((i & 31) == 0) {
-      const uint32_t hb = f2h(sc);
-      blk[0] = (uint8_t)(hb & 0xff);
-      blk[1] = (uint8_t)(hb >> 8);
-    }
+    xq[(size_t)s * F + i] = (int8_t)q;
+    if ((i & 31) == 0) xd[(size_t)s * (F / 32) + (i >> 5)] = h2f(f2h(sc));
   }
 }
 
@@ -711,11 +703,11 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
 
 // Prefill attention, merge pass: k_attn_merge's arithmetic for token t0 + sl
 // (blockIdx.x = sl * n_heads + qh), writing the Q8_0 row of attn_output's
-// input in standard blocks.
+// input in the GEMM's split layout.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restrict__ PO, const float* __restrict__ PML,
                                                             int n_heads, int n_kv, int n_chunks, int pos0, int t0,
-                                                            uint8_t* __restrict__ Y) {
+                                                            int8_t* __restrict__ yq, float* __restrict__ yd) {
   extern __shared__ __align__(16) float wm[];
   float* wts = wm;                         // n_chunks
   float* pw = wm + n_chunks;               // 4 x 64
@@ -773,13 +765,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restr
   const float scq = q8_scale(am);
   const int q = q8_round_r(o, scq, q8_rcp(scq));
   const int e = qh * HD + d, K = n_heads * HD;
-  uint8_t* blk = Y + (size_t)s * (K / 32) * 34 + (size_t)(e >> 5) * 34;
-  blk[2 + (e & 31)] = (uint8_t)(int8_t)q;
-  if ((lane & 31) == 0) {
-    const uint32_t hbits = f2h(scq);
-    blk[0] = (uint8_t)(hbits & 0xff);
-    blk[1] = (uint8_t)(hbits >> 8);
-  }
+  yq[(size_t)s * K + e] = (int8_t)q;
+  if ((lane & 31) == 0) yd[(size_t)s * (K / 32) + (e >> 5)] = h2f(f2h(scq));
 }
 
 // ---------------------------------------------------------------------------
@@ -1037,15 +1024,16 @@ int hh_embed_rows_launch(int type, const uint8_t* table, int d, const uint32_t* 
   return ok();
 }
 
-int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int S, uint8_t* out, hipStream_t s) {
+int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int S, int8_t* xq, float* xd,
+                           hipStream_t s) {
   if (K % 1024 != 0) return 1;
-  hipLaunchKernelGGL(k_norm_q8_rows, dim3(S), dim3(256), 0, s, X, w, eps, K, out);
+  hipLaunchKernelGGL(k_norm_q8_rows, dim3(S), dim3(256), 0, s, X, w, eps, K, xq, xd);
   return ok();
 }
 
-int hh_silu_q8_rows_launch(const float* GU, int F, int S, uint8_t* out, hipStream_t s) {
+int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, hipStream_t s) {
   if (F % 256 != 0) return 1;
-  hipLaunchKernelGGL(k_silu_q8_rows, dim3(S), dim3(256), 0, s, GU, F, out);
+  hipLaunchKernelGGL(k_silu_q8_rows, dim3(S), dim3(256), 0, s, GU, F, xq, xd);
   return ok();
 }
 
@@ -1071,8 +1059,8 @@ int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_
 
 // Attention for tokens [t0, t0 + n) of a prefill; PO/PML hold n tokens' partials.
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
-                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML, uint8_t* Y,
-                           hipStream_t s) {
+                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML, int8_t* yq,
+                           float* yd, hipStream_t s) {
   const int G = n_heads / n_kv, TT = 16;
   if (G > 8 || n_kv * G != n_heads) return 1;
   const size_t split_lds = 4 * ((size_t)G * (8192 / hd) + 2 * G + 4 + (ATTN_NT / 64) * 4 * (size_t)hd);
@@ -1082,12 +1070,12 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
     hipLaunchKernelGGL((k_attn_prefill_split<128, ATTN_NT>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, v_cache,
                        n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML);
     hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, Y);
+                       t0, yq, yd);
   } else if (hd == 256) {
     hipLaunchKernelGGL((k_attn_prefill_split<256, ATTN_NT>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, v_cache,
                        n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML);
     hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, Y);
+                       t0, yq, yd);
   } else {
     return 1;
   }

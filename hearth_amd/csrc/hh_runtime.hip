@@ -89,6 +89,8 @@ struct hh_ctx {
   hipEvent_t ev[8] = {};
   void* attn_scratch = nullptr;     // standalone attention partials + counters
   size_t attn_scratch_bytes = 0;
+  void* gemm_scratch = nullptr;     // standalone GEMM: activations in split layout
+  size_t gemm_scratch_bytes = 0;
 };
 
 namespace {
@@ -397,12 +399,13 @@ int prefill_dense(hh_model* m, const uint32_t* toks, int S, int pos0) {
   const int wt = c.wtype;
   const int TA = 128;                              // attention tokens per pass
   const int n_chunks = m->attn_splits, G = c.n_heads / c.n_kv_heads;
-  auto q8b = [](long long K) { return (size_t)(K / 32) * 34; };
   // scratch layout
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
-  const size_t oH = take((size_t)S * d * 4), oX = take((size_t)S * q8b(std::max(d, F))),
-               oQKV = take((size_t)S * n_in * 4), oQB = take((size_t)S * nq * 4), oA = take((size_t)S * q8b(nq)),
+  const size_t oH = take((size_t)S * d * 4), oXq = take((size_t)S * std::max(d, F)),
+               oXd = take((size_t)S * (std::max(d, F) / 32) * 4),
+               oQKV = take((size_t)S * n_in * 4), oQB = take((size_t)S * nq * 4), oAq = take((size_t)S * nq),
+               oAd = take((size_t)S * (nq / 32) * 4),
                oT = take((size_t)S * d * 4), oGU = take((size_t)S * 2 * F * 4),
                oPO = take((size_t)TA * c.n_kv_heads * n_chunks * G * hd * 4),
                oPML = take((size_t)TA * c.n_kv_heads * n_chunks * G * 2 * 4);
@@ -415,10 +418,12 @@ int prefill_dense(hh_model* m, const uint32_t* toks, int S, int pos0) {
   }
   uint8_t* B = m->pf_buf;
   float* H = (float*)(B + oH);
-  uint8_t* X = B + oX;
+  int8_t* Xq = (int8_t*)(B + oXq);
+  float* Xd = (float*)(B + oXd);
   float* QKV = (float*)(B + oQKV);
   float* QB = (float*)(B + oQB);
-  uint8_t* A = B + oA;
+  int8_t* Aq = (int8_t*)(B + oAq);
+  float* Ad = (float*)(B + oAd);
   float* T = (float*)(B + oT);
   float* GU = (float*)(B + oGU);
   float* PO = (float*)(B + oPO);
@@ -426,20 +431,20 @@ int prefill_dense(hh_model* m, const uint32_t* toks, int S, int pos0) {
   KTRY(hh_embed_rows_launch(c.head_type, m->token_embd->d, d, toks, S, H, s));
   for (int li = 0; li < c.n_layers; ++li) {
     Layer& L = m->layers[li];
-    KTRY(hh_norm_q8_rows_launch(H, L.attn_norm, c.eps, d, S, X, s));
-    KTRY(hh_gemm_launch(m->wfmt, L.w_in, n_in, d, X, S, QKV, s));
+    KTRY(hh_norm_q8_rows_launch(H, L.attn_norm, c.eps, d, S, Xq, Xd, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_in, n_in, d, Xq, Xd, S, QKV, s));
     KTRY(hh_prefill_qk_launch(hd, QKV, n_in, c.n_heads, c.n_kv_heads, c.qk_norm ? L.q_norm : nullptr,
                               c.qk_norm ? L.k_norm : nullptr, c.eps, m->rope, m->rope_dim, c.max_seq, pos0, S,
                               L.k_cache, L.v_cache, QB, s));
     for (int t0 = 0; t0 < S; t0 += TA)
       KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, c.max_seq, pos0, t0,
-                                  std::min(TA, S - t0), n_chunks, PO, PML, A, s));
-    KTRY(hh_gemm_launch(m->wfmt, L.w_out, d, nq, A, S, T, s));
+                                  std::min(TA, S - t0), n_chunks, PO, PML, Aq, Ad, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_out, d, nq, Aq, Ad, S, T, s));
     KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
-    KTRY(hh_norm_q8_rows_launch(H, L.ffn_norm, c.eps, d, S, X, s));
-    KTRY(hh_gemm_launch(m->wfmt, L.w_gu, 2 * F, d, X, S, GU, s));
-    KTRY(hh_silu_q8_rows_launch(GU, F, S, X, s));
-    KTRY(hh_gemm_launch(m->wfmt, L.w_down, d, F, X, S, T, s));
+    KTRY(hh_norm_q8_rows_launch(H, L.ffn_norm, c.eps, d, S, Xq, Xd, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_gu, 2 * F, d, Xq, Xd, S, GU, s));
+    KTRY(hh_silu_q8_rows_launch(GU, F, S, Xq, Xd, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_down, d, F, Xq, Xd, S, T, s));
     KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
   }
   (void)wt;
@@ -479,6 +484,7 @@ int hh_ctx_destroy(hh_ctx* c) {
   hipFree(c->counter);
   if (c->counts) hipFree(c->counts);
   if (c->attn_scratch) hipFree(c->attn_scratch);
+  if (c->gemm_scratch) hipFree(c->gemm_scratch);
   for (hipEvent_t e : c->ev)
     if (e) hipEventDestroy(e);
   hipStreamDestroy(c->stream);
@@ -579,7 +585,20 @@ int hh_gemm_q8(hh_ctx* c, int type, const void* w, int64_t n_rows, int64_t n_col
   if (n_rows <= 0 || n_rows > (1ll << 30) || seq_len <= 0 || seq_len > (1ll << 24))
     return fail(HH_ERR_DIM, "bad n_rows or seq_len");
   if ((n_rows + 63) / 64 > 2147483647ll || (seq_len + 63) / 64 > 65535) return fail(HH_ERR_DIM, "grid too large");
-  KTRY(hh_gemm_launch(fmt, (const uint8_t*)w, (int)n_rows, (int)n_cols, xq8, (int)seq_len, out, c->stream));
+  // the GEMM reads its activations as int8 rows plus f32 block scales
+  const size_t nq = (size_t)seq_len * n_cols, need = align256(nq) + nq / 32 * 4;
+  if (c->gemm_scratch_bytes < need) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->gemm_scratch) HIP_TRY(hipFree(c->gemm_scratch));
+    c->gemm_scratch = nullptr;
+    c->gemm_scratch_bytes = 0;
+    HIP_TRY(hipMalloc(&c->gemm_scratch, need));
+    c->gemm_scratch_bytes = need;
+  }
+  int8_t* xq = (int8_t*)c->gemm_scratch;
+  float* xd = (float*)((char*)c->gemm_scratch + align256(nq));
+  KTRY(hh_q8_split_launch(xq8, (int64_t)(nq / 32), xq, xd, c->stream));
+  KTRY(hh_gemm_launch(fmt, (const uint8_t*)w, (int)n_rows, (int)n_cols, xq, xd, (int)seq_len, out, c->stream));
   return HH_OK;
 }
 
