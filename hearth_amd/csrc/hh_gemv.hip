@@ -192,96 +192,146 @@ template <int FMT> HH_DEV void put_ds(float* ds, int blk32, float d, int s) {
 // repeats, and 16 waves hide its instruction latencies.
 constexpr int NT = 1024;
 
-// PRO_RMSNORM: rms_norm(x, w) then Q8_0.  Lane t owns the float4s at
-// 4t + 4096c (c < NORM_CH).  Sum of squares in the order of block_sumsq_f4:
-// slot t sums its float4s in c order as ss + (((x0^2 + x1^2) + x2^2) + x3^2),
-// waves reduce by butterfly, the 16 wave sums by tree16.  All prologue loads
-// precede the weight loads, so their conditions never delay a weight.
+// The RMSNorm prologue runs in the first NORM_L lanes (waves 0-3) and its
+// sum of squares is complete before any wave issues a weight load: the
+// activation read then meets an idle memory system instead of queueing behind
+// the whole chip's weight stream (measured on the 8B gate+up: 13.3 -> 12.2 us).
+// The packed prologue (a plain copy) is staged by every lane and overlaps the
+// weight loads.
+constexpr int NORM_L = 256;
+constexpr int PK_L = NT;
+
+// PRO_RMSNORM: rms_norm(x, w) then Q8_0, in lanes t < NORM_L.  Slot s
+// (s < 1024) owns the float4s at 4s + 4096c (c < NORM_CH); lane t runs slots
+// t + NORM_L*j (j < NJ).  Sum of squares in the order of block_sumsq_f4:
+// slot s sums its float4s in c order as ss + (((x0^2 + x1^2) + x2^2) + x3^2),
+// slots 64w .. 64w+63 reduce by butterfly into W_w, the total is tree16(W).
 constexpr int NORM_CH = 2;   // K <= 8192
-struct NormRegs { float4 x[NORM_CH], w[NORM_CH]; };
+constexpr int NJ = 1024 / NORM_L;
+struct NormRegs { float4 x[NJ][NORM_CH], w[NJ][NORM_CH]; };
 
 HH_DEV void norm_issue(const GemvArgs& p, NormRegs& r) {
   const int tid = threadIdx.x;
+  if (tid >= NORM_L) return;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int c = 0; c < NORM_CH; ++c) {
+      const int e = (tid + NORM_L * j) * 4 + 4096 * c;
+      if (e < p.K) {
+        r.x[j][c] = *(const float4*)(p.x + e);
+        r.w[j][c] = *(const float4*)(p.norm_w + e);
+      }
+    }
+}
+
+HH_DEV void norm_partial(const GemvArgs& p, const NormRegs& r, float* red) {
+  const int tid = threadIdx.x;
+  if (tid >= NORM_L) return;
+  float ss[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    ss[j] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NORM_CH; ++c)
+      if ((tid + NORM_L * j) * 4 + 4096 * c < p.K)
+        ss[j] += r.x[j][c].x * r.x[j][c].x + r.x[j][c].y * r.x[j][c].y + r.x[j][c].z * r.x[j][c].z +
+                 r.x[j][c].w * r.x[j][c].w;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) ss[j] = wave_sum(ss[j]);
+  if ((tid & 63) == 0) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) red[(tid >> 6) + (NORM_L / 64) * j] = ss[j];
+  }
+}
+
+template <int FMT>
+HH_DEV void norm_finish(const GemvArgs& p, const NormRegs& r, int8_t* aq, float* ds, const float* red) {
+  const int tid = threadIdx.x;
+  if (tid >= NORM_L) return;
+  const int K = p.K;
+  const float tot = tree16(red);
+  const float inv = 1.0f / sqrtf(tot / (float)K + p.eps);   // ops.rs:22-23
 #pragma unroll
   for (int c = 0; c < NORM_CH; ++c) {
-    const int e = tid * 4 + c * 4096;
-    if (e < p.K) {
-      r.x[c] = *(const float4*)(p.x + e);
-      r.w[c] = *(const float4*)(p.norm_w + e);
+    if (c > 0 && 4096 * c >= K) break;   // uniform: whole chunk absent
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int e = (tid + NORM_L * j) * 4 + 4096 * c;
+      if (4096 * c + NORM_L * j * 4 >= K) break;   // uniform
+      const bool in = e < K;
+      float vv[4] = {r.x[j][c].x * inv * r.w[j][c].x, r.x[j][c].y * inv * r.w[j][c].y,   // ops.rs:29 (x * inv) * w
+                     r.x[j][c].z * inv * r.w[j][c].z, r.x[j][c].w * inv * r.w[j][c].w};
+      float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+      am = group_max<8>(am);
+      const float sc = q8_scale(am), rc = q8_rcp(sc);
+      int qs = 0;
+      uint32_t word = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int q = q8_round_r(vv[i], sc, rc);
+        qs += q;
+        word |= ((uint32_t)q & 0xffu) << (8 * i);
+      }
+      qs = group_sum_i<8>(qs);
+      if (in) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)(word >> (8 * i));
+        if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
+      }
     }
   }
 }
 
 template <int FMT>
 HH_DEV void norm_store(const GemvArgs& p, const NormRegs& r, int8_t* aq, float* ds, float* red) {
-  const int tid = threadIdx.x;
-  const int K = p.K;
-  float ss = 0.0f;
-#pragma unroll
-  for (int c = 0; c < NORM_CH; ++c)
-    if (tid * 4 + c * 4096 < K)
-      ss += r.x[c].x * r.x[c].x + r.x[c].y * r.x[c].y + r.x[c].z * r.x[c].z + r.x[c].w * r.x[c].w;
-  ss = wave_sum(ss);
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  norm_partial(p, r, red);
   __syncthreads();
-  const float tot = tree16(red);
-  const float inv = 1.0f / sqrtf(tot / (float)K + p.eps);   // ops.rs:22-23
-#pragma unroll
-  for (int c = 0; c < NORM_CH; ++c) {
-    const int e = tid * 4 + c * 4096;
-    if (c > 0 && 4096 * c >= K) break;   // uniform: whole chunk absent
-    const bool in = e < K;
-    float vv[4] = {r.x[c].x * inv * r.w[c].x, r.x[c].y * inv * r.w[c].y,   // ops.rs:29 (x * inv) * w
-                   r.x[c].z * inv * r.w[c].z, r.x[c].w * inv * r.w[c].w};
-    float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
-    am = group_max<8>(am);
-    const float sc = q8_scale(am), rc = q8_rcp(sc);
-    int qs = 0;
-    uint32_t word = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int q = q8_round_r(vv[i], sc, rc);
-      qs += q;
-      word |= ((uint32_t)q & 0xffu) << (8 * i);
-    }
-    qs = group_sum_i<8>(qs);
-    if (in) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)(word >> (8 * i));
-      if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
-    }
-  }
+  norm_finish<FMT>(p, r, aq, ds, red);
 }
 
-// PRO_PACKED: packed activation [q K][d K/32][s K/32] from a producer kernel.
-constexpr int PK_Q = 2;   // 16-byte chunks per lane: K <= 32768
-struct PackedRegs { i32x4 q[PK_Q]; float d; int s; };
+// PRO_PACKED: packed activation [q K][d K/32][s K/32] from a producer kernel,
+// staged by lanes t < PK_L.
+constexpr int PK_Q = 32768 / 16 / PK_L;   // 16-byte chunks per lane: K <= 32768
+constexpr int PK_D = 1024 / PK_L;
+struct PackedRegs { i32x4 q[PK_Q]; float d[PK_D]; int s[PK_D]; };
 
 HH_DEV void packed_issue(const GemvArgs& p, PackedRegs& r) {
   const int tid = threadIdx.x, K = p.K;
+  if (tid >= PK_L) return;
 #pragma unroll
   for (int i = 0; i < PK_Q; ++i) {
-    int c = tid + NT * i;
+    int c = tid + PK_L * i;
     if (c < K / 16) r.q[i] = *(const i32x4*)(p.act + c * 16);
   }
-  if (tid < K / 32) {
-    r.d = ((const float*)(p.act + K))[tid];
-    r.s = ((const int*)(p.act + K + (K / 32) * 4))[tid];
+#pragma unroll
+  for (int i = 0; i < PK_D; ++i) {
+    int b = tid + PK_L * i;
+    if (b < K / 32) {
+      r.d[i] = ((const float*)(p.act + K))[b];
+      r.s[i] = ((const int*)(p.act + K + (K / 32) * 4))[b];
+    }
   }
 }
 
 template <int FMT> HH_DEV void packed_store(const GemvArgs& p, const PackedRegs& r, int8_t* aq, float* ds) {
   const int tid = threadIdx.x, K = p.K;
+  if (tid >= PK_L) return;
   constexpr int EL = UnitT<FMT>::EL;
 #pragma unroll
   for (int i = 0; i < PK_Q; ++i) {
-    int c = tid + NT * i;
+    int c = tid + PK_L * i;
     if (c < K / 16) {
       int e = c * 16;
       *(i32x4*)(aq + (e / EL) * qstride<FMT>() + (e % EL)) = r.q[i];
     }
   }
-  if (tid < K / 32) put_ds<FMT>(ds, tid, r.d, r.s);
+#pragma unroll
+  for (int i = 0; i < PK_D; ++i) {
+    int b = tid + PK_L * i;
+    if (b < K / 32) put_ds<FMT>(ds, b, r.d[i], r.s[i]);
+  }
 }
 
 // PRO_STDQ8: standard Q8_0 blocks (DotFn activation format), K <= 20480.
@@ -325,6 +375,8 @@ template <int FMT> struct ActStage<FMT, PRO_RMSNORM> {
   NormRegs r;
   HH_DEV void issue(const GemvArgs& p) { norm_issue(p, r); }
   HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT>(p, r, aq, ds, red); }
+  HH_DEV void part1(const GemvArgs& p, int8_t*, float*, float* red) { norm_partial(p, r, red); }
+  HH_DEV void part2(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_finish<FMT>(p, r, aq, ds, red); }
 };
 template <int FMT> struct ActStage<FMT, PRO_PACKED> {
   PackedRegs r;
@@ -426,7 +478,14 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
 
   ActStage<FMT, PRO> act;
   act.issue(p);                      // activation first (in-order retirement)
-  if constexpr (NU > 0) {
+  if constexpr (NU > 0 && PRO == PRO_RMSNORM) {
+    act.part1(p, aq, ds, red);       // waits for this lane's activation loads
+    __syncthreads();
+    load_batch(wa, 0);               // the whole share of this lane
+    act.part2(p, aq, ds, red);
+    __syncthreads();
+    comp_batch(wa, 0);
+  } else if constexpr (NU > 0) {
     load_batch(wa, 0);               // the whole share of this lane
     act.store(p, aq, ds, red);
     __syncthreads();
@@ -729,7 +788,7 @@ template <int FMT>
 int launch_p(const GemvArgs& a, int pro, int epi, int nu, int n_wg, size_t lds, hipStream_t s) {
   switch (pro) {
     case PRO_PACKED:
-      if (a.K > PK_Q * 16 * NT) return 1;
+      if (a.K > PK_Q * 16 * PK_L) return 1;
       if (epi == EPI_ADD) return launch_u<FMT, PRO_PACKED, EPI_ADD>(a, nu, n_wg, lds, s);
       if (epi == EPI_STORE) return launch_u<FMT, PRO_PACKED, EPI_STORE>(a, nu, n_wg, lds, s);
       return 1;
@@ -738,7 +797,7 @@ int launch_p(const GemvArgs& a, int pro, int epi, int nu, int n_wg, size_t lds, 
       if (epi == EPI_STORE) return launch_u<FMT, PRO_STDQ8, EPI_STORE>(a, nu, n_wg, lds, s);
       return 1;
     case PRO_RMSNORM:
-      if (a.K % 1024 != 0 || a.K > NORM_CH * 4 * NT) return 1;
+      if (a.K % 1024 != 0 || a.K > NORM_CH * 4096) return 1;
       if (epi == EPI_STORE) return launch_u<FMT, PRO_RMSNORM, EPI_STORE>(a, nu, n_wg, lds, s);
       if (epi == EPI_SILU) return launch_u<FMT, PRO_RMSNORM, EPI_SILU>(a, nu, n_wg, lds, s);
       return 1;
@@ -775,7 +834,7 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   a.P = a.K / el;
   int n_wg, rows_total;
   if (epi == EPI_LOGITS) {   // persistent row-streaming head + finalize
-    if (pro != PRO_RMSNORM || a.K % 1024 != 0 || a.K > NORM_CH * 4 * NT) return 1;
+    if (pro != PRO_RMSNORM || a.K % 1024 != 0 || a.K > NORM_CH * 4096) return 1;
     int rc = 1;
     switch (fmt) {
       case FMT_Q2: rc = launch_head<FMT_Q2>(a, s, &n_wg); break;
