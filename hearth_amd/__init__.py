@@ -9,6 +9,7 @@ from .lib import (  # noqa: F401
     HHError,
     Ctx,
     Model,
+    Gguf,
     ModelConfig,
     CONFIGS,
     GGML_F32,

@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = ["hh_gemv.hip", "hh_gemm.hip", "hh_ops.hip", "hh_gdn.hip", "hh_runtime.hip"]
+SOURCES = ["hh_gemv.hip", "hh_gemm.hip", "hh_ops.hip", "hh_gdn.hip", "hh_runtime.hip", "hh_gguf.cpp"]
 LIB = os.path.join(HERE, "libhearth_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -28,7 +28,7 @@ FLAGS = [
 def build(verbose: bool = False) -> str:
     objs = []
     for src in SOURCES:
-        obj = os.path.join(CSRC, src.replace(".hip", ".o"))
+        obj = os.path.join(CSRC, os.path.splitext(src)[0] + ".o")
         cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)

@@ -16,16 +16,21 @@
 #include <vector>
 
 #include "../../include/hearth_hip.h"
+#include "hh_host.h"
 #include "hh_kernels.h"
 
 namespace {
-
 thread_local std::string g_err;
+}  // namespace
 
-int fail(int code, const std::string& msg) {
+int hh_set_error(int code, const std::string& msg) {
   g_err = msg;
   return code;
 }
+
+namespace {
+
+int fail(int code, const std::string& msg) { return hh_set_error(code, msg); }
 
 #define HIP_TRY(expr)                                                                \
   do {                                                                               \

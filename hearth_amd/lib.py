@@ -44,6 +44,11 @@ def row_bytes(t: int, n: int) -> int:
     raise ValueError(f"unknown ggml type {t}")
 
 
+# hh_status (include/hearth_hip.h)
+HH_OK, HH_ERR_INVALID, HH_ERR_DTYPE, HH_ERR_DIM, HH_ERR_OOM, HH_ERR_HIP, HH_ERR_NOT_FOUND, HH_ERR_RANGE, \
+    HH_ERR_CANCELLED = range(9)
+
+
 class HHError(RuntimeError):
     def __init__(self, status: int, msg: str):
         super().__init__(f"hearth_hip status {status}: {msg}")
@@ -155,6 +160,20 @@ _EXPORTS = {
     "hh_model_time_stages": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int]),
     "hh_model_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     "hh_model_last_prefill_ms": (C.c_int, [C.c_void_p, C.POINTER(C.c_double)]),
+    "hh_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "hh_gguf_close": (C.c_int, [C.c_void_p]),
+    "hh_gguf_header": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "hh_gguf_tensor_count": (C.c_int, [C.c_void_p]),
+    "hh_gguf_tensor_info": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_int),
+                                       C.POINTER(C.c_int), C.POINTER(C.c_int64), C.POINTER(C.c_uint64),
+                                       C.POINTER(C.c_uint64)]),
+    "hh_gguf_tensor_data": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p)]),
+    "hh_gguf_meta_u32": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint32)]),
+    "hh_gguf_meta_f32": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_float)]),
+    "hh_gguf_meta_str": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "hh_gguf_meta_array_len": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "hh_gguf_model_config": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(ModelConfigC)]),
+    "hh_model_load_gguf": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
 }
 
 
@@ -269,6 +288,80 @@ class Ctx:
         _check(self.lib.hh_argmax(self.h, _ptr(logits), n, _ptr(past), n_past, pen, rule, _ptr(out)))
 
 
+class Gguf:
+    """A parsed GGUF file (hh_gguf_*): header, metadata, tensor table.  Host only."""
+
+    def __init__(self, path: str, lib: Optional[C.CDLL] = None):
+        self.lib = lib or load_library()
+        h = C.c_void_p()
+        _check(self.lib.hh_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.hh_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def header(self):
+        v, off, al = C.c_uint32(), C.c_uint64(), C.c_uint64()
+        _check(self.lib.hh_gguf_header(self.h, C.byref(v), C.byref(off), C.byref(al)))
+        return v.value, off.value, al.value
+
+    def tensors(self):
+        out = []
+        for i in range(self.lib.hh_gguf_tensor_count(self.h)):
+            name, t, nd = C.c_char_p(), C.c_int(), C.c_int()
+            shape = (C.c_int64 * 4)()
+            off, nb = C.c_uint64(), C.c_uint64()
+            _check(self.lib.hh_gguf_tensor_info(self.h, i, C.byref(name), C.byref(t), C.byref(nd), shape,
+                                                C.byref(off), C.byref(nb)))
+            out.append(dict(name=name.value.decode(), type=t.value, shape=tuple(shape[:nd.value]),
+                            offset=off.value, nbytes=nb.value))
+        return out
+
+    def tensor_bytes(self, index: int, nbytes: int) -> bytes:
+        p = C.c_void_p()
+        _check(self.lib.hh_gguf_tensor_data(self.h, index, C.byref(p)))
+        return C.string_at(p, nbytes)
+
+    def meta_u32(self, key: str) -> int:
+        v = C.c_uint32()
+        _check(self.lib.hh_gguf_meta_u32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_f32(self, key: str) -> float:
+        v = C.c_float()
+        _check(self.lib.hh_gguf_meta_f32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_str(self, key: str) -> str:
+        v = C.c_char_p()
+        _check(self.lib.hh_gguf_meta_str(self.h, key.encode(), C.byref(v)))
+        return v.value.decode()
+
+    def meta_array_len(self, key: str) -> int:
+        v = C.c_uint64()
+        _check(self.lib.hh_gguf_meta_array_len(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def model_config(self, ctx_cap: int = 0) -> "ModelConfig":
+        c = ModelConfigC()
+        _check(self.lib.hh_gguf_model_config(self.h, ctx_cap, C.byref(c)))
+        return ModelConfig(**{f[0]: getattr(c, f[0]) for f in ModelConfigC._fields_})
+
+
 class Model:
     """A model resident in HBM; weights synthesized on device or uploaded."""
 
@@ -281,6 +374,21 @@ class Model:
         _check(self.lib.hh_model_create(ctx.h, C.byref(self._c), C.byref(h)))
         self.h = h
         ctx._models.add(self)
+
+    @classmethod
+    def from_gguf(cls, ctx: Ctx, path: str, ctx_cap: int = 0) -> "Model":
+        """hh_model_load_gguf: configuration derived from the file's metadata,
+        every tensor uploaded from the mapping (LlamaModel::load, mod.rs:103-150)."""
+        with Gguf(path, ctx.lib) as g:
+            cfg = g.model_config(ctx_cap)
+        self = cls.__new__(cls)
+        self.ctx, self.cfg, self.lib = ctx, cfg, ctx.lib
+        self._c = cfg.to_c()
+        h = C.c_void_p()
+        _check(self.lib.hh_model_load_gguf(ctx.h, os.fsencode(path), ctx_cap, C.byref(h)))
+        self.h = h
+        ctx._models.add(self)
+        return self
 
     def close(self) -> None:
         if self.h and self.ctx.h:

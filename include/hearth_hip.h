@@ -207,6 +207,43 @@ int hh_model_last_decode_ms(hh_model* m, double* ms);
  * outside a generation. */
 int hh_model_time_stages(hh_model* m, int layer, int iters, double* out_ms, int n_out);
 
+/* ---- GGUF files ----
+ * A GGUF v2/v3 file, memory-mapped and parsed: header, metadata and tensor table
+ * (hearth-gguf GgufFile::open, gguf.rs:138-218; tensor byte sizes from the
+ * GgmlDType block table, ggml.rs:57-171).  Errors: HH_ERR_INVALID (bad magic,
+ * unsupported version, truncated file -- GgufError, gguf.rs:12-27),
+ * HH_ERR_DTYPE (unknown dtype id), HH_ERR_NOT_FOUND (missing file or key). */
+typedef struct hh_gguf hh_gguf;
+int hh_gguf_open(const char* path, hh_gguf** out);
+int hh_gguf_close(hh_gguf* g);
+int hh_gguf_header(hh_gguf* g, uint32_t* version, uint64_t* data_offset, uint64_t* alignment);
+int hh_gguf_tensor_count(hh_gguf* g);
+/* shape4[d] = ne_d (1 past n_dims); offset is relative to the data section
+ * (TensorInfo, tensor.rs:1-24). */
+int hh_gguf_tensor_info(hh_gguf* g, int index, const char** name, int* ggml_type, int* n_dims, int64_t* shape4,
+                        uint64_t* offset, uint64_t* nbytes);
+/* Host pointer to a tensor's bytes inside the mapping (GgufFile::tensor_data, gguf.rs:220-224). */
+int hh_gguf_tensor_data(hh_gguf* g, int index, const void** data);
+/* Metadata getters with MetaValue::as_u32 / as_f32 / as_str / as_array semantics (meta.rs:26-64). */
+int hh_gguf_meta_u32(hh_gguf* g, const char* key, uint32_t* out);
+int hh_gguf_meta_f32(hh_gguf* g, const char* key, float* out);
+int hh_gguf_meta_str(hh_gguf* g, const char* key, const char** out);
+int hh_gguf_meta_array_len(hh_gguf* g, const char* key, uint64_t* out);
+/* The decode model's configuration: ModelConfig::from_gguf (config.rs:57-217,
+ * arch key prefixes :288-307), head_dim from the Q (dense, mod.rs:156-167) or
+ * K projection (qwen35.rs:475-488), the qwen35 GDN geometry (qwen35.rs:490-528)
+ * and the KV context cap (kv_budget.rs:19-58: 1.25 GiB of f32 KV, at most 4096
+ * tokens for dense models).  ctx_cap_override > 0 replaces that cap
+ * (HEARTH_CTX_CAP).  Weight formats come from the tensors: wtype from
+ * blk.0.ffn_gate.weight, head_type from token_embd.weight. */
+int hh_gguf_model_config(hh_gguf* g, int ctx_cap_override, hh_model_config* cfg);
+/* LlamaModel::load / qwen35::load for the device (mod.rs:103-150, model/gpu.rs:8-50):
+ * open, derive the configuration, create the model and upload every tensor from
+ * the mapping in its native blocks.  A missing output.weight is the tied head
+ * (mod.rs:360-364): token_embd.weight is uploaded in its place.  F16 norm/GDN
+ * vectors are widened to the f32 the decode path keeps. */
+int hh_model_load_gguf(hh_ctx* ctx, const char* path, int ctx_cap_override, hh_model** out);
+
 #ifdef __cplusplus
 }
 #endif
