@@ -19,6 +19,7 @@ from .lib import (  # noqa: F401
     GGML_Q2_0,
     GGML_Q1_0_G128,
     GGML_PQ2_0,
+    GGML_PTQ1_0,
     lib_path,
     load_library,
     row_bytes,

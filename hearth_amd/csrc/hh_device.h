@@ -23,15 +23,17 @@
 
 #define HH_DEV __device__ __forceinline__
 
-enum : int { FMT_Q8 = 0, FMT_Q1 = 1, FMT_Q2 = 2 };
+enum : int { FMT_Q8 = 0, FMT_Q1 = 1, FMT_Q2 = 2, FMT_PT = 3 };
 
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 template <int FMT> struct UnitT;
 template <> struct UnitT<FMT_Q2> { static constexpr int EL = 256, DW = 17, BYTES = 68, SUBS = 8; };
 template <> struct UnitT<FMT_Q1> { static constexpr int EL = 256, DW = 9, BYTES = 36, SUBS = 8; };
 template <> struct UnitT<FMT_Q8> { static constexpr int EL = 64, DW = 17, BYTES = 68, SUBS = 2; };
+template <> struct UnitT<FMT_PT> { static constexpr int EL = 256, DW = 14, BYTES = 56, SUBS = 8; };
 
 // LDS stride of one unit's int8 activations (16 B pad spreads units over banks).
 template <int FMT> HH_DEV constexpr int qstride() { return UnitT<FMT>::EL + 16; }
@@ -125,6 +127,7 @@ HH_DEV float hx_log(float x) {
 // Position of element e (within the vector) in the permuted int8 array.
 //   Q2: chunk of 16; element 4i+k -> k*4+i     (matches (D >> 2k) & 0x03030303)
 //   Q1: chunk of 32; element 8i+j -> j*4+i     (matches (D >> j)  & 0x01010101)
+//   PTQ1_0 and Q8_0: natural order (a PTQ1_0 slot covers consecutive elements)
 HH_DEV int perm_pos(int fmt, int e) {
   if (fmt == FMT_Q2) { int r = e & 15; return (e & ~15) | ((r & 3) << 2) | (r >> 2); }
   if (fmt == FMT_Q1) { int r = e & 31; return (e & ~31) | ((r & 7) << 2) | (r >> 3); }

@@ -58,7 +58,27 @@ HH_DEV uint32_t q1_spread4(uint32_t y) {
   return ((z << 1) + 0x7f7f7f7fu) ^ 0x80808080u;
 }
 
-template <int FMT> HH_DEV constexpr int w_code_units() { return FMT == FMT_Q2 ? 16 : FMT == FMT_Q1 ? 8 : 64; }
+// PTQ1_0 block (ptq1_0.rs:1-13) as 7 dwords: qs[24] (5 trits per byte; bytes
+// 0..15 -> elements 16n + m, 16..23 -> 80 + 8n + (m-16)), then qh[2] (4 trits,
+// elements 120 + 2n + h) and the f16 scale.  Trit n of byte b is
+// ((b*3^n mod 256)*3) >> 8, walked on two 16-bit lanes per dword.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+HH_DEV uint32_t pt_step(u16x2& lo, u16x2& hi) {   // the next slot's trits of 4 bytes, as bytes
+  const u16x2 three = {3, 3}, eight = {8, 8};
+  const u16x2 ql = lo * three, qh = hi * three;
+  const uint32_t t = __builtin_bit_cast(uint32_t, (u16x2)(ql >> eight)) |
+                     (__builtin_bit_cast(uint32_t, (u16x2)(qh >> eight)) << 8);
+  lo = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, ql) & 0x00ff00ffu);
+  hi = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, qh) & 0x00ff00ffu);
+  return t;
+}
+HH_DEV uint32_t trit_to_i8x4(uint32_t t) { return (t + 0x7f7f7f7fu) ^ 0x80808080u; }   // t - 1 per byte
+
+template <int FMT> HH_DEV constexpr int w_code_units() {
+  return FMT == FMT_Q2 ? 16 : FMT == FMT_Q1 ? 8 : FMT == FMT_PT ? 7 : 64;
+}
+template <int FMT> HH_DEV constexpr int w_block_bytes() { return FMT == FMT_Q1 ? 18 : FMT == FMT_PT ? 28 : 34; }
+template <int FMT> HH_DEV constexpr int w_scale_off() { return FMT == FMT_PT ? 26 : 0; }
 template <int FMT> HH_DEV constexpr int w_regs() { return (TN * w_code_units<FMT>() + NTG - 1) / NTG; }
 template <int FMT> HH_DEV constexpr int w_scales() { return FMT == FMT_Q8 ? 4 : 1; }   // per row per step
 
@@ -85,19 +105,20 @@ HH_DEV void stage_load(Regs<FMT>& R, const uint8_t* __restrict__ w, const int8_t
     R.ad = xd[(size_t)sidx * (K / 32) + kb * 4 + sub];
   }
   constexpr int CU = w_code_units<FMT>();
-  const size_t row_bytes = (size_t)K / (FMT == FMT_Q8 ? 32 : 128) * (FMT == FMT_Q8 ? 34 : FMT == FMT_Q2 ? 34 : 18);
-  const size_t step_bytes = FMT == FMT_Q8 ? 136 : FMT == FMT_Q2 ? 34 : 18;
+  const size_t row_bytes = (size_t)K / (FMT == FMT_Q8 ? 32 : 128) * w_block_bytes<FMT>();
+  const size_t step_bytes = FMT == FMT_Q8 ? 136 : w_block_bytes<FMT>();
 #pragma unroll
   for (int i = 0; i < w_regs<FMT>(); ++i) {
     const int idx = min(tid + NTG * i, TN * CU - 1);
     const int rr = idx / CU, u = idx % CU, r = min(r0 + rr, n - 1);
     const uint8_t* base = w + (size_t)r * row_bytes + (size_t)kb * step_bytes;
     if constexpr (FMT == FMT_Q8) R.w[i] = *(const uint16_t*)(base + (u / 16) * 34 + 2 + 2 * (u % 16));
+    else if constexpr (FMT == FMT_PT) R.w[i] = *(const uint32_t*)(base + 4 * u);
     else R.w[i] = *(const uint16_t*)(base + 2 + 2 * u);
   }
   if (tid < TN * w_scales<FMT>()) {   // waves 0 (Q2/Q1) or 0-3 (Q8): uniform
     const int rr = tid / w_scales<FMT>(), b = tid % w_scales<FMT>(), r = min(r0 + rr, n - 1);
-    R.ws = *(const uint16_t*)(w + (size_t)r * row_bytes + (size_t)kb * step_bytes + 34 * b);
+    R.ws = *(const uint16_t*)(w + (size_t)r * row_bytes + (size_t)kb * step_bytes + 34 * b + w_scale_off<FMT>());
   }
 }
 
@@ -114,11 +135,33 @@ HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
 #pragma unroll
   for (int i = 0; i < w_regs<FMT>(); ++i) {
     const int idx = tid + NTG * i;
-    if (idx < TN * CU) {   // Q2: 1024, Q1: 512, Q8: 4096 = whole multiples of 512
+    if (idx < TN * CU) {   // Q2: 1024, Q1: 512, Q8: 4096, PTQ1_0: 448 (lanes 448.. idle)
       const int rr = idx / CU, u = idx % CU;
       const uint32_t v = R.w[i];
       if constexpr (FMT == FMT_Q2) {
         *(uint2*)(st.w + rr * AROW + 8 * u) = make_uint2(q2_spread4(v & 0xffu), q2_spread4(v >> 8));
+      } else if constexpr (FMT == FMT_PT) {
+        int8_t* wr = st.w + rr * AROW;
+        if (u < 6) {   // qs dword: stage A (u < 4) or stage B
+          u16x2 lo = __builtin_bit_cast(u16x2, v & 0x00ff00ffu), hi = __builtin_bit_cast(u16x2, (v >> 8) & 0x00ff00ffu);
+#pragma unroll
+          for (int n = 0; n < 5; ++n) {
+            const int e = u < 4 ? 16 * n + 4 * u : 80 + 8 * n + 4 * (u - 4);
+            *(uint32_t*)(wr + e) = trit_to_i8x4(pt_step(lo, hi));
+          }
+        } else {       // qh bytes 24, 25 -> elements 120 + 2n + h
+          u16x2 p = __builtin_bit_cast(u16x2, (v & 0xffu) | ((v << 8) & 0x00ff0000u));
+          const u16x2 three = {3, 3}, eight = {8, 8};
+          uint32_t t[4];
+#pragma unroll
+          for (int n = 0; n < 4; ++n) {
+            const u16x2 q = p * three;
+            t[n] = __builtin_bit_cast(uint32_t, (u16x2)(q >> eight));
+            p = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, q) & 0x00ff00ffu);
+          }
+          *(uint32_t*)(wr + 120) = trit_to_i8x4(__builtin_amdgcn_perm(t[1], t[0], 0x06040200u));
+          *(uint32_t*)(wr + 124) = trit_to_i8x4(__builtin_amdgcn_perm(t[3], t[2], 0x06040200u));
+        }
       } else if constexpr (FMT == FMT_Q1) {
         *(uint4*)(st.w + rr * AROW + 16 * u) = make_uint4(q1_spread4(v & 0xfu), q1_spread4((v >> 4) & 0xfu),
                                                           q1_spread4((v >> 8) & 0xfu), q1_spread4((v >> 12) & 0xfu));
@@ -228,6 +271,7 @@ int hh_gemm_launch(int fmt, const uint8_t* w, int n, int K, const int8_t* xq, co
     case FMT_Q2: hipLaunchKernelGGL(k_gemm<FMT_Q2>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
     case FMT_Q1: hipLaunchKernelGGL(k_gemm<FMT_Q1>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
     case FMT_Q8: hipLaunchKernelGGL(k_gemm<FMT_Q8>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
+    case FMT_PT: hipLaunchKernelGGL(k_gemm<FMT_PT>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
     default: return 1;
   }
   return hipGetLastError() == hipSuccess ? 0 : 1;

@@ -141,11 +141,87 @@ HH_DEV void unit_q8(const uint32_t (&w)[17], const int8_t* aq, const float* ad, 
   }
 }
 
+// PTQ1_0 (ptq1_0.rs:1-13): a block is qs[24] at 5 trits per byte (bytes 0..15
+// give elements 16n + m, bytes 16..23 elements 80 + 8n + (m-16)), qh[2] at 4
+// trits per byte (elements 120 + 2n + h), then the f16 scale.  Trit n of byte b
+// is ((b*3^n mod 256)*3) >> 8, walked as p <- b; q = 3p; trit = q >> 8;
+// p <- q mod 256, on two 16-bit lanes at once (v_pk_mul_lo_u16).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+struct PtLanes {
+  u16x2 lo, hi;   // bytes 0,2 and 1,3 of a qs dword
+  HH_DEV explicit PtLanes(uint32_t q)
+      : lo(__builtin_bit_cast(u16x2, q & 0x00ff00ffu)), hi(__builtin_bit_cast(u16x2, (q >> 8) & 0x00ff00ffu)) {}
+  // the next slot's four trits (0..2) as bytes, in the dword's byte order
+  HH_DEV uint32_t next() {
+    const u16x2 three = {3, 3};
+    const u16x2 ql = lo * three, qh = hi * three;
+    const uint32_t tl = __builtin_bit_cast(uint32_t, (u16x2)(ql >> (u16x2){8, 8}));
+    const uint32_t th = __builtin_bit_cast(uint32_t, (u16x2)(qh >> (u16x2){8, 8}));
+    lo = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, ql) & 0x00ff00ffu);
+    hi = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, qh) & 0x00ff00ffu);
+    return tl | (th << 8);
+  }
+};
+
+// One PTQ1_0 block (dwords w[0..6]) against its 128 activations: the
+// sub-block int dots sum(trit * a) - sum(a) = sum((trit - 1) * a), then the
+// scalar kernel's fp32 combine (ptq1_0.rs:587-599), as unit_q2.
+HH_DEV float block_pt(const uint32_t* w, const int8_t* aq, const float* ad, const int* as) {
+#pragma clang fp contract(off)
+  const int* A = (const int*)aq;   // 32 activation dwords of the block
+  int s[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {   // stage A: slot n -> elements 16n + 4j .. +3
+    PtLanes L(w[j]);
+#pragma unroll
+    for (int n = 0; n < 5; ++n) s[n >> 1] = sdot4(L.next(), (uint32_t)A[4 * n + j], s[n >> 1]);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {   // stage B: slot n -> elements 80 + 8n + 4j .. +3
+    PtLanes L(w[4 + j]);
+#pragma unroll
+    for (int n = 0; n < 5; ++n) {
+      const int sub = n < 2 ? 2 : 3;
+      s[sub] = sdot4(L.next(), (uint32_t)A[20 + 2 * n + j], s[sub]);
+    }
+  }
+  {   // qh: bytes 24, 25 in the 16-bit lanes; elements 120 + 2n + h
+    const uint32_t W = w[6];
+    u16x2 p = __builtin_bit_cast(u16x2, (W & 0xffu) | ((W << 8) & 0x00ff0000u));
+    const u16x2 three = {3, 3};
+    uint32_t t[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const u16x2 q = p * three;
+      t[n] = __builtin_bit_cast(uint32_t, (u16x2)(q >> (u16x2){8, 8}));
+      p = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, q) & 0x00ff00ffu);
+    }
+    s[3] = sdot4(__builtin_amdgcn_perm(t[1], t[0], 0x06040200u), (uint32_t)A[30], s[3]);
+    s[3] = sdot4(__builtin_amdgcn_perm(t[3], t[2], 0x06040200u), (uint32_t)A[31], s[3]);
+  }
+  float bacc = 0.0f;
+#pragma unroll
+  for (int sub = 0; sub < 4; ++sub) bacc += (float)(s[sub] - as[sub]) * ad[sub];
+  return bacc * h2f(w[6] >> 16);
+}
+
+HH_DEV void unit_pt(const uint32_t (&w)[14], const int8_t* aq, const float* ad, const int* as, float (&pr)[2]) {
+  pr[0] = block_pt(w, aq, ad, as);
+  pr[1] = block_pt(w + 7, aq + 128, ad + 4, as + 4);
+}
+
 // Plain loads: on gfx950 the non-temporal variant of this stream measured
 // ~4.0 TB/s against ~6.2 TB/s for ordinary loads of the same 68-byte units.
 template <int FMT> HH_DEV void load_unit(uint32_t (&w)[UnitT<FMT>::DW], const uint8_t* p) {
   const u32x4_a4* v = (const u32x4_a4*)p;
-  if constexpr (FMT == FMT_Q1) {
+  if constexpr (FMT == FMT_PT) {
+    u32x4_a4 a = v[0], b = v[1], c = v[2];
+    u32x2_a4 d = *(const u32x2_a4*)(p + 48);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    w[8] = c.x; w[9] = c.y; w[10] = c.z; w[11] = c.w;
+    w[12] = d.x; w[13] = d.y;
+  } else if constexpr (FMT == FMT_Q1) {
     u32x4_a4 a = v[0], b = v[1];
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
@@ -164,6 +240,7 @@ template <int FMT> HH_DEV void unit_dot(const uint32_t (&w)[UnitT<FMT>::DW], con
                                         const float* ad, const int* as, float (&pr)[2]) {
   if constexpr (FMT == FMT_Q2) unit_q2(w, aq, ad, as, pr);
   else if constexpr (FMT == FMT_Q1) unit_q1(w, aq, ad, as, pr);
+  else if constexpr (FMT == FMT_PT) unit_pt(w, aq, ad, as, pr);
   else unit_q8(w, aq, ad, as, pr);
 }
 
@@ -812,6 +889,7 @@ int hh_fmt_of(int ggml_type) {
     case 8: return FMT_Q8;
     case 41: case 43: return FMT_Q1;
     case 42: case 142: return FMT_Q2;
+    case 143: return FMT_PT;
   }
   return -1;
 }
@@ -861,6 +939,7 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   switch (fmt) {
     case FMT_Q2: rc = launch_p<FMT_Q2>(a, pro, epi, nu, n_wg, lds, s); break;
     case FMT_Q1: rc = launch_p<FMT_Q1>(a, pro, epi, nu, n_wg, lds, s); break;
+    case FMT_PT: rc = launch_p<FMT_PT>(a, pro, epi, nu, n_wg, lds, s); break;
     case FMT_Q8: rc = launch_p<FMT_Q8>(a, pro, epi, nu, n_wg, lds, s); break;
   }
   if (rc == 0 && epi == EPI_LOGITS) {

@@ -48,6 +48,16 @@ __global__ void k_dequant(int type, const uint8_t* __restrict__ w, int64_t n, fl
     int e = (int)(i % 128);
     int bit = (blk[2 + e / 8] >> (e % 8)) & 1;
     v = (float)(bit ? 1 : -1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  } else if (type == 143) {                          // ptq1_0.rs:72-110
+    const uint8_t* blk = w + (i / 128) * 28;
+    const int e = (int)(i % 128);
+    int byte, n;
+    if (e < 80) { byte = e & 15; n = e >> 4; }
+    else if (e < 120) { byte = 16 + ((e - 80) & 7); n = (e - 80) >> 3; }
+    else { byte = 24 + ((e - 120) & 1); n = (e - 120) >> 1; }
+    const uint32_t p3[5] = {1, 3, 9, 27, 81};
+    const int t = (int)(((((uint32_t)blk[byte] * p3[n]) & 0xffu) * 3u) >> 8);
+    v = (float)(t - 1) * h2f((uint32_t)blk[26] | ((uint32_t)blk[27] << 8));
   } else if (type == 1) {
     const uint8_t* p = w + i * 2;
     v = h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8));
@@ -869,7 +879,10 @@ __global__ void k_synth_q8(uint64_t key, int64_t nblocks, float c, uint8_t* out)
 
 // Q1_0 / Q2_0 from the integers: absmean scale S*c/128, sign bit (I >= 0), or
 // ternary code (256|I| >= S -> +-1, else 0).
-__global__ void k_synth_bits(int is_q1, uint64_t key, int64_t nblocks, float cq, uint8_t* out) {
+// mode 0: Q2_0 codes, 1: Q1_0 sign bits, 2: the Q2_0 codes packed as PTQ1_0
+// (ptq1_0.rs:604-643 packing), so a PTQ1_0 model holds the Q2_0 weights.
+__global__ void k_synth_bits(int mode, uint64_t key, int64_t nblocks, float cq, uint8_t* out) {
+  const int is_q1 = mode == 1;
   int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= nblocks) return;
   int32_t iv[128];
@@ -880,6 +893,27 @@ __global__ void k_synth_bits(int is_q1, uint64_t key, int64_t nblocks, float cq,
   }
   float scale = __fmul_rn((float)S, cq);
   uint32_t h = f2h(scale);
+  if (mode == 2) {
+    auto code = [&](int e) -> uint32_t {
+      int32_t x = iv[e];
+      int64_t ax = x < 0 ? -(int64_t)x : x;
+      return (S > 0 && 256 * ax >= S) ? (x > 0 ? 2u : 0u) : 1u;
+    };
+    uint8_t* o = out + b * 28;
+    for (int m = 0; m < 24; ++m) {
+      uint32_t q = 0;
+      for (int n = 0; n < 5; ++n) q = q * 3u + code(m < 16 ? 16 * n + m : 80 + 8 * n + (m - 16));
+      o[m] = (uint8_t)((q * 256u + 242u) / 243u);
+    }
+    for (int hh = 0; hh < 2; ++hh) {
+      uint32_t q = 0;
+      for (int n = 0; n < 4; ++n) q = q * 3u + code(120 + hh + 2 * n);
+      o[24 + hh] = (uint8_t)((q * 3u * 256u + 242u) / 243u);
+    }
+    o[26] = (uint8_t)(h & 0xff);
+    o[27] = (uint8_t)(h >> 8);
+    return;
+  }
   int bb = is_q1 ? 18 : 34;
   uint8_t* o = out + b * bb;
   o[0] = (uint8_t)(h & 0xff);
@@ -1001,9 +1035,9 @@ int hh_synth_launch(int type, uint64_t key, int64_t rows, int64_t cols, float c,
     hipLaunchKernelGGL(k_synth_f32, dim3(nblk(n, 256)), dim3(256), 0, s, key, n, c, mean, (float*)out);
   } else if (type == 8) {
     hipLaunchKernelGGL(k_synth_q8, dim3(nblk(n / 32, 256)), dim3(256), 0, s, key, n / 32, c, (uint8_t*)out);
-  } else if (type == 41 || type == 43 || type == 42 || type == 142) {
-    int is_q1 = (type == 41 || type == 43);
-    hipLaunchKernelGGL(k_synth_bits, dim3(nblk(n / 128, 128)), dim3(128), 0, s, is_q1, key, n / 128, cq,
+  } else if (type == 41 || type == 43 || type == 42 || type == 142 || type == 143) {
+    int mode = (type == 41 || type == 43) ? 1 : type == 143 ? 2 : 0;
+    hipLaunchKernelGGL(k_synth_bits, dim3(nblk(n / 128, 128)), dim3(128), 0, s, mode, key, n / 128, cq,
                        (uint8_t*)out);
   } else {
     return 1;

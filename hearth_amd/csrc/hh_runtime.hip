@@ -54,12 +54,13 @@ size_t row_bytes(int type, int64_t n) {
     case HH_Q8_0: return (size_t)(n / 32) * 34;
     case HH_Q1_0: case HH_Q1_0_G128: return (size_t)(n / 128) * 18;
     case HH_Q2_0: case HH_PQ2_0: return (size_t)(n / 128) * 34;
+    case HH_PTQ1_0: return (size_t)(n / 128) * 28;
   }
   return 0;
 }
 
 bool is_quant(int t) {
-  return t == HH_Q8_0 || t == HH_Q1_0 || t == HH_Q1_0_G128 || t == HH_Q2_0 || t == HH_PQ2_0;
+  return t == HH_Q8_0 || t == HH_Q1_0 || t == HH_Q1_0_G128 || t == HH_Q2_0 || t == HH_PQ2_0 || t == HH_PTQ1_0;
 }
 
 uint64_t mix64h(uint64_t x) {
@@ -696,7 +697,7 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   const hh_model_config& c = *cfg;
   if (c.arch != 0 && c.arch != 1) return fail(HH_ERR_INVALID, "arch must be 0 (dense) or 1 (qwen35)");
   int wf = hh_fmt_of(c.wtype);
-  if (wf < 0 || wf == 0) return fail(HH_ERR_DTYPE, "layer weights must be Q1_0/Q1_0_G128/Q2_0/PQ2_0");
+  if (wf < 0 || wf == 0) return fail(HH_ERR_DTYPE, "layer weights must be Q1_0/Q1_0_G128/Q2_0/PQ2_0/PTQ1_0");
   if (c.head_type != HH_Q8_0) return fail(HH_ERR_DTYPE, "token_embd/output must be Q8_0");
   if (c.d_model % 1024 || c.d_ffn % 1024 || c.n_layers <= 0 || c.vocab <= 0)
     return fail(HH_ERR_DIM, "d_model and d_ffn must be multiples of 1024");

@@ -19,7 +19,7 @@ from typing import Optional, Sequence
 import numpy as np
 
 GGML_F32, GGML_F16, GGML_Q8_0 = 0, 1, 8
-GGML_Q1_0, GGML_Q2_0, GGML_Q1_0_G128, GGML_PQ2_0 = 41, 42, 43, 142
+GGML_Q1_0, GGML_Q2_0, GGML_Q1_0_G128, GGML_PQ2_0, GGML_PTQ1_0 = 41, 42, 43, 142, 143
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB: Optional[C.CDLL] = None
@@ -41,6 +41,8 @@ def row_bytes(t: int, n: int) -> int:
         return n // 128 * 18
     if t in (GGML_Q2_0, GGML_PQ2_0):
         return n // 128 * 34
+    if t == GGML_PTQ1_0:
+        return n // 128 * 28
     raise ValueError(f"unknown ggml type {t}")
 
 

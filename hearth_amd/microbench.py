@@ -1,5 +1,6 @@
-"""GEMV microbenchmark: Q1_0 and Q2_0 GEMVs at the
-1.7B shapes N x K = 6144x2048, 2048x6144, 151936x2048 on Q8_0 activations from
+"""GEMV microbenchmark: Q1_0 and Q2_0 GEMVs (and
+PTQ1_0, the 28-byte ternary format) at the 1.7B shapes N x K = 6144x2048,
+2048x6144, 151936x2048, plus the 8B FFN shapes, on Q8_0 activations from
 N(0,1), 1000 repetitions.  Each repetition reads a different weight copy from a
 ring larger than 512 MB (twice the 256 MB last-level cache), so the traffic is
 HBM; bytes per launch = N*(K/128)*block_bytes + (K/32)*34 + 4N.
@@ -16,37 +17,41 @@ import sys
 
 import numpy as np
 
-SHAPES = [(6144, 2048), (2048, 6144), (151936, 2048)]
+SHAPES = [(6144, 2048), (2048, 6144), (151936, 2048), (24576, 4096), (4096, 12288)]
 PEAK_GBS = 8000.0
 
 
 def run(reps: int = 1000, ring_bytes: int = 600 << 20, seed: int = 1):
     import torch
-    from hearth_amd import Ctx, GGML_Q1_0, GGML_Q2_0, row_bytes
+    from hearth_amd import Ctx, GGML_Q1_0, GGML_Q2_0, GGML_PTQ1_0, row_bytes
     ctx = Ctx(0)
     out = []
     rng = np.random.default_rng(seed)
-    for t, tname in ((GGML_Q1_0, "Q1_0"), (GGML_Q2_0, "Q2_0")):
+    for t, tname in ((GGML_Q1_0, "Q1_0"), (GGML_Q2_0, "Q2_0"), (GGML_PTQ1_0, "PTQ1_0")):
         for n, k in SHAPES:
             wb = n * row_bytes(t, k)
             copies = max(2, -(-ring_bytes // wb))
             ring = torch.randint(0, 256, (copies, wb), dtype=torch.uint8, device="cuda")
             # finite fp16 block scales in every block
-            bb = 18 if t == GGML_Q1_0 else 34
+            bb = {GGML_Q1_0: 18, GGML_Q2_0: 34, GGML_PTQ1_0: 28}[t]
+            so = 26 if t == GGML_PTQ1_0 else 0   # scale offset in the block
             sc = torch.tensor(np.frombuffer(np.float16(0.01).tobytes(), np.uint8), device="cuda")
             view = ring.view(copies, n * (k // 128), bb)
-            view[:, :, 0] = sc[0]
-            view[:, :, 1] = sc[1]
+            view[:, :, so] = sc[0]
+            view[:, :, so + 1] = sc[1]
             x = torch.tensor(rng.standard_normal(k).astype(np.float32), device="cuda")
             xq = torch.zeros(k // 32 * 34, dtype=torch.uint8, device="cuda")
             y = torch.zeros(n, dtype=torch.float32, device="cuda")
             torch.cuda.synchronize()
             ctx.quantize_q8_0(x, k, xq)
+            # raw device addresses: the timed loop makes no torch call per launch
+            wp = [ring[i].data_ptr() for i in range(copies)]
+            xp, yp = xq.data_ptr(), y.data_ptr()
             for i in range(min(copies, 8)):
-                ctx.gemv_q8(t, ring[i], n, k, xq, y)
+                ctx.gemv_q8(t, wp[i], n, k, xp, yp)
             ctx.event(0)
             for i in range(reps):
-                ctx.gemv_q8(t, ring[i % copies], n, k, xq, y)
+                ctx.gemv_q8(t, wp[i % copies], n, k, xp, yp)
             ctx.event(1)
             ms = ctx.elapsed_ms(0, 1) / reps
             nbytes = wb + (k // 32) * 34 + 4 * n

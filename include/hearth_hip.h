@@ -50,7 +50,8 @@ enum {
   HH_Q1_0 = 41,
   HH_Q2_0 = 42,
   HH_Q1_0_G128 = 43,
-  HH_PQ2_0 = 142
+  HH_PQ2_0 = 142,
+  HH_PTQ1_0 = 143       /* 128 weights in 28 B: 5 trits/byte (ptq1_0.rs:1-13) */
 };
 
 typedef struct hh_ctx hh_ctx;
@@ -133,7 +134,7 @@ typedef struct {
   float eps, rope_theta;
   int rope_dim;           /* 0 = head_dim */
   int max_seq;
-  int wtype;              /* HH_Q1_0 / HH_Q1_0_G128 / HH_Q2_0 / HH_PQ2_0 / HH_Q8_0 */
+  int wtype;              /* HH_Q1_0 / HH_Q1_0_G128 / HH_Q2_0 / HH_PQ2_0 / HH_PTQ1_0 */
   int head_type;          /* token_embd / output: HH_Q8_0 */
   int qk_norm;
   int full_attn_interval; /* qwen35: layer i is full attention iff (i+1)%interval==0 */

@@ -170,6 +170,7 @@ size_t ho_row_bytes(int type, int64_t n) {
     case HO_Q1_0_G128: return (size_t)(n / 128) * 18;
     case HO_Q2_0:
     case HO_PQ2_0: return (size_t)(n / 128) * 34;
+    case HO_PTQ1_0: return (size_t)(n / 128) * 28;
     default: return 0;
   }
 }
@@ -212,6 +213,61 @@ void ho_quantize_q8_0(const float* src, int64_t n, uint8_t* dst) {
   }
 }
 
+/* PTQ1_0 (ptq1_0.rs:1-13, :72-110).  Trit n of a packed byte: the byte is
+ * ceil(256*Q/243) for Q = sum t_k 3^(4-k), and b*3^n mod 256 keeps the fraction
+ * Q*3^n/243 mod 1 to within the rounding, so ((b*3^n mod 256)*3) >> 8 is t_n. */
+static inline int ptq_trit(unsigned b, int n) {
+  static const unsigned p3[5] = {1, 3, 9, 27, 81};
+  return (int)((((b * p3[n]) & 0xffu) * 3u) >> 8);
+}
+/* Position in the block of element (stage byte m, slot n) and of qh trits:
+ * stage A = bytes 0..15 -> 16n + m; stage B = bytes 16..23 -> 80 + 8n + (m-16);
+ * qh byte h (0,1), slot n < 4 -> 120 + 2n + h. */
+static void ptq_block_trits(const uint8_t* blk, int8_t* t /* 128 weights in {-1,0,1} */) {
+  for (int m = 0; m < 24; m++)
+    for (int n = 0; n < 5; n++) {
+      int e = m < 16 ? 16 * n + m : 80 + 8 * n + (m - 16);
+      t[e] = (int8_t)(ptq_trit(blk[m], n) - 1);
+    }
+  for (int h = 0; h < 2; h++)
+    for (int n = 0; n < 4; n++) t[120 + 2 * n + h] = (int8_t)(ptq_trit(blk[24 + h], n) - 1);
+}
+
+/* ptq1_0.rs:604-643 quantize (ternary round of x/amax, base-3 pack, ceil to the
+ * 256/243 grid; the qh byte carries 4 trits and a trailing zero). */
+void ho_quantize_ptq1_0(const float* src, int64_t n, uint8_t* dst) {
+  int64_t blocks = n / 128;
+  for (int64_t b = 0; b < blocks; b++) {
+    const float* x = src + b * 128;
+    float amax = 0.0f;
+    for (int i = 0; i < 128; i++) amax = fmaxf(amax, fabsf(x[i]));
+    float d = amax, id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint8_t* o = dst + b * 28;
+    memset(o, 0, 28);
+    uint16_t h = ho_f32_to_f16(d);
+    o[26] = (uint8_t)(h & 0xff);
+    o[27] = (uint8_t)(h >> 8);
+    for (int m = 0; m < 24; m++) {
+      unsigned q = 0;
+      for (int nn = 0; nn < 5; nn++) {
+        int e = m < 16 ? 16 * nn + m : 80 + 8 * nn + (m - 16);
+        int xi = (int)roundf(x[e] * id) + 1;
+        q = (q * 3u + (unsigned)xi) & 0xffu;
+      }
+      o[m] = (uint8_t)((q * 256u + 242u) / 243u);
+    }
+    for (int hh = 0; hh < 2; hh++) {
+      unsigned q = 0;
+      for (int mm = 0; mm < 4; mm++) {
+        int xi = (int)roundf(x[120 + hh + 2 * mm] * id) + 1;
+        q = (q * 3u + (unsigned)xi) & 0xffu;
+      }
+      q = (q * 3u) & 0xffu;
+      o[24 + hh] = (uint8_t)((q * 256u + 242u) / 243u);
+    }
+  }
+}
+
 /* q8_0.rs:4-18, q2_0.rs:66-84 (pq2_0.rs:32-50 same bytes), q1_0g128.rs:75-98. */
 int ho_dequantize(int type, const uint8_t* w, int64_t n, float* out) {
   switch (type) {
@@ -241,6 +297,15 @@ int ho_dequantize(int type, const uint8_t* w, int64_t n, float* out) {
         int e = (int)(i % 128);
         int bit = (blk[2 + e / 8] >> (e % 8)) & 1;
         out[i] = (float)(bit ? 1 : -1) * rd_f16(blk);
+      }
+      return 0;
+    case HO_PTQ1_0:   /* ptq1_0.rs:72-110 */
+      for (int64_t b = 0; b < n / 128; b++) {
+        int8_t t[128];
+        const uint8_t* blk = w + b * 28;
+        ptq_block_trits(blk, t);
+        float d = rd_f16(blk + 26);
+        for (int e = 0; e < 128; e++) out[b * 128 + e] = (float)t[e] * d;
       }
       return 0;
     default: return 1;
@@ -273,6 +338,29 @@ float ho_dot_q2_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n) {
       block_acc += (float)dot * a_scale;
     }
     sum += block_acc * w_scale;
+  }
+  return sum;
+}
+
+/* ptq1_0.rs:555-602 scalar PTQ1_0 x Q8_0: per 32-element sub-block an exact
+ * int dot, block_acc += dot * d_a, sum += block_acc * d (the Q2_0 structure). */
+float ho_dot_ptq1_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n) {
+  int64_t blocks = n / 128;
+  float sum = 0.0f;
+  for (int64_t b = 0; b < blocks; b++) {
+    const uint8_t* wb = w + b * 28;
+    int8_t t[128];
+    ptq_block_trits(wb, t);
+    float block_acc = 0.0f;
+    for (int sub = 0; sub < 4; sub++) {
+      const uint8_t* ab = a + (b * 4 + sub) * 34;
+      float a_scale = rd_f16(ab);
+      const int8_t* av = (const int8_t*)(ab + 2);
+      int32_t dot = 0;
+      for (int i = 0; i < 32; i++) dot += (int32_t)t[sub * 32 + i] * (int32_t)av[i];
+      block_acc += (float)dot * a_scale;
+    }
+    sum += block_acc * rd_f16(wb + 26);
   }
   return sum;
 }
@@ -419,6 +507,7 @@ static dot_fn pick_dot(int type, int arm) {
     case HO_Q1_0:
     case HO_Q1_0_G128: return avx ? ho_dot_q1_0_q8_0_avx2 : ho_dot_q1_0_q8_0;
     case HO_Q8_0: return ho_dot_q8_0_q8_0;
+    case HO_PTQ1_0: return ho_dot_ptq1_0_q8_0;
     default: return NULL;
   }
 }
@@ -632,6 +721,25 @@ uint32_t ho_synth_token(uint64_t seed, int64_t i, uint32_t vocab) {
   return (uint32_t)(mix64(key + (uint64_t)i * 0x9e3779b97f4a7c15ull) % vocab);
 }
 
+/* Packs 128 ternary codes (0/1/2 = weight -1/0/+1) and an f16 scale into one
+ * PTQ1_0 block, as ho_quantize_ptq1_0 packs rounded values. */
+void ho_ptq1_0_pack_codes(const int* code, uint16_t h, uint8_t* o) {
+  memset(o, 0, 28);
+  o[26] = (uint8_t)(h & 0xff);
+  o[27] = (uint8_t)(h >> 8);
+  for (int m = 0; m < 24; m++) {
+    unsigned q = 0;
+    for (int nn = 0; nn < 5; nn++) q = q * 3u + (unsigned)code[m < 16 ? 16 * nn + m : 80 + 8 * nn + (m - 16)];
+    o[m] = (uint8_t)((q * 256u + 242u) / 243u);
+  }
+  for (int hh = 0; hh < 2; hh++) {
+    unsigned q = 0;
+    for (int mm = 0; mm < 4; mm++) q = q * 3u + (unsigned)code[120 + hh + 2 * mm];
+    q *= 3u;
+    o[24 + hh] = (uint8_t)((q * 256u + 242u) / 243u);
+  }
+}
+
 void ho_synth_tensor(int type, uint64_t seed, const char* name, int64_t rows, int64_t cols,
                      float std, float mean, void* out, int n_threads) {
   uint64_t key = ho_name_key(seed, name);
@@ -653,6 +761,26 @@ void ho_synth_tensor(int type, uint64_t seed, const char* name, int64_t rows, in
       for (int64_t b = 0; b < cols / 32; b++) {
         for (int j = 0; j < 32; j++) tmp[j] = (float)ho_synth_int(key, base + b * 32 + j) * c;
         ho_quantize_q8_0(tmp, 32, o + b * 34);
+      }
+    } else if (type == HO_PTQ1_0) {
+      /* the Q2_0 generator's ternary codes and scale, packed as PTQ1_0: the two
+       * formats then hold the same weights */
+      uint8_t* o = (uint8_t*)out + (size_t)r * rb;
+      for (int64_t b = 0; b < cols / 128; b++) {
+        int32_t iv[128];
+        int64_t S = 0;
+        for (int j = 0; j < 128; j++) {
+          iv[j] = ho_synth_int(key, base + b * 128 + j);
+          S += iv[j] < 0 ? -(int64_t)iv[j] : iv[j];
+        }
+        float scale = (float)S * (c / 128.0f);
+        int code[128];
+        for (int j = 0; j < 128; j++) {
+          int64_t a = iv[j] < 0 ? -(int64_t)iv[j] : iv[j];
+          code[j] = 1;
+          if (S > 0 && 256 * a >= S) code[j] = iv[j] > 0 ? 2 : 0;
+        }
+        ho_ptq1_0_pack_codes(code, ho_f32_to_f16(scale), o + b * 28);
       }
     } else if (type == HO_Q1_0 || type == HO_Q1_0_G128 || type == HO_Q2_0 || type == HO_PQ2_0) {
       int is_q1 = (type == HO_Q1_0 || type == HO_Q1_0_G128);

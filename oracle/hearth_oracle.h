@@ -21,7 +21,7 @@ extern "C" {
 
 /* GGML type ids, crates/hearth-gguf/src/ggml.rs:49-53, :96-100 */
 enum { HO_F32 = 0, HO_F16 = 1, HO_Q8_0 = 8, HO_Q1_0 = 41, HO_Q2_0 = 42, HO_Q1_0_G128 = 43,
-       HO_PQ2_0 = 142 };
+       HO_PQ2_0 = 142, HO_PTQ1_0 = 143 };
 
 /* ---- scalar conversions (half 2.7.1 f16::from_f32 / to_f32 semantics) ---- */
 uint16_t ho_f32_to_f16(float x);
@@ -35,11 +35,17 @@ float ho_log(float x);
 size_t ho_row_bytes(int type, int64_t n_cols);
 void ho_quantize_q8_0(const float* x, int64_t n, uint8_t* out);          /* q8_0.rs:20-51 */
 int ho_dequantize(int type, const uint8_t* w, int64_t n, float* out);    /* quant lib.rs:169-239 */
+/* PTQ1_0 (type 143): 128 weights in 28 bytes, qs[24] at 5 trits/byte (a 16-byte
+ * then an 8-byte stage, slot-major), qh[2] at 4 trits/byte, f16 d last
+ * (ptq1_0.rs:1-13).  Trit n of byte b is ((b*3^n mod 256)*3) >> 8. */
+void ho_quantize_ptq1_0(const float* x, int64_t n, uint8_t* out);        /* ptq1_0.rs:604-643 */
+void ho_ptq1_0_pack_codes(const int* code, uint16_t f16_scale, uint8_t* out); /* one block from codes 0/1/2 */
 
 /* ---- dot kernels: DotFn = fn(w, a_q8, n) -> f32 (pool.rs:6) ---- */
 float ho_dot_q2_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n);   /* q2_0.rs:537-574 */
 float ho_dot_q1_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n);   /* q1_0g128.rs:1113-1152 */
 float ho_dot_q8_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n);   /* q8_0.rs:154-171 */
+float ho_dot_ptq1_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n); /* ptq1_0.rs:555-602 */
 float ho_dot_q2_0_q8_0_avx2(const uint8_t* w, const uint8_t* a, int64_t n); /* q2_0.rs:308-392 */
 float ho_dot_q1_0_q8_0_avx2(const uint8_t* w, const uint8_t* a, int64_t n); /* q1_0g128.rs:255-377 */
 int ho_have_avx2(void);

@@ -50,6 +50,9 @@ def load() -> C.CDLL:
         "ho_dot_q2_0_q8_0": (C.c_float, [u8p, u8p, C.c_int64]),
         "ho_dot_q1_0_q8_0": (C.c_float, [u8p, u8p, C.c_int64]),
         "ho_dot_q8_0_q8_0": (C.c_float, [u8p, u8p, C.c_int64]),
+        "ho_dot_ptq1_0_q8_0": (C.c_float, [u8p, u8p, C.c_int64]),
+        "ho_quantize_ptq1_0": (None, [f32p, C.c_int64, u8p]),
+        "ho_ptq1_0_pack_codes": (None, [C.c_void_p, C.c_uint16, u8p]),
         "ho_dot_q2_0_q8_0_avx2": (C.c_float, [u8p, u8p, C.c_int64]),
         "ho_dot_q1_0_q8_0_avx2": (C.c_float, [u8p, u8p, C.c_int64]),
         "ho_have_avx2": (C.c_int, []),
@@ -117,9 +120,24 @@ def dequantize(t: int, w: np.ndarray, n: int) -> np.ndarray:
     return out
 
 
+def quantize_ptq1_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 128 * 28, dtype=np.uint8)
+    load().ho_quantize_ptq1_0(_p(x), x.size, _p(out))
+    return out
+
+
+def ptq1_0_pack_codes(codes: np.ndarray, f16_scale: int) -> np.ndarray:
+    c = np.ascontiguousarray(codes, dtype=np.int32)
+    assert c.size == 128
+    out = np.zeros(28, dtype=np.uint8)
+    load().ho_ptq1_0_pack_codes(_p(c), f16_scale, _p(out))
+    return out
+
+
 def dot(t: int, w: np.ndarray, a: np.ndarray, n: int, avx2: bool = False) -> float:
     lib = load()
-    fn = {42: "q2_0", 142: "q2_0", 41: "q1_0", 43: "q1_0", 8: "q8_0"}[t]
+    fn = {42: "q2_0", 142: "q2_0", 41: "q1_0", 43: "q1_0", 8: "q8_0", 143: "ptq1_0"}[t]
     name = f"ho_dot_{fn}_q8_0" + ("_avx2" if avx2 else "")
     return getattr(lib, name)(_p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(a)), n)
 

@@ -12,7 +12,8 @@ _FMT = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f
         U64: "<Q", I64: "<q", F64: "<d"}
 
 # (elements per block, bytes per block) of the ggml types the tests write
-BLOCKS = {0: (1, 4), 1: (1, 2), 8: (32, 34), 41: (128, 18), 42: (128, 34), 43: (128, 18), 142: (128, 34)}
+BLOCKS = {0: (1, 4), 1: (1, 2), 8: (32, 34), 41: (128, 18), 42: (128, 34), 43: (128, 18), 142: (128, 34),
+          143: (128, 28)}
 
 
 def tensor_nbytes(ggml_type: int, shape) -> int:

@@ -13,7 +13,7 @@ do to each other."""
 import numpy as np
 import pytest
 
-from hearth_amd.lib import ModelConfig, GGML_Q1_0, GGML_Q2_0, GGML_PQ2_0, CONFIGS
+from hearth_amd.lib import ModelConfig, GGML_Q1_0, GGML_Q2_0, GGML_PQ2_0, GGML_PTQ1_0, CONFIGS
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -38,8 +38,9 @@ def make(ctx, oracle, cfg, seed, threads=16, order=1):
     return m, o
 
 
-@pytest.mark.parametrize("cfg", [TINY, TINY_HYB, TINY.replace(wtype=GGML_Q1_0), TINY_HYB.replace(wtype=GGML_PQ2_0)],
-                         ids=["dense-q2", "hybrid-q2", "dense-q1", "hybrid-pq2"])
+@pytest.mark.parametrize("cfg", [TINY, TINY_HYB, TINY.replace(wtype=GGML_Q1_0), TINY_HYB.replace(wtype=GGML_PQ2_0),
+                                 TINY.replace(wtype=GGML_PTQ1_0)],
+                         ids=["dense-q2", "hybrid-q2", "dense-q1", "hybrid-pq2", "dense-ptq1"])
 def test_synthesized_bytes_bit_exact(ctx, oracle, cfg):
     m, o = make(ctx, oracle, cfg, seed=21)
     names = o.tensor_names()
@@ -51,8 +52,8 @@ def test_synthesized_bytes_bit_exact(ctx, oracle, cfg):
         assert np.array_equal(got, want), n
 
 
-@pytest.mark.parametrize("cfg", [TINY, TINY.replace(wtype=GGML_Q1_0), TINY_HYB],
-                         ids=["dense-q2", "dense-q1", "hybrid-q2"])
+@pytest.mark.parametrize("cfg", [TINY, TINY.replace(wtype=GGML_Q1_0), TINY_HYB, TINY.replace(wtype=GGML_PTQ1_0)],
+                         ids=["dense-q2", "dense-q1", "hybrid-q2", "dense-ptq1"])
 def test_forward_logits_parity(ctx, oracle, cfg):
     m, o = make(ctx, oracle, cfg, seed=5)
     for pos, tok in enumerate([17, 400, 9, 4095, 0, 1234]):
@@ -65,7 +66,8 @@ def test_forward_logits_parity(ctx, oracle, cfg):
 
 
 @pytest.mark.parametrize("cfg,pen", [(TINY, 1.1), (TINY, 1.0), (TINY.replace(wtype=GGML_Q1_0), 1.1),
-                                     (TINY_HYB, 1.0)], ids=["dense-pen", "dense", "dense-q1", "hybrid"])
+                                     (TINY_HYB, 1.0), (TINY_HYB.replace(wtype=GGML_PTQ1_0), 1.0)],
+                         ids=["dense-pen", "dense", "dense-q1", "hybrid", "hybrid-ptq1"])
 def test_generate_tokens_parity(ctx, oracle, cfg, pen):
     m, o = make(ctx, oracle, cfg, seed=7)
     prompt = [oracle.synth_token(7, i, cfg.vocab) for i in range(5)]
@@ -162,8 +164,9 @@ def _model_with_env(ctx, cfg, seed, env):
 
 
 @pytest.mark.parametrize("cfg,n_prompt", [(TINY, 9), (TINY.replace(wtype=GGML_Q1_0), 40),
-                                          (CONFIGS["8b-q2"].replace(n_layers=2, max_seq=640), 300)],
-                         ids=["dense-q2", "dense-q1", "8b-2layer-300"])
+                                          (CONFIGS["8b-q2"].replace(n_layers=2, max_seq=640), 300),
+                                          (TINY.replace(wtype=GGML_PTQ1_0), 33)],
+                         ids=["dense-q2", "dense-q1", "8b-2layer-300", "dense-ptq1"])
 def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
     """forward_batch on the MFMA GEMM leaves the same KV cache as feeding the
     prompt one token at a time: the first generated token's logits and the next
@@ -203,3 +206,20 @@ def test_prefill_then_forward(ctx):
     assert m.last_prefill_ms() > 0
     m.close()
     m2.close()
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY_HYB], ids=["dense", "hybrid"])
+def test_ptq1_0_model_equals_q2_0_model(ctx, cfg):
+    """The generator gives a PTQ1_0 model the Q2_0 model's ternary weights: the
+    two formats' decoders must then produce identical logits and tokens."""
+    from hearth_amd import Model
+    ma, mb = Model(ctx, cfg), Model(ctx, cfg.replace(wtype=GGML_PTQ1_0))
+    ma.synthesize(31)
+    mb.synthesize(31)
+    prompt = [5, 900, 17, 3000]
+    ta, la = ma.generate(prompt, 16, repeat_pen=1.1 if cfg.arch == 0 else 1.0, want_logits=True)
+    tb, lb = mb.generate(prompt, 16, repeat_pen=1.1 if cfg.arch == 0 else 1.0, want_logits=True)
+    assert list(ta) == list(tb)
+    assert np.array_equal(la, lb)
+    ma.close()
+    mb.close()

@@ -61,7 +61,7 @@ def test_quantize_near_ties(ctx, oracle):
     assert np.array_equal(host(out), oracle.quantize_q8_0(x))
 
 
-@pytest.mark.parametrize("t", [8, 41, 42, 43, 142])
+@pytest.mark.parametrize("t", [8, 41, 42, 43, 142, 143])
 def test_dequantize_bit_exact(ctx, oracle, t):
     n = 128 * 256
     w = oracle.synth_tensor(t, 3, "w", 1, n, 0.02, 0.0)
@@ -74,7 +74,7 @@ SHAPES = [(6144, 2048), (2048, 6144), (151936, 2048), (4096, 4096), (12288, 4096
           (1, 4096), (3, 256), (37, 5120), (5120, 17408)]
 
 
-@pytest.mark.parametrize("t", [42, 41])
+@pytest.mark.parametrize("t", [42, 41, 143])
 @pytest.mark.parametrize("shape", SHAPES)
 def test_gemv_parity(ctx, oracle, t, shape):
     n_rows, n_cols = shape
@@ -89,6 +89,36 @@ def test_gemv_parity(ctx, oracle, t, shape):
     assert rel_err(got, want) < 1e-3
     # stronger than the 1e-3 bar: the device keeps the scalar kernel's fp32 order
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("shape", [(6144, 2048), (5, 768), (1000, 4096)])
+def test_gemv_ptq1_0_every_byte_pattern(ctx, oracle, shape):
+    """PTQ1_0 rows of uniformly random bytes (every qs/qh byte value, not only the
+    ones the packer emits) against the scalar dot (ptq1_0.rs:555-602), bit for bit."""
+    n_rows, n_cols = shape
+    rng = np.random.default_rng(n_rows + n_cols)
+    w = rng.integers(0, 256, n_rows * n_cols // 128 * 28, dtype=np.uint8)
+    sc = np.float16(rng.uniform(0.001, 0.05, n_rows * n_cols // 128)).view(np.uint8).reshape(-1, 2)
+    w.reshape(-1, 28)[:, 26:28] = sc
+    a = oracle.quantize_q8_0(rng.standard_normal(n_cols).astype(np.float32))
+    want = oracle.gemv(143, w, n_rows, n_cols, a, threads=8)
+    y = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
+    ctx.gemv_q8(143, dev(w), n_rows, n_cols, dev(a), y)
+    assert np.array_equal(host(y), want)
+
+
+def test_gemv_ptq1_0_equals_q2_0_on_the_same_weights(ctx, oracle):
+    """The generator writes the same ternary weights in both formats, so the two
+    GEMVs (different decoders, same combine order) must agree bit for bit."""
+    n_rows, n_cols = 4096, 4096
+    pt = oracle.synth_tensor(143, 5, "same", n_rows, n_cols, 0.02, 0.0, threads=8)
+    q2 = oracle.synth_tensor(42, 5, "same", n_rows, n_cols, 0.02, 0.0, threads=8)
+    a = dev(oracle.quantize_q8_0(np.random.default_rng(3).standard_normal(n_cols).astype(np.float32)))
+    y1 = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
+    y2 = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
+    ctx.gemv_q8(143, dev(pt), n_rows, n_cols, a, y1)
+    ctx.gemv_q8(42, dev(q2), n_rows, n_cols, a, y2)
+    assert np.array_equal(host(y1), host(y2))
 
 
 @pytest.mark.parametrize("shape", [(151936, 4096), (64, 2048), (5, 64)])
@@ -202,7 +232,7 @@ def test_argmax_rules(ctx, oracle):
     assert int(host(out)[0]) == want == 20
 
 
-@pytest.mark.parametrize("t", [41, 42, 8])
+@pytest.mark.parametrize("t", [41, 42, 8, 143])
 @pytest.mark.parametrize("n,k,seq", [(200, 512, 70), (2048, 2048, 16), (64, 5120, 1), (130, 1024, 129)])
 def test_gemm_bit_exact_vs_per_token_dot(ctx, oracle, t, n, k, seq):
     """Batched MFMA GEMM == the scalar DotFn on every token (the reference's paired
