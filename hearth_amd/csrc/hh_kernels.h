@@ -67,8 +67,11 @@ struct AttnArgs {
   float* out_f32;        // optional [n_heads*hd]
   uint8_t* act_out;      // optional packed activation (K = n_heads*hd)
   int act_fmt;
+  int kv_q8;             // caches hold Q8_0 rows: int8 [n_kv][max_seq][hd], then f16 scales [..][hd/32]
 };
 int hh_attn_launch(const AttnArgs& a, hipStream_t s);
+int hh_kv_synth_q8_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq, float cs, float* cache,
+                          hipStream_t s);
 
 // Batched prefill row kernels (hh_ops.hip).
 int hh_embed_rows_launch(int type, const uint8_t* table, int d, const uint32_t* toks, int S, float* H, hipStream_t s);

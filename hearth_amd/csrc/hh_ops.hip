@@ -216,7 +216,50 @@ template <int N> HH_DEV float pairwise_tree(float* t) {
   return t[0];
 }
 
-template <int HD, int NTA>
+// Q8_0 KV rows (KV8): the cache holds int8 values [n_kv][max_seq][hd] followed
+// by the f16 block scales [n_kv][max_seq][hd/32].  A lane's float4 slice of a
+// row is its 4 int8 times the block's f16 scale, exactly the f32 value
+// attention_q8_0 (ops.rs:946-1030) multiplies.
+struct KvQ8 {
+  int8_t* q;
+  uint16_t* d;
+  HH_DEV KvQ8(float* cache, int n_kv, int max_seq, int hd)
+      : q((int8_t*)cache), d((uint16_t*)((int8_t*)cache + (size_t)n_kv * max_seq * hd)) {}
+  HH_DEV float4 load(size_t row, int hd, int c) const {   // row = kvh*max_seq + p, lane slice c
+    const uint32_t v = *(const uint32_t*)(q + row * hd + 4 * c);
+    const float s = h2f(d[row * (hd / 32) + (c >> 3)]);
+    return make_float4((float)(int8_t)(v & 0xff) * s, (float)(int8_t)((v >> 8) & 0xff) * s,
+                       (float)(int8_t)((v >> 16) & 0xff) * s, (float)(int8_t)(v >> 24) * s);
+  }
+};
+
+// write_kv for a Q8_0 cache (kvcache.rs:104-108, quantize_q8_0_block :274-303):
+// the 8 lanes of a 32-value block share max|x|; returns the dequantized slice
+// that every later reader sees.  `write`: this lane stores its 4 bytes (and
+// lane 0 of the block the scale).
+HH_DEV float4 kv_q8_store(float4 x, const KvQ8& kv, size_t row, int hd, int c, bool write) {
+  const float vv[4] = {x.x, x.y, x.z, x.w};
+  float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+  am = group_max<8>(am);
+  const float sc = q8_scale(am), rc = q8_rcp(sc);
+  const uint32_t h = f2h(sc);
+  const float d = h2f(h);
+  uint32_t word = 0;
+  float out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = q8_round_r(vv[i], sc, rc);
+    word |= ((uint32_t)q & 0xffu) << (8 * i);
+    out[i] = (float)q * d;
+  }
+  if (write) {
+    *(uint32_t*)(kv.q + row * hd + 4 * c) = word;
+    if ((c & 7) == 0) kv.d[row * (hd / 32) + (c >> 3)] = (uint16_t)h;
+  }
+  return make_float4(out[0], out[1], out[2], out[3]);
+}
+
+template <int HD, int NTA, bool KV8>
 __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   constexpr int LPR = HD / 4, RPI = NTA / LPR, C = 8192 / HD, NR = C / RPI, NW = NTA / 64;
   static_assert(NR * RPI == C && NR >= 1, "geometry");
@@ -242,6 +285,8 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   const size_t hstride = (size_t)a.max_seq * HD;
   const float* kg = a.k_cache + (size_t)kvh * hstride + 4 * c;
   const float* vg = a.v_cache + (size_t)kvh * hstride + 4 * c;
+  const KvQ8 kq(a.k_cache, a.n_kv, a.max_seq, HD), vq(a.v_cache, a.n_kv, a.max_seq, HD);
+  const size_t row0 = (size_t)kvh * a.max_seq;
 
   // 1. the small loads first (vector loads return in issue order): this
   // lane's slice of every q head and of the new k/v, the norm weights and the
@@ -280,8 +325,13 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
     kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     vr[i] = kr[i];
     if (j < np && p0 + j != pos) {
-      kr[i] = *(const float4*)(kg + (size_t)(p0 + j) * HD);
-      vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
+      if constexpr (KV8) {
+        kr[i] = kq.load(row0 + p0 + j, HD, c);
+        vr[i] = vq.load(row0 + p0 + j, HD, c);
+      } else {
+        kr[i] = *(const float4*)(kg + (size_t)(p0 + j) * HD);
+        vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
+      }
     }
   }
   // 3. q heads and the new k: per-head norm + rope on the lane's slice
@@ -297,7 +347,10 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
       if (a.k_norm) kn4 = slice_norm<LPR>(kn4, nk4, a.eps);
       if (a.rope) kn4 = slice_rope(kn4, sn4, cs4, 4 * c, a.rope_dim);
       // kvcache.rs:92-113 write_kv, then the row joins this chunk
-      if (sub == 0) {
+      if constexpr (KV8) {
+        kn4 = kv_q8_store(kn4, kq, row0 + pos, HD, c, sub == 0);
+        vn4 = kv_q8_store(vn4, vq, row0 + pos, HD, c, sub == 0);
+      } else if (sub == 0) {
         *(float4*)(a.k_cache + (size_t)kvh * hstride + (size_t)pos * HD + 4 * c) = kn4;
         *(float4*)(a.v_cache + (size_t)kvh * hstride + (size_t)pos * HD + 4 * c) = vn4;
       }
@@ -952,6 +1005,27 @@ __global__ void k_kv_synth(uint64_t key, int n_pos, int n_kv, int hd, int max_se
   cache[((size_t)h * max_seq + p) * hd + j] = v;
 }
 
+// Same values, stored as Q8_0 rows (one thread per 32-value block).
+__global__ void k_kv_synth_q8(uint64_t key, int n_pos, int n_kv, int hd, int max_seq, float cs, float* cache) {
+  int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int nb = hd / 32;
+  if (b >= (int64_t)n_pos * n_kv * nb) return;
+  const int blk = (int)(b % nb);
+  const int64_t r = b / nb;
+  const int h = (int)(r % n_kv), p = (int)(r / n_kv);
+  float v[32], am = 0.0f;
+  for (int j = 0; j < 32; ++j) {
+    const int64_t i = r * hd + blk * 32 + j;   // the f32 generator's index ((p*n_kv)+h)*hd + j
+    v[j] = h2f(f2h(__fmul_rn((float)synth_int(key, (uint64_t)i), cs)));
+    am = fmaxf(am, fabsf(v[j]));
+  }
+  const float sc = q8_scale(am), rc = q8_rcp(sc);
+  int8_t* q = (int8_t*)cache + ((size_t)h * max_seq + p) * hd + blk * 32;
+  uint16_t* d = (uint16_t*)((int8_t*)cache + (size_t)n_kv * max_seq * hd);
+  for (int j = 0; j < 32; ++j) q[j] = (int8_t)q8_round_r(v[j], sc, rc);
+  d[((size_t)h * max_seq + p) * nb + blk] = (uint16_t)f2h(sc);
+}
+
 inline int ok() { return hipGetLastError() == hipSuccess ? 0 : 1; }
 inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 
@@ -996,11 +1070,14 @@ int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
   if (a.chunk != 8192 / a.hd || a.n_kv * G != a.n_heads || G > 8) return 1;
   const size_t split_lds = 4 * ((size_t)G * a.chunk + 2 * G + 4 + (ATTN_NT / 64) * 4 * (size_t)a.hd);
   const size_t merge_lds = 4 * ((size_t)a.max_splits + 256 + 4);
+  const dim3 g(a.max_splits, a.n_kv), b(ATTN_NT);
   if (a.hd == 128) {
-    hipLaunchKernelGGL((k_attn_split<128, ATTN_NT>), dim3(a.max_splits, a.n_kv), dim3(ATTN_NT), split_lds, s, a);
+    if (a.kv_q8) hipLaunchKernelGGL((k_attn_split<128, ATTN_NT, true>), g, b, split_lds, s, a);
+    else hipLaunchKernelGGL((k_attn_split<128, ATTN_NT, false>), g, b, split_lds, s, a);
     hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_heads, 2), dim3(256), merge_lds, s, a);
   } else {
-    hipLaunchKernelGGL((k_attn_split<256, ATTN_NT>), dim3(a.max_splits, a.n_kv), dim3(ATTN_NT), split_lds, s, a);
+    if (a.kv_q8) hipLaunchKernelGGL((k_attn_split<256, ATTN_NT, true>), g, b, split_lds, s, a);
+    else hipLaunchKernelGGL((k_attn_split<256, ATTN_NT, false>), g, b, split_lds, s, a);
     hipLaunchKernelGGL(k_attn_merge<256>, dim3(a.n_heads, 4), dim3(256), merge_lds, s, a);
   }
   return ok();
@@ -1050,6 +1127,15 @@ int hh_kv_synth_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq, f
   int64_t total = (int64_t)n_pos * n_kv * hd;
   if (total == 0) return 0;
   hipLaunchKernelGGL(k_kv_synth, dim3(nblk(total, 256)), dim3(256), 0, s, key, n_pos, n_kv, hd, max_seq, cs, cache);
+  return ok();
+}
+
+int hh_kv_synth_q8_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq, float cs, float* cache,
+                          hipStream_t s) {
+  int64_t total = (int64_t)n_pos * n_kv * (hd / 32);
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(k_kv_synth_q8, dim3(nblk(total, 64)), dim3(64), 0, s, key, n_pos, n_kv, hd, max_seq, cs,
+                     cache);
   return ok();
 }
 

@@ -349,6 +349,7 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
       aa.out_f32 = nullptr;
       aa.act_out = m->act_mid;
       aa.act_fmt = wf;
+      aa.kv_q8 = c.kv_type == HH_Q8_0;
       if (want(2, li)) KTRY(hh_attn_launch(aa, s));
       k_out = nq;
       (void)nkv;
@@ -705,6 +706,7 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
     return fail(HH_ERR_DIM, "unsupported attention geometry (head_dim 128 or 256)");
   if ((c.n_heads * c.head_dim) % 256) return fail(HH_ERR_DIM, "n_heads*head_dim must be a multiple of 256");
   if (c.max_seq <= 0) return fail(HH_ERR_DIM, "max_seq must be positive");
+  if (c.kv_type != HH_F32 && c.kv_type != HH_Q8_0) return fail(HH_ERR_DTYPE, "kv_type must be F32 or Q8_0");
   if (c.arch == 1) {
     if (c.full_attn_interval <= 0 || c.ssm_n_k_heads <= 0 || c.ssm_n_v_heads % c.ssm_n_k_heads ||
         c.ssm_head_dim != 128 || c.ssm_conv_kernel < 2 || c.ssm_conv_kernel > 8)
@@ -777,9 +779,13 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
     L.w_gu = T("ffn_gate.weight")->d;
     L.w_down = T("ffn_down.weight")->d;
   }
-  // KV cache: [attn layer][K|V][kv_head][max_seq][hd] f32 (kvcache.rs:11-39)
+  // KV cache: [attn layer][K|V][kv_head][max_seq][hd] f32 (kvcache.rs:11-39), or
+  // Q8_0 rows (kvcache.rs:41-57): int8 [kv_head][max_seq][hd], then the f16
+  // block scales [kv_head][max_seq][hd/32] (136 B per row at hd 128, as the
+  // reference's 34-byte blocks)
   size_t per = (size_t)c.n_kv_heads * c.max_seq * hd;
-  m->kv_bytes = sizeof(float) * per * 2 * (size_t)n_attn;
+  const size_t cache_bytes = c.kv_type == HH_Q8_0 ? align256(per + per / 32 * 2) : per * sizeof(float);
+  m->kv_bytes = cache_bytes * 2 * (size_t)n_attn;
   if (m->kv_bytes) {
     e = hipMalloc(&m->kv, m->kv_bytes);
     if (e != hipSuccess) { hh_model_destroy(m); return fail(HH_ERR_OOM, "KV cache allocation failed"); }
@@ -800,8 +806,8 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
       L.conv_state = L.gdn_state + (size_t)c.ssm_n_v_heads * c.ssm_head_dim * c.ssm_head_dim;
       gi++;
     } else {
-      L.k_cache = m->kv + per * 2 * ai;
-      L.v_cache = L.k_cache + per;
+      L.k_cache = (float*)((uint8_t*)m->kv + cache_bytes * 2 * ai);
+      L.v_cache = (float*)((uint8_t*)L.k_cache + cache_bytes);
       ai++;
     }
   }
@@ -956,12 +962,13 @@ int hh_model_prefill_kv_synthetic(hh_model* m, uint64_t seed, int n_pos) {
   for (int i = 0; i < m->cfg.n_layers; ++i) {
     Layer& L = m->layers[i];
     if (L.gdn) continue;
+    auto synth = m->cfg.kv_type == HH_Q8_0 ? hh_kv_synth_q8_launch : hh_kv_synth_launch;
     snprintf(b, sizeof b, "blk.%d.kv_k", i);
-    KTRY(hh_kv_synth_launch(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->cfg.max_seq, cs,
-                            L.k_cache, m->ctx->stream));
+    KTRY(synth(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->cfg.max_seq, cs, L.k_cache,
+               m->ctx->stream));
     snprintf(b, sizeof b, "blk.%d.kv_v", i);
-    KTRY(hh_kv_synth_launch(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->cfg.max_seq, cs,
-                            L.v_cache, m->ctx->stream));
+    KTRY(synth(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->cfg.max_seq, cs, L.v_cache,
+               m->ctx->stream));
   }
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
   return HH_OK;
@@ -1024,7 +1031,7 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
   // the last prompt token runs the decode step, which yields the first
   // generated token.  Hybrids feed the prompt token by token (qwen35.rs:1693-1700).
   int fed = 0;
-  if (m->cfg.arch == 0 && m->batched_prefill && n_prompt >= 2) {
+  if (m->cfg.arch == 0 && m->cfg.kv_type == HH_F32 && m->batched_prefill && n_prompt >= 2) {
     KTRY(prefill_dense(m, m->prompt, n_prompt - 1, start_pos));
     fed = n_prompt - 1;
     st.pos = start_pos + fed;
@@ -1094,6 +1101,7 @@ int hh_model_prefill(hh_model* m, const uint32_t* tokens, int n, int start_pos) 
   if (!m || !tokens) return fail(HH_ERR_INVALID, "null argument");
   if (n <= 0) return fail(HH_ERR_INVALID, "Empty prompt");
   if (m->cfg.arch != 0) return fail(HH_ERR_INVALID, "batched prefill covers the dense architecture only");
+  if (m->cfg.kv_type != HH_F32) return fail(HH_ERR_DTYPE, "batched prefill writes an f32 KV cache only");
   if (start_pos < 0 || start_pos + n > m->cfg.max_seq) return fail(HH_ERR_RANGE, "sequence exceeds max_seq");
   for (int i = 0; i < n; ++i)
     if (tokens[i] >= (uint32_t)m->cfg.vocab) return fail(HH_ERR_RANGE, "prompt token out of range");

@@ -65,6 +65,7 @@ class ModelConfigC(C.Structure):
         ("wtype", C.c_int), ("head_type", C.c_int), ("qk_norm", C.c_int),
         ("full_attn_interval", C.c_int), ("ssm_n_k_heads", C.c_int), ("ssm_n_v_heads", C.c_int),
         ("ssm_head_dim", C.c_int), ("ssm_conv_kernel", C.c_int), ("attn_out_gate", C.c_int),
+        ("kv_type", C.c_int),
     ]
 
 
@@ -92,6 +93,7 @@ class ModelConfig:
     ssm_head_dim: int = 128
     ssm_conv_kernel: int = 4
     attn_out_gate: int = 0
+    kv_type: int = 0        # 0 = f32 KV cache, 8 = Q8_0 rows
 
     def to_c(self) -> ModelConfigC:
         return ModelConfigC(*[getattr(self, f[0]) for f in ModelConfigC._fields_])

@@ -140,6 +140,9 @@ typedef struct {
   int full_attn_interval; /* qwen35: layer i is full attention iff (i+1)%interval==0 */
   int ssm_n_k_heads, ssm_n_v_heads, ssm_head_dim, ssm_conv_kernel;
   int attn_out_gate;      /* qwen35 full attention: attn_q emits [q_h | gate_h] */
+  int kv_type;            /* HH_F32 (0): f32 cache (KVStorage::F32, the default); HH_Q8_0: Q8_0 rows
+                             (KVStorage::Q8_0, kvcache.rs:41-57, written by write_kv :92-113, read
+                             through the dequantized rows as attention_q8_0, ops.rs:946-1030) */
 } hh_model_config;
 
 /* Allocates every weight (native GGUF block layout, uploaded once), the f32 KV

@@ -1204,6 +1204,21 @@ void ho_model_reset(ho_model* m) {
   }
 }
 
+/* KVStorage::Q8_0 (kvcache.rs:41-57): write_kv quantizes the row into Q8_0
+ * blocks (:92-113, quantize_q8_0_block :274-303) and every reader dequantizes
+ * it (:287-317, attention_q8_0 ops.rs:946-1030: the int8 times the f16 scale,
+ * exact in f32).  Holding dequant(quant(row)) in f32 is therefore the same
+ * cache as seen by attention. */
+static void kv_store_row(const ho_config* c, float* dst, const float* src, int hd) {
+  if (c->kv_type != HO_Q8_0) {
+    memcpy(dst, src, sizeof(float) * hd);
+    return;
+  }
+  uint8_t blk[34 * 16];
+  ho_quantize_q8_0(src, hd, blk);
+  ho_dequantize(HO_Q8_0, blk, hd, dst);
+}
+
 /* KV prefill with N(0,1) values rounded to fp16 (stored exactly in f32):
  * value(layer l, kv head h, pos p, dim j) = f16(I * (1/sd)) with stream
  * "blk.<l>.kv_k" / "blk.<l>.kv_v", index ((p * n_kv) + h) * hd + j. */
@@ -1222,12 +1237,15 @@ int ho_model_kv_prefill_synth(ho_model* m, uint64_t seed, int n_pos) {
     for (int h = 0; h < c->n_kv_heads; h++) {
       float* kb = m->k_cache + ((size_t)ly->attn_idx * c->n_kv_heads + h) * (size_t)c->max_seq * hd;
       float* vb = m->v_cache + ((size_t)ly->attn_idx * c->n_kv_heads + h) * (size_t)c->max_seq * hd;
-      for (int p = 0; p < n_pos; p++)
+      for (int p = 0; p < n_pos; p++) {
         for (int j = 0; j < hd; j++) {
           uint64_t idx = ((uint64_t)p * c->n_kv_heads + h) * hd + j;
           kb[(size_t)p * hd + j] = ho_f16_to_f32(ho_f32_to_f16((float)ho_synth_int(kk, idx) * cs));
           vb[(size_t)p * hd + j] = ho_f16_to_f32(ho_f32_to_f16((float)ho_synth_int(kvk, idx) * cs));
         }
+        kv_store_row(c, kb + (size_t)p * hd, kb + (size_t)p * hd, hd);
+        kv_store_row(c, vb + (size_t)p * hd, vb + (size_t)p * hd, hd);
+      }
     }
     m->cur_len[ly->attn_idx] = n_pos;
   }
@@ -1335,8 +1353,8 @@ static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
     float* kbase = m->k_cache + (size_t)ai * nkvh * head_stride;
     float* vbase = m->v_cache + (size_t)ai * nkvh * head_stride;
     for (int h = 0; h < nkvh; h++) { /* kvcache.rs:92-113 */
-      memcpy(kbase + h * head_stride + (size_t)pos * hd, m->k + h * hd, sizeof(float) * hd);
-      memcpy(vbase + h * head_stride + (size_t)pos * hd, m->v + h * hd, sizeof(float) * hd);
+      kv_store_row(c, kbase + h * head_stride + (size_t)pos * hd, m->k + h * hd, hd);
+      kv_store_row(c, vbase + h * head_stride + (size_t)pos * hd, m->v + h * hd, hd);
     }
     int seq_len = m->cur_len[ai] + 1; /* mod.rs:474: current_len before this write + 1 */
     if (pos + 1 > m->cur_len[ai]) m->cur_len[ai] = pos + 1;
@@ -1521,8 +1539,8 @@ static void attn_layer_q35(ho_model* m, int pos, layer_t* ly) {
   float* kb = m->k_cache + (size_t)ai * nkvh * hs;
   float* vb = m->v_cache + (size_t)ai * nkvh * hs;
   for (int h = 0; h < nkvh; h++) {
-    memcpy(kb + h * hs + (size_t)pos * hd, m->k + h * hd, sizeof(float) * hd);
-    memcpy(vb + h * hs + (size_t)pos * hd, m->v + h * hd, sizeof(float) * hd);
+    kv_store_row(c, kb + h * hs + (size_t)pos * hd, m->k + h * hd, hd);
+    kv_store_row(c, vb + h * hs + (size_t)pos * hd, m->v + h * hd, hd);
   }
   if (pos + 1 > m->cur_len[ai]) m->cur_len[ai] = pos + 1;
   int seq_len = m->cur_len[ai];

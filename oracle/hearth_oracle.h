@@ -94,6 +94,7 @@ typedef struct {
   int full_attn_interval; /* layer i is full attention iff (i+1) % interval == 0 */
   int ssm_n_k_heads, ssm_n_v_heads, ssm_head_dim, ssm_conv_kernel;
   int attn_out_gate;   /* full-attention layers emit [q|gate] per head */
+  int kv_type;         /* HO_F32 or HO_Q8_0 (KVStorage, kvcache.rs:6-9) */
 } ho_config;
 
 typedef struct ho_model ho_model;

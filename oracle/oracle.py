@@ -25,6 +25,7 @@ class HoConfig(C.Structure):
         ("wtype", C.c_int), ("head_type", C.c_int), ("qk_norm", C.c_int),
         ("full_attn_interval", C.c_int), ("ssm_n_k_heads", C.c_int), ("ssm_n_v_heads", C.c_int),
         ("ssm_head_dim", C.c_int), ("ssm_conv_kernel", C.c_int), ("attn_out_gate", C.c_int),
+        ("kv_type", C.c_int),
     ]
 
 

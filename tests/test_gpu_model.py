@@ -223,3 +223,47 @@ def test_ptq1_0_model_equals_q2_0_model(ctx, cfg):
     assert np.array_equal(la, lb)
     ma.close()
     mb.close()
+
+
+@pytest.mark.parametrize("cfg,pen", [(TINY.replace(kv_type=8), 1.1), (TINY_HYB.replace(kv_type=8), 1.0)],
+                         ids=["dense", "hybrid"])
+def test_q8_0_kv_cache_parity(ctx, oracle, cfg, pen):
+    """KVStorage::Q8_0 (kvcache.rs:41-57): rows quantized on write, attention over
+    the dequantized rows (attention_q8_0, ops.rs:946-1030).  Logits and tokens
+    equal the device-order oracle holding dequant(quantize(row))."""
+    m, o = make(ctx, oracle, cfg, seed=17)
+    prompt = [oracle.synth_token(17, i, cfg.vocab) for i in range(6)]
+    toks, lg = m.generate(prompt, 24, repeat_pen=pen, want_logits=True)
+    tw, lw = o.generate(prompt, 24, repeat_pen=pen, want_logits=True)
+    assert list(toks) == list(tw)
+    assert rel(lg, lw) < 1e-3
+    assert np.array_equal(lg, lw)
+    # the cache is really quantized: the f32-cache model diverges from it
+    o32 = oracle.OracleModel(cfg.replace(kv_type=0), seed=17, threads=16, order=1)
+    _, l32 = o32.generate(prompt, 24, repeat_pen=pen, want_logits=True)
+    assert not np.array_equal(lg, l32)
+    o32.close()
+
+
+def test_q8_0_kv_prefilled_8b_shape(ctx, oracle):
+    """8B geometry, 2 layers, Q8_0 KV prefilled to 2048 positions (the seeded
+    fp16 values quantized per 32-block), greedy decode from pos 2048."""
+    cfg = CONFIGS["8b-q2"].replace(n_layers=2, kv_type=8)
+    m, o = make(ctx, oracle, cfg, seed=3)
+    m.prefill_kv_synthetic(99, 2048)
+    o.prefill_kv_synthetic(99, 2048)
+    tok0 = oracle.synth_token(3, 0, cfg.vocab)
+    toks, lg = m.generate([tok0], 16, start_pos=2048, repeat_pen=1.1, want_logits=True)
+    tw, lw = o.generate([tok0], 16, start_pos=2048, repeat_pen=1.1, want_logits=True)
+    assert list(toks) == list(tw)
+    assert np.array_equal(lg, lw)
+
+
+def test_q8_0_kv_rejects_batched_prefill(ctx):
+    from hearth_amd import HHError, Model
+    m = Model(ctx, TINY.replace(kv_type=8))
+    m.synthesize(1)
+    with pytest.raises(HHError) as e:
+        m.prefill([1, 2, 3])
+    assert e.value.status == 2
+    m.close()
