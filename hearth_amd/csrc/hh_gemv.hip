@@ -527,6 +527,11 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     return p.w + ((size_t)grow * P + t) * UB;
   };
 
+  // With the RMSNorm prologue, lanes 0..NORM_L-1 stage the activation before
+  // issuing weights; they take the last units of each batch (none at all when
+  // the workgroup holds fewer than NT - NORM_L units).  Products are indexed by
+  // unit, so the mapping does not change any sum.
+  const int lt = PRO == PRO_RMSNORM ? ((tid + NORM_L) & (NT - 1)) : tid;
   const int NI = (U + NT - 1) / NT;
   const int NB = (NI + DEPTH - 1) / DEPTH;
   uint32_t wa[DEPTH][DW], wb[NU > 0 ? 1 : DEPTH][DW];
@@ -534,14 +539,14 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   auto load_batch = [&](uint32_t (&wr)[DEPTH][DW], int b) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      int lu = min((b * DEPTH + d) * NT + tid, U - 1);
+      int lu = min((b * DEPTH + d) * NT + lt, U - 1);
       load_unit<FMT>(wr[d], unit_addr(lu));
     }
   };
   auto comp_batch = [&](const uint32_t (&wr)[DEPTH][DW], int b) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      int lu = (b * DEPTH + d) * NT + tid;
+      int lu = (b * DEPTH + d) * NT + lt;
       if (lu < U) {
         int rl = lu / P, t = lu - rl * P;
         float pr[2];
@@ -556,11 +561,22 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   ActStage<FMT, PRO> act;
   act.issue(p);                      // activation first (in-order retirement)
   if constexpr (NU > 0 && PRO == PRO_RMSNORM) {
+    // Waves 0-3 stage the activation and raise `ready`; every wave computes as
+    // soon as `ready` is complete and its own weights have arrived.  No barrier
+    // separates the weight loads from the dot products: a CU's weight stream
+    // retires in issue order while the waves that issued first already compute.
+    __shared__ int ready;
+    if (tid == 0) ready = 0;
     act.part1(p, aq, ds, red);       // waits for this lane's activation loads
-    __syncthreads();
+    __syncthreads();                 // sum of squares complete, `ready` cleared
+    if (tid < NORM_L) {
+      act.part2(p, aq, ds, red);
+      if ((tid & 63) == 0) __hip_atomic_fetch_add(&ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     load_batch(wa, 0);               // the whole share of this lane
-    act.part2(p, aq, ds, red);
-    __syncthreads();
+    for (int it = 0; __hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < NORM_L / 64 &&
+                     it < (1 << 22); ++it)
+      __builtin_amdgcn_s_sleep(1);
     comp_batch(wa, 0);
   } else if constexpr (NU > 0) {
     load_batch(wa, 0);               // the whole share of this lane
