@@ -14,8 +14,8 @@
 // once per token.
 //
 // Kernel 1 (prep): workgroups [0, conv_dim/256) do conv + silu (+ L2 norm for
-//   the q/k channels, 2 heads of 128 per workgroup); the remaining workgroups
-//   compute alpha/beta for 4 v-heads each from rms_norm(hidden, attn_norm).
+//   the q/k channels, 2 heads of 128 per workgroup); then one workgroup per
+//   v-head computes its alpha/beta from rms_norm(hidden, attn_norm).
 // Kernel 2 (recurrence): workgroup (h, 32-column slice) updates its columns;
 //   the last of a head's workgroups applies the gated norm and writes the
 //   packed Q8_0 input of ssm_out.
@@ -56,27 +56,78 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
     }
     return;
   }
-  // alpha/beta for v-heads [4*j, 4*j+4)
-  extern __shared__ float xs[];   // d floats: rms_norm(hidden, attn_norm)
+  // alpha/beta of v-head h = blockIdx.x - n_conv_wg (matvec_dense :1015-1025 on
+  // rms_norm(hidden, attn_norm)).  Lane t holds the float4s at 4(t + 256j) +
+  // 4096c (the block_sumsq_f4 slots) of hidden, attn_norm and both weight rows,
+  // all loaded at once.  Order: lane t sums its normalized products in (c, j,
+  // element) order, each wave adds its lanes by butterfly, then
+  // (W0 + W1) + (W2 + W3).
   const int d = a.d;
-  float tot = block_sumsq_f4(a.hidden, d, red);
-  float inv = 1.0f / sqrtf(tot / (float)d + a.eps);
-  for (int i = tid; i < d; i += 256) xs[i] = a.hidden[i] * inv * a.attn_norm[i];
-  __syncthreads();
-  int h = ((int)blockIdx.x - n_conv_wg) * 4 + wid;
-  if (h >= a.n_v) return;
+  const int h = (int)blockIdx.x - n_conv_wg;
   const float* wa = a.w_alpha + (size_t)h * d;
   const float* wb = a.w_beta + (size_t)h * d;
-  float sa = 0.0f, sb = 0.0f;
-  for (int i = lane; i < d; i += 64) {
-    sa += wa[i] * xs[i];
-    sb += wb[i] * xs[i];
+  constexpr int NC = 2;   // d <= 8192
+  float4 hx[4][NC], hw[4][NC], va[4][NC], vb[4][NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * (tid + 256 * j) + 4096 * c;
+      hx[j][c] = hw[j][c] = va[j][c] = vb[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (e < d) {
+        hx[j][c] = *(const float4*)(a.hidden + e);
+        hw[j][c] = *(const float4*)(a.attn_norm + e);
+        va[j][c] = *(const float4*)(wa + e);
+        vb[j][c] = *(const float4*)(wb + e);
+      }
+    }
+  // sum of squares in block_sumsq_f4's order
+  float ss[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ss[j] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (4 * (tid + 256 * j) + 4096 * c < d)
+        ss[j] += hx[j][c].x * hx[j][c].x + hx[j][c].y * hx[j][c].y + hx[j][c].z * hx[j][c].z + hx[j][c].w * hx[j][c].w;
   }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ss[j] = wave_sum(ss[j]);
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wid + 4 * j] = ss[j];
+  }
+  __syncthreads();
+  const float inv = 1.0f / sqrtf(tree16(red) / (float)d + a.eps);
+  float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (4 * (tid + 256 * j) + 4096 * c >= d) continue;
+      const float x[4] = {hx[j][c].x * inv * hw[j][c].x, hx[j][c].y * inv * hw[j][c].y,
+                          hx[j][c].z * inv * hw[j][c].z, hx[j][c].w * inv * hw[j][c].w};
+      const float ua[4] = {va[j][c].x, va[j][c].y, va[j][c].z, va[j][c].w};
+      const float ub[4] = {vb[j][c].x, vb[j][c].y, vb[j][c].z, vb[j][c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sa = sa + ua[i] * x[i];
+        sb = sb + ub[i] * x[i];
+      }
+    }
   sa = wave_sum(sa);
   sb = wave_sum(sb);
+  __syncthreads();   // red reused
   if (lane == 0) {
-    a.ab[h] = softplus_f(sa + a.dt_bias[h]) * a.ssm_a[h];
-    a.ab[a.n_v + h] = 1.0f / (1.0f + hx_exp(-sb));
+    red[wid] = sa;
+    red[4 + wid] = sb;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const float A = (red[0] + red[1]) + (red[2] + red[3]);
+    const float B = (red[4] + red[5]) + (red[6] + red[7]);
+    a.ab[h] = softplus_f(A + a.dt_bias[h]) * a.ssm_a[h];
+    a.ab[a.n_v + h] = 1.0f / (1.0f + hx_exp(-B));
   }
 }
 
@@ -173,8 +224,8 @@ int hh_gdn_launch(const GdnArgs& a, hipStream_t s) {
   const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
   if (conv_dim % 256 || a.hd != 128 || a.kernel > 8) return 1;
   int n_conv_wg = conv_dim / 256;
-  int n_ab_wg = (a.n_v + 3) / 4;
-  hipLaunchKernelGGL(k_gdn_prep, dim3(n_conv_wg + n_ab_wg), dim3(256), sizeof(float) * a.d, s, a);
+  if (a.d % 1024 || a.d > 8192) return 1;
+  hipLaunchKernelGGL(k_gdn_prep, dim3(n_conv_wg + a.n_v), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
   hipLaunchKernelGGL(k_gdn_rec, dim3(a.n_v * (a.hd / 32)), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;

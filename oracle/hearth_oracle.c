@@ -1401,16 +1401,26 @@ static void gdn_layer(ho_model* m, int li, layer_t* ly) {
   for (int r = 0; r < nv; r++) {
     const float* wa = (const float*)ly->ssm_alpha->data + (size_t)r * d;
     const float* wb = (const float*)ly->ssm_beta->data + (size_t)r * d;
-    if (m->order) {   /* lane-strided partial sums, butterfly */
-      float la[64], lb[64];
-      for (int l = 0; l < 64; l++) {
+    if (m->order) {   /* 256 lanes: lane t sums the float4s at 4(t+256j)+4096c in (c, j, element)
+                         order; each 64-lane wave by butterfly; (W0 + W1) + (W2 + W3) */
+      float la[256], lb[256], wa4[4], wb4[4];
+      for (int t = 0; t < 256; t++) {
         float a = 0.0f, b = 0.0f;
-        for (int j = l; j < d; j += 64) { a = a + wa[j] * m->normed[j]; b = b + wb[j] * m->normed[j]; }
-        la[l] = a;
-        lb[l] = b;
+        for (int cc = 0; 4096 * cc < d; cc++)
+          for (int jj = 0; jj < 4; jj++) {
+            int e0 = 4 * (t + 256 * jj) + 4096 * cc;
+            if (e0 >= d) continue;
+            for (int i = 0; i < 4; i++) {
+              a = a + wa[e0 + i] * m->normed[e0 + i];
+              b = b + wb[e0 + i] * m->normed[e0 + i];
+            }
+          }
+        la[t] = a;
+        lb[t] = b;
       }
-      abuf[r] = bfly64(la);
-      bbuf[r] = bfly64(lb);
+      for (int w = 0; w < 4; w++) { wa4[w] = bfly64(la + 64 * w); wb4[w] = bfly64(lb + 64 * w); }
+      abuf[r] = (wa4[0] + wa4[1]) + (wa4[2] + wa4[3]);
+      bbuf[r] = (wb4[0] + wb4[1]) + (wb4[2] + wb4[3]);
       continue;
     }
     float acc = 0.0f, accb = 0.0f;
