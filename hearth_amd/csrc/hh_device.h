@@ -77,10 +77,10 @@ HH_DEV uint32_t f2h(float xf) {
 // s = (m-1)/(m+1), log m = 2 atanh(s) (odd series to s^13).  Every step is an
 // IEEE single operation with explicit fmaf, so the CPU checker evaluates the
 // identical function bit for bit.  Accuracy ~1-2 ulp (tested against libm).
-HH_DEV float hx_exp(float x) {
-  if (x != x) return x;
-  if (x > 88.72f) return __uint_as_float(0x7f800000u);
-  if (x < -87.33f) return 0.0f;   // results below the normal range are flushed (both sides)
+HH_DEV float hx_exp(float x_in) {
+  // branch-free: the range cases are selected at the end, the polynomial runs
+  // on the clamped argument (equal to x_in whenever its result is kept)
+  const float x = fminf(fmaxf(x_in, -87.33f), 88.72f);
   float n = rintf(x * 1.44269504088896341f);
   float r = fmaf(-n, 0.693145751953125f, x);
   r = fmaf(-n, 1.428606765330187e-06f, r);
@@ -94,7 +94,10 @@ HH_DEV float hx_exp(float x) {
   p = fmaf(p, r, 1.0f);
   int ni = (int)n;
   int n1 = ni / 2, n2 = ni - n1;
-  return p * __uint_as_float((uint32_t)(127 + n1) << 23) * __uint_as_float((uint32_t)(127 + n2) << 23);
+  float r_ = p * __uint_as_float((uint32_t)(127 + n1) << 23) * __uint_as_float((uint32_t)(127 + n2) << 23);
+  r_ = x_in > 88.72f ? __uint_as_float(0x7f800000u) : r_;
+  r_ = x_in < -87.33f ? 0.0f : r_;   // results below the normal range are flushed (both sides)
+  return x_in != x_in ? x_in : r_;
 }
 HH_DEV float hx_log(float x) {
   if (!(x > 0.0f)) return x == 0.0f ? __uint_as_float(0xff800000u) : __uint_as_float(0x7fc00000u);

@@ -16,9 +16,8 @@
 // Kernel 1 (prep): workgroups [0, conv_dim/256) do conv + silu (+ L2 norm for
 //   the q/k channels, 2 heads of 128 per workgroup); then one workgroup per
 //   v-head computes its alpha/beta from rms_norm(hidden, attn_norm).
-// Kernel 2 (recurrence): workgroup (h, 32-column slice) updates its columns;
-//   the last of a head's workgroups applies the gated norm and writes the
-//   packed Q8_0 input of ssm_out.
+// Kernel 2 (recurrence): one workgroup per v-head updates the head's state,
+//   then applies the gated norm and writes the packed Q8_0 input of ssm_out.
 #include "hh_kernels.h"
 
 namespace {
@@ -131,37 +130,49 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   }
 }
 
-// workgroup (h, jb): columns j in [jb*32, jb*32+32), thread = (i-chunk ic, column jj)
-__global__ __launch_bounds__(256) void k_gdn_rec(GdnArgs a) {
+// One 1024-lane workgroup per v-head h.  Lane = (column slice jb, row chunk
+// ic, column jj): column j = 32 jb + jj, rows 16 ic .. 16 ic + 15.  The
+// column dots sum the 8 row-chunk partials in chunk order.  The gated norm of
+// the head's 128 outputs then runs in wave 0 from LDS.
+__global__ __launch_bounds__(1024) void k_gdn_rec(GdnArgs a) {
   const int tid = threadIdx.x;
-  const int hd = a.hd;                       // 128
-  const int h = blockIdx.x / (hd / 32), jb = blockIdx.x % (hd / 32);
-  const int jj = tid & 31, ic = tid >> 5;    // 8 chunks of 16 rows
+  constexpr int hd = 128;
+  const int h = blockIdx.x;
+  const int jj = tid & 31, ic = (tid >> 5) & 7, jb = tid >> 8;
   const int j = jb * 32 + jj;
   const int kg = h % a.n_k;
   const int kdim = a.n_k * hd;
   const float* qn = a.qk + (size_t)kg * hd;
   const float* kn = a.qk + kdim + (size_t)kg * hd;
-  const float decay = hx_exp(a.ab[h]);
-  const float b = a.ab[a.n_v + h];
   float* S = a.state + (size_t)h * hd * hd;
-  __shared__ float part[8][33];
-  __shared__ float kv_s[2][128];
-  __shared__ int is_last;
-  if (tid < hd) { kv_s[0][tid] = kn[tid]; kv_s[1][tid] = qn[tid]; }
+  __shared__ float part[4][8][33];
+  __shared__ float kv_s[2][hd];
+  __shared__ float o_s[hd];
   float sreg[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) sreg[r] = S[(size_t)(ic * 16 + r) * hd + j];
+  const float vj = a.vconv[(size_t)h * hd + j];
+  const float decay = hx_exp(a.ab[h]);
+  const float b = a.ab[a.n_v + h];
+  if (tid < hd) { kv_s[0][tid] = kn[tid]; kv_s[1][tid] = qn[tid]; }
+  // wave 0 also fetches the gate and norm weight of its two elements
+  float zg[2] = {0.0f, 0.0f}, nw[2] = {0.0f, 0.0f};
+  if (tid < 64) {
+    zg[0] = a.z[(size_t)h * hd + tid];
+    zg[1] = a.z[(size_t)h * hd + 64 + tid];
+    nw[0] = a.ssm_norm[tid];
+    nw[1] = a.ssm_norm[64 + tid];
+  }
   __syncthreads();
   float dp = 0.0f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) dp += sreg[r] * kv_s[0][ic * 16 + r];
-  part[ic][jj] = dp;
+  part[jb][ic][jj] = dp;
   __syncthreads();
   float dot = 0.0f;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) dot += part[c][jj];
-  float bd = b * (a.vconv[(size_t)h * hd + j] - dot);
+  for (int c = 0; c < 8; ++c) dot += part[jb][c][jj];
+  const float bd = b * (vj - dot);
   float op = 0.0f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -170,51 +181,39 @@ __global__ __launch_bounds__(256) void k_gdn_rec(GdnArgs a) {
     op += sn * kv_s[1][ic * 16 + r];
   }
   __syncthreads();
-  part[ic][jj] = op;
+  part[jb][ic][jj] = op;
   __syncthreads();
   if (ic == 0) {
     float o = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) o += part[c][jj];
-    a.obuf[(size_t)h * hd + j] = o * (1.0f / sqrtf((float)hd));
-  }
-  // last column-slice of head h: gated RMSNorm + Q8_0 of the head's 128 outputs
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    is_last = atomicAdd(a.counter + h, 1) == hd / 32 - 1;
+    for (int c = 0; c < 8; ++c) o += part[jb][c][jj];
+    o_s[j] = o * (1.0f / sqrtf((float)hd));
   }
   __syncthreads();
-  if (!is_last) return;
-  __threadfence();
   if (tid >= 64) return;
+  // gated RMSNorm + Q8_0 of the head's outputs (qwen35.rs:1425-1439)
   const int lane = tid;
-  float v0 = a.obuf[(size_t)h * hd + lane], v1 = a.obuf[(size_t)h * hd + 64 + lane];
-  float ss = wave_sum(v0 * v0 + v1 * v1);
-  float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
-  float vals[2] = {v0, v1};
+  const float v0 = o_s[lane], v1 = o_s[64 + lane];
+  const float ss = wave_sum(v0 * v0 + v1 * v1);
+  const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+  const float vals[2] = {v0, v1};
+  const int Kv = a.n_v * hd;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
-    int dd = k * 64 + lane;
-    float nv = vals[k] * inv * a.ssm_norm[dd];
-    float z = a.z[(size_t)h * hd + dd];
-    float o = nv * (z / (1.0f + hx_exp(-z)));
-    if (a.out_f32) a.out_f32[(size_t)h * hd + dd] = o;
-    float am = group_max<32>(fabsf(o));
-    float sc = q8_scale(am);
-    int q = q8_round_r(o, sc, q8_rcp(sc));
-    int qs = group_sum_i<32>(q);
-    int e = h * hd + dd;
-    int Kv = a.n_v * hd;
+    const int dd = k * 64 + lane;
+    const float nv = vals[k] * inv * nw[k];
+    const float z = zg[k];
+    const float o = nv * (z / (1.0f + hx_exp(-z)));
+    const float am = group_max<32>(fabsf(o));
+    const float sc = q8_scale(am);
+    const int q = q8_round_r(o, sc, q8_rcp(sc));
+    const int qs = group_sum_i<32>(q);
+    const int e = h * hd + dd;
     a.act_out[perm_pos(a.act_fmt, e)] = (uint8_t)(int8_t)q;
     if ((lane & 31) == 0) {
       ((float*)(a.act_out + Kv))[e >> 5] = h2f(f2h(sc));
       ((int*)(a.act_out + Kv + (Kv / 32) * 4))[e >> 5] = qs;
     }
-  }
-  if (lane == 0) {
-    a.counter[h] = 0;
-    __threadfence();
   }
 }
 
@@ -227,6 +226,6 @@ int hh_gdn_launch(const GdnArgs& a, hipStream_t s) {
   if (a.d % 1024 || a.d > 8192) return 1;
   hipLaunchKernelGGL(k_gdn_prep, dim3(n_conv_wg + a.n_v), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
-  hipLaunchKernelGGL(k_gdn_rec, dim3(a.n_v * (a.hd / 32)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_gdn_rec, dim3(a.n_v), dim3(1024), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }

@@ -129,12 +129,9 @@ struct GdnArgs {
   float eps;
   uint8_t* act_out;       // packed activation of the gated-norm output (K = v_dim)
   int act_fmt;
-  float* out_f32;         // optional
   float* ab;              // scratch [2*n_v]
   float* qk;              // scratch [2*k_dim] conv+silu+l2norm q,k
   float* vconv;           // scratch [v_dim]
-  float* obuf;            // scratch [v_dim] recurrence output
   const float* z;         // [v_dim] gate projection
-  int* counter;           // [n_v]
 };
 int hh_gdn_launch(const GdnArgs& a, hipStream_t s);

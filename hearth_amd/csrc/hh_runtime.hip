@@ -315,12 +315,9 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
       ga.eps = c.eps;
       ga.act_out = m->act_mid;
       ga.act_fmt = wf;
-      ga.out_f32 = nullptr;
       ga.ab = m->gdn_scratch;
       ga.qk = m->gdn_scratch + 256;
       ga.vconv = ga.qk + 2 * kdim;
-      ga.obuf = ga.vconv + vdim;
-      ga.counter = m->counters + 128;
       if (want(2, li)) KTRY(hh_gdn_launch(ga, s));
       k_out = vdim;
     } else {
@@ -853,7 +850,7 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   HIP_TRY(hipMemset(m->counters, 0, sizeof(int) * 256));
   HIP_TRY(hipMalloc(&m->attn_po, sizeof(float) * (size_t)c.n_kv_heads * m->attn_splits * G * hd));
   HIP_TRY(hipMalloc(&m->attn_pml, sizeof(float) * (size_t)c.n_kv_heads * m->attn_splits * G * 2));
-  HIP_TRY(hipMalloc(&m->gdn_scratch, sizeof(float) * (size_t)(256 + 2 * kdim + 2 * vdim + 64)));
+  HIP_TRY(hipMalloc(&m->gdn_scratch, sizeof(float) * (size_t)(256 + 2 * kdim + vdim + 64)));
   HIP_TRY(hipMalloc(&m->counts, sizeof(int) * c.vocab));
   HIP_TRY(hipMemset(m->counts, 0, sizeof(int) * c.vocab));
   HIP_TRY(hipMalloc(&m->prompt, sizeof(uint32_t) * (c.max_seq + 8)));
