@@ -24,19 +24,34 @@ namespace {
 
 HH_DEV float softplus_f(float x) { return x > 20.0f ? x : hx_log(1.0f + hx_exp(x)); }
 
+// ROWS = false: the decode step (one token; the conv window comes from
+// conv_state, which is advanced).  ROWS = true: token s = blockIdx.y of a
+// batched prefill; the window's earlier inputs come from the projection rows
+// of tokens s-1, s-2, ... and, before the first token, from conv_state, which
+// k_gdn_conv_advance moves on afterwards.
+template <bool ROWS>
 __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
   const int n_conv_wg = conv_dim / 256;
+  const int s = ROWS ? (int)blockIdx.y : 0;
   __shared__ float red[16];
   if ((int)blockIdx.x < n_conv_wg) {
     const int ch = blockIdx.x * 256 + tid;
     const int K = a.kernel;
     float win[8];
     float* cs = a.conv_state + (size_t)ch * (K - 1);
-    for (int t = 0; t < K - 1; ++t) win[t] = cs[t];
-    win[K - 1] = a.proj[ch];
-    for (int t = 0; t < K - 1; ++t) cs[t] = win[t + 1];
+    if constexpr (ROWS) {
+      for (int t = 0; t < K - 1; ++t) {
+        const int u = s - (K - 1) + t;   // token of window slot t
+        win[t] = u >= 0 ? a.proj[(size_t)u * a.row_in + ch] : cs[s + t];
+      }
+      win[K - 1] = a.proj[(size_t)s * a.row_in + ch];
+    } else {
+      for (int t = 0; t < K - 1; ++t) win[t] = cs[t];
+      win[K - 1] = a.proj[ch];
+      for (int t = 0; t < K - 1; ++t) cs[t] = win[t + 1];
+    }
     const float* w = a.conv_w + (size_t)ch * K;
     float acc = 0.0f;
     for (int t = 0; t < K; ++t) acc += w[t] * win[t];
@@ -49,9 +64,9 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
       int hw = wid & ~1;
       float tot = red[hw] + red[hw + 1];
       float inv = 1.0f / sqrtf(tot + a.eps);
-      a.qk[ch] = y * inv;
+      a.qk[(size_t)s * 2 * kdim + ch] = y * inv;
     } else {
-      a.vconv[ch - 2 * kdim] = y;
+      a.vconv[(size_t)s * vdim + ch - 2 * kdim] = y;
     }
     return;
   }
@@ -74,7 +89,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
       const int e = 4 * (tid + 256 * j) + 4096 * c;
       hx[j][c] = hw[j][c] = va[j][c] = vb[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (e < d) {
-        hx[j][c] = *(const float4*)(a.hidden + e);
+        hx[j][c] = *(const float4*)(a.hidden + (size_t)s * d + e);
         hw[j][c] = *(const float4*)(a.attn_norm + e);
         va[j][c] = *(const float4*)(wa + e);
         vb[j][c] = *(const float4*)(wb + e);
@@ -125,8 +140,8 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   if (tid == 0) {
     const float A = (red[0] + red[1]) + (red[2] + red[3]);
     const float B = (red[4] + red[5]) + (red[6] + red[7]);
-    a.ab[h] = softplus_f(A + a.dt_bias[h]) * a.ssm_a[h];
-    a.ab[a.n_v + h] = 1.0f / (1.0f + hx_exp(-B));
+    a.ab[(size_t)s * 2 * a.n_v + h] = softplus_f(A + a.dt_bias[h]) * a.ssm_a[h];
+    a.ab[(size_t)s * 2 * a.n_v + a.n_v + h] = 1.0f / (1.0f + hx_exp(-B));
   }
 }
 
@@ -217,6 +232,116 @@ __global__ __launch_bounds__(1024) void k_gdn_rec(GdnArgs a) {
   }
 }
 
+// Batched prefill: conv_state after S tokens holds the last K-1 inputs.
+__global__ __launch_bounds__(256) void k_gdn_conv_advance(GdnArgs a) {
+  const int kdim = a.n_k * a.hd, conv_dim = 2 * kdim + a.n_v * a.hd;
+  const int ch = blockIdx.x * 256 + threadIdx.x;
+  if (ch >= conv_dim) return;
+  const int K = a.kernel, S = a.S;
+  float* cs = a.conv_state + (size_t)ch * (K - 1);
+  float nw[7];
+  for (int t = 0; t < K - 1; ++t) {
+    const int u = S - (K - 1) + t;
+    nw[t] = u >= 0 ? a.proj[(size_t)u * a.row_in + ch] : cs[S + t];
+  }
+  for (int t = 0; t < K - 1; ++t) cs[t] = nw[t];
+}
+
+// Batched prefill recurrence: workgroup h runs k_gdn_rec's per-token
+// arithmetic for tokens 0 .. S-1 in order with the head's state held in
+// registers, and writes o (before the gated norm) to o_rows[s][v_dim].  The
+// next token's inputs are loaded while the current one is computed.
+__global__ __launch_bounds__(1024) void k_gdn_rec_rows(GdnArgs a) {
+  const int tid = threadIdx.x;
+  constexpr int hd = 128;
+  const int h = blockIdx.x;
+  const int jj = tid & 31, ic = (tid >> 5) & 7, jb = tid >> 8;
+  const int j = jb * 32 + jj;
+  const int kg = h % a.n_k;
+  const int kdim = a.n_k * hd, vdim = a.n_v * hd, S = a.S;
+  float* St = a.state + (size_t)h * hd * hd;
+  __shared__ float part[2][4][8][33];
+  __shared__ float kv_s[2][hd];
+  float sreg[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sreg[r] = St[(size_t)(ic * 16 + r) * hd + j];
+  const float* qk0 = a.qk + (size_t)kg * hd + (tid & (hd - 1)) + (tid < hd ? kdim : 0);
+  // token 0's inputs
+  float nkq = tid < 2 * hd ? qk0[0] : 0.0f;
+  float nvj = a.vconv[(size_t)h * hd + j];
+  float ng = a.ab[h], nb = a.ab[a.n_v + h];
+  const float inv_hd = 1.0f / sqrtf((float)hd);
+  for (int s = 0; s < S; ++s) {
+    const float kq = nkq, vj = nvj, g = ng, b = nb;
+    if (s + 1 < S) {
+      const size_t n = (size_t)(s + 1);
+      if (tid < 2 * hd) nkq = qk0[n * 2 * kdim];
+      nvj = a.vconv[n * vdim + (size_t)h * hd + j];
+      ng = a.ab[n * 2 * a.n_v + h];
+      nb = a.ab[n * 2 * a.n_v + a.n_v + h];
+    }
+    // lanes 0..127 carry k, 128..255 carry q
+    if (tid < 2 * hd) kv_s[tid >> 7][tid & (hd - 1)] = kq;
+    const float decay = hx_exp(g);
+    __syncthreads();
+    float dp = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dp += sreg[r] * kv_s[0][ic * 16 + r];
+    part[0][jb][ic][jj] = dp;
+    __syncthreads();
+    float dot = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) dot += part[0][jb][c][jj];
+    const float bd = b * (vj - dot);
+    float op = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sreg[r] = sreg[r] * decay + kv_s[0][ic * 16 + r] * bd;
+      op += sreg[r] * kv_s[1][ic * 16 + r];
+    }
+    part[1][jb][ic][jj] = op;
+    __syncthreads();
+    if (ic == 0) {
+      float o = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o += part[1][jb][c][jj];
+      a.o_rows[(size_t)s * vdim + (size_t)h * hd + j] = o * inv_hd;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) St[(size_t)(ic * 16 + r) * hd + j] = sreg[r];
+}
+
+// Gated RMSNorm + Q8_0 of o_rows (k_gdn_rec's tail per token and head), into
+// the GEMM's split activation layout xq[S][v_dim], xd[S][v_dim/32].
+// Workgroup (s, 4 heads), one wave per head.
+__global__ __launch_bounds__(256) void k_gdn_gated_rows(GdnArgs a) {
+  constexpr int hd = 128;
+  const int lane = threadIdx.x & 63;
+  const int s = blockIdx.y, h = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (h >= a.n_v) return;
+  const int kdim = a.n_k * hd, vdim = a.n_v * hd;
+  const float* o = a.o_rows + (size_t)s * vdim + (size_t)h * hd;
+  const float* z = a.proj + (size_t)s * a.row_in + 2 * kdim + vdim + (size_t)h * hd;
+  const float v0 = o[lane], v1 = o[64 + lane];
+  const float ss = wave_sum(v0 * v0 + v1 * v1);
+  const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+  const float vals[2] = {v0, v1};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int dd = k * 64 + lane;
+    const float nv = vals[k] * inv * a.ssm_norm[dd];
+    const float zz = z[dd];
+    const float y = nv * (zz / (1.0f + hx_exp(-zz)));
+    const float am = group_max<32>(fabsf(y));
+    const float sc = q8_scale(am);
+    const int q = q8_round_r(y, sc, q8_rcp(sc));
+    const int e = h * hd + dd;
+    a.xq[(size_t)s * vdim + e] = (int8_t)q;
+    if ((lane & 31) == 0) a.xd[(size_t)s * (vdim / 32) + (e >> 5)] = h2f(f2h(sc));
+  }
+}
+
 }  // namespace
 
 int hh_gdn_launch(const GdnArgs& a, hipStream_t s) {
@@ -224,8 +349,26 @@ int hh_gdn_launch(const GdnArgs& a, hipStream_t s) {
   if (conv_dim % 256 || a.hd != 128 || a.kernel > 8) return 1;
   int n_conv_wg = conv_dim / 256;
   if (a.d % 1024 || a.d > 8192) return 1;
-  hipLaunchKernelGGL(k_gdn_prep, dim3(n_conv_wg + a.n_v), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_gdn_prep<false>, dim3(n_conv_wg + a.n_v), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
   hipLaunchKernelGGL(k_gdn_rec, dim3(a.n_v), dim3(1024), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// Batched prefill of one GDN layer over a.S tokens (the proj rows already hold
+// the in_proj outputs): prep per token, conv window advance, recurrence,
+// gated norm rows.
+int hh_gdn_rows_launch(const GdnArgs& a, hipStream_t s) {
+  const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
+  if (conv_dim % 256 || a.hd != 128 || a.kernel > 8 || a.kernel < 2) return 1;
+  if (a.d % 1024 || a.d > 8192 || a.S <= 0 || a.S > 65535) return 1;
+  const int n_conv_wg = conv_dim / 256;
+  hipLaunchKernelGGL(k_gdn_prep<true>, dim3(n_conv_wg + a.n_v, a.S), dim3(256), 0, s, a);
+  if (hipGetLastError() != hipSuccess) return 1;
+  hipLaunchKernelGGL(k_gdn_conv_advance, dim3(n_conv_wg), dim3(256), 0, s, a);
+  if (hipGetLastError() != hipSuccess) return 1;
+  hipLaunchKernelGGL(k_gdn_rec_rows, dim3(a.n_v), dim3(1024), 0, s, a);
+  if (hipGetLastError() != hipSuccess) return 1;
+  hipLaunchKernelGGL(k_gdn_gated_rows, dim3((a.n_v + 3) / 4, a.S), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }

@@ -82,10 +82,11 @@ int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd,
 int hh_add_rows_launch(float* H, const float* T, int64_t n, hipStream_t s);
 int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_kv, const float* q_norm,
                          const float* k_norm, float eps, const float* rope, int rope_dim, int max_seq, int pos0, int S,
-                         float* k_cache, float* v_cache, float* QB, hipStream_t s);
+                         int gated, float* k_cache, float* v_cache, float* QB, hipStream_t s);
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
-                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML, int8_t* yq,
-                           float* yd, hipStream_t s);
+                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
+                           const float* gate, int gate_row, int8_t* yq, float* yd, hipStream_t s);
+// gate: qwen35 gated attention's projection rows (gate_row floats apart), or null
 
 // Batched Q8_0 GEMM on int8 MFMA (prefill): out[s*n + r], K % 128 == 0, activations
 // split (int8 xq[seq][K], f32 xd[seq][K/32]); hh_q8_split_launch converts standard Q8_0 rows.
@@ -133,5 +134,13 @@ struct GdnArgs {
   float* qk;              // scratch [2*k_dim] conv+silu+l2norm q,k
   float* vconv;           // scratch [v_dim]
   const float* z;         // [v_dim] gate projection
+  // batched prefill (hh_gdn_rows_launch): qk, vconv, ab, hidden are per-token
+  // rows [S][...]; proj rows are row_in floats apart
+  int S;
+  int row_in;
+  float* o_rows;          // [S][v_dim] recurrence outputs
+  int8_t* xq;             // [S][v_dim] gated-norm Q8_0 codes (GEMM split layout)
+  float* xd;              // [S][v_dim/32] scales
 };
 int hh_gdn_launch(const GdnArgs& a, hipStream_t s);
+int hh_gdn_rows_launch(const GdnArgs& a, hipStream_t s);

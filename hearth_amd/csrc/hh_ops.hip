@@ -598,7 +598,7 @@ template <int HD>
 __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QKV, int n_in, int n_heads, int n_kv,
                                                     const float* __restrict__ q_norm, const float* __restrict__ k_norm,
                                                     float eps, const float* __restrict__ rope, int rope_dim,
-                                                    int max_seq, int pos0, float* __restrict__ k_cache,
+                                                    int max_seq, int pos0, int gated, float* __restrict__ k_cache,
                                                     float* __restrict__ v_cache, float* __restrict__ QB) {
   constexpr int LPR = HD / 4;
   const int s = blockIdx.x, kvh = blockIdx.y, G = n_heads / n_kv;
@@ -608,8 +608,10 @@ __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QK
   if (grp > G) return;   // whole LPR-lane groups
   const bool is_k = grp == G;
   const int qh = kvh * G + grp;
-  float4 x = is_k ? *(const float4*)(row + (size_t)n_heads * HD + (size_t)kvh * HD + 4 * c)
-                  : *(const float4*)(row + (size_t)qh * HD + 4 * c);
+  // qwen35 gated attention interleaves [q_h | gate_h] per head (qwen35.rs:1552-1559)
+  const size_t qs = gated ? 2 * HD : HD, kv0 = (size_t)n_heads * qs;
+  float4 x = is_k ? *(const float4*)(row + kv0 + (size_t)kvh * HD + 4 * c)
+                  : *(const float4*)(row + (size_t)qh * qs + 4 * c);
   const float* nw = is_k ? k_norm : q_norm;
   if (nw) x = slice_norm<LPR>(x, *(const float4*)(nw + 4 * c), eps);
   if (rope) {
@@ -625,7 +627,7 @@ __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QK
   if (is_k) {
     const size_t off = ((size_t)kvh * max_seq + pos) * HD + 4 * c;
     *(float4*)(k_cache + off) = x;
-    *(float4*)(v_cache + off) = *(const float4*)(row + (size_t)(n_heads + n_kv) * HD + (size_t)kvh * HD + 4 * c);
+    *(float4*)(v_cache + off) = *(const float4*)(row + kv0 + (size_t)n_kv * HD + (size_t)kvh * HD + 4 * c);
   } else {
     *(float4*)(QB + (size_t)s * n_heads * HD + (size_t)qh * HD + 4 * c) = x;
   }
@@ -770,6 +772,7 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restrict__ PO, const float* __restrict__ PML,
                                                             int n_heads, int n_kv, int n_chunks, int pos0, int t0,
+                                                            const float* __restrict__ gate, int gate_row,
                                                             int8_t* __restrict__ yq, float* __restrict__ yd) {
   extern __shared__ __align__(16) float wm[];
   float* wts = wm;                         // n_chunks
@@ -824,6 +827,10 @@ __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restr
   if (wid != 0) return;
   float o = (pw[lane] + pw[64 + lane]) + (pw[128 + lane] + pw[192 + lane]);
   o = o * (1.0f / *sL);
+  if (gate) {   // qwen35.rs:1627-1629, as k_attn_merge
+    const float g = gate[(size_t)s * gate_row + (size_t)qh * 2 * HD + HD + d];
+    o = o / (1.0f + hx_exp(-g));
+  }
   const float am = group_max<32>(fabsf(o));
   const float scq = q8_scale(am);
   const int q = q8_round_r(o, scq, q8_rcp(scq));
@@ -1164,14 +1171,14 @@ int hh_add_rows_launch(float* H, const float* T, int64_t n, hipStream_t s) {
 
 int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_kv, const float* q_norm,
                          const float* k_norm, float eps, const float* rope, int rope_dim, int max_seq, int pos0, int S,
-                         float* k_cache, float* v_cache, float* QB, hipStream_t s) {
+                         int gated, float* k_cache, float* v_cache, float* QB, hipStream_t s) {
   const int G = n_heads / n_kv;
   if (hd == 128 && G + 1 <= 512 / 32)
     hipLaunchKernelGGL(k_prefill_qk<128>, dim3(S, n_kv), dim3(512), 0, s, QKV, n_in, n_heads, n_kv, q_norm, k_norm,
-                       eps, rope, rope_dim, max_seq, pos0, k_cache, v_cache, QB);
+                       eps, rope, rope_dim, max_seq, pos0, gated, k_cache, v_cache, QB);
   else if (hd == 256 && G + 1 <= 512 / 64)
     hipLaunchKernelGGL(k_prefill_qk<256>, dim3(S, n_kv), dim3(512), 0, s, QKV, n_in, n_heads, n_kv, q_norm, k_norm,
-                       eps, rope, rope_dim, max_seq, pos0, k_cache, v_cache, QB);
+                       eps, rope, rope_dim, max_seq, pos0, gated, k_cache, v_cache, QB);
   else
     return 1;
   return ok();
@@ -1179,8 +1186,8 @@ int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_
 
 // Attention for tokens [t0, t0 + n) of a prefill; PO/PML hold n tokens' partials.
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
-                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML, int8_t* yq,
-                           float* yd, hipStream_t s) {
+                           int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
+                           const float* gate, int gate_row, int8_t* yq, float* yd, hipStream_t s) {
   const int G = n_heads / n_kv, TT = 16;
   if (G > 8 || n_kv * G != n_heads) return 1;
   const size_t split_lds = 4 * ((size_t)G * (8192 / hd) + 2 * G + 4 + (ATTN_NT / 64) * 4 * (size_t)hd);
@@ -1190,12 +1197,12 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
     hipLaunchKernelGGL((k_attn_prefill_split<128, ATTN_NT>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, v_cache,
                        n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML);
     hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, yq, yd);
+                       t0, gate, gate_row, yq, yd);
   } else if (hd == 256) {
     hipLaunchKernelGGL((k_attn_prefill_split<256, ATTN_NT>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, v_cache,
                        n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML);
     hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, yq, yd);
+                       t0, gate, gate_row, yq, yd);
   } else {
     return 1;
   }

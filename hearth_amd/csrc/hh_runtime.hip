@@ -395,24 +395,33 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
 // and row kernels that restate the decode step's arithmetic, writing the KV
 // cache; no logits (mod.rs:1201-1218 computes only the last token's, which the
 // caller runs through the decode step).
-int prefill_dense(hh_model* m, const uint32_t* toks, int S, int pos0) {
+// Batched prefill (forward_batch, mod.rs:899-1221) of S prompt tokens from
+// pos0: every projection is one MFMA GEMM over the S token rows.  Dense and
+// qwen35 full-attention layers run the split/merge attention per 128-token
+// tile; GDN layers run the per-token prep in parallel and the recurrence in
+// token order per v-head (the state stays in registers).  The result is the
+// state that feeding the tokens one at a time leaves, bit for bit.
+int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
   const hh_model_config& c = m->cfg;
   hipStream_t s = m->ctx->stream;
   const int d = c.d_model, hd = c.head_dim, nq = c.n_heads * hd, F = c.d_ffn;
-  const int n_in = nq + 2 * c.n_kv_heads * hd;
-  const int wt = c.wtype;
   const int TA = 128;                              // attention tokens per pass
   const int n_chunks = m->attn_splits, G = c.n_heads / c.n_kv_heads;
+  const bool hyb = c.arch == 1;
+  const int kdim = hyb ? c.ssm_n_k_heads * c.ssm_head_dim : 0, vdim = hyb ? c.ssm_n_v_heads * c.ssm_head_dim : 0;
+  int n_in_max = 0;
+  for (const Layer& L : m->layers) n_in_max = std::max(n_in_max, L.n_in);
+  const int kmax = std::max(std::max(d, F), std::max(nq, vdim));
   // scratch layout
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
-  const size_t oH = take((size_t)S * d * 4), oXq = take((size_t)S * std::max(d, F)),
-               oXd = take((size_t)S * (std::max(d, F) / 32) * 4),
-               oQKV = take((size_t)S * n_in * 4), oQB = take((size_t)S * nq * 4), oAq = take((size_t)S * nq),
-               oAd = take((size_t)S * (nq / 32) * 4),
+  const size_t oH = take((size_t)S * d * 4), oXq = take((size_t)S * kmax), oXd = take((size_t)S * (kmax / 32) * 4),
+               oQKV = take((size_t)S * n_in_max * 4), oQB = take((size_t)S * nq * 4),
                oT = take((size_t)S * d * 4), oGU = take((size_t)S * 2 * F * 4),
                oPO = take((size_t)TA * c.n_kv_heads * n_chunks * G * hd * 4),
-               oPML = take((size_t)TA * c.n_kv_heads * n_chunks * G * 2 * 4);
+               oPML = take((size_t)TA * c.n_kv_heads * n_chunks * G * 2 * 4),
+               oGQK = take(hyb ? (size_t)S * 2 * kdim * 4 : 0), oGV = take(hyb ? (size_t)S * vdim * 4 : 0),
+               oGAB = take(hyb ? (size_t)S * 2 * c.ssm_n_v_heads * 4 : 0), oGO = take(hyb ? (size_t)S * vdim * 4 : 0);
   if (off > m->pf_cap) {
     if (m->pf_buf) HIP_TRY(hipFree(m->pf_buf));
     m->pf_buf = nullptr;
@@ -426,8 +435,6 @@ int prefill_dense(hh_model* m, const uint32_t* toks, int S, int pos0) {
   float* Xd = (float*)(B + oXd);
   float* QKV = (float*)(B + oQKV);
   float* QB = (float*)(B + oQB);
-  int8_t* Aq = (int8_t*)(B + oAq);
-  float* Ad = (float*)(B + oAd);
   float* T = (float*)(B + oT);
   float* GU = (float*)(B + oGU);
   float* PO = (float*)(B + oPO);
@@ -436,14 +443,49 @@ int prefill_dense(hh_model* m, const uint32_t* toks, int S, int pos0) {
   for (int li = 0; li < c.n_layers; ++li) {
     Layer& L = m->layers[li];
     KTRY(hh_norm_q8_rows_launch(H, L.attn_norm, c.eps, d, S, Xq, Xd, s));
-    KTRY(hh_gemm_launch(m->wfmt, L.w_in, n_in, d, Xq, Xd, S, QKV, s));
-    KTRY(hh_prefill_qk_launch(hd, QKV, n_in, c.n_heads, c.n_kv_heads, c.qk_norm ? L.q_norm : nullptr,
-                              c.qk_norm ? L.k_norm : nullptr, c.eps, m->rope, m->rope_dim, c.max_seq, pos0, S,
-                              L.k_cache, L.v_cache, QB, s));
-    for (int t0 = 0; t0 < S; t0 += TA)
-      KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, c.max_seq, pos0, t0,
-                                  std::min(TA, S - t0), n_chunks, PO, PML, Aq, Ad, s));
-    KTRY(hh_gemm_launch(m->wfmt, L.w_out, d, nq, Aq, Ad, S, T, s));
+    KTRY(hh_gemm_launch(m->wfmt, L.w_in, L.n_in, d, Xq, Xd, S, QKV, s));
+    int k_out;
+    if (L.gdn) {
+      GdnArgs ga{};
+      ga.proj = QKV;
+      ga.hidden = H;
+      ga.attn_norm = L.attn_norm;
+      ga.w_alpha = L.ssm_alpha;
+      ga.w_beta = L.ssm_beta;
+      ga.dt_bias = L.ssm_dt;
+      ga.ssm_a = L.ssm_a;
+      ga.conv_w = L.ssm_conv;
+      ga.conv_state = L.conv_state;
+      ga.ssm_norm = L.ssm_norm;
+      ga.state = L.gdn_state;
+      ga.d = d;
+      ga.n_k = c.ssm_n_k_heads;
+      ga.n_v = c.ssm_n_v_heads;
+      ga.hd = c.ssm_head_dim;
+      ga.kernel = c.ssm_conv_kernel;
+      ga.eps = c.eps;
+      ga.qk = (float*)(B + oGQK);
+      ga.vconv = (float*)(B + oGV);
+      ga.ab = (float*)(B + oGAB);
+      ga.S = S;
+      ga.row_in = L.n_in;
+      ga.o_rows = (float*)(B + oGO);
+      ga.xq = Xq;
+      ga.xd = Xd;
+      KTRY(hh_gdn_rows_launch(ga, s));
+      k_out = vdim;
+    } else {
+      const int gated = hyb && c.attn_out_gate;
+      KTRY(hh_prefill_qk_launch(hd, QKV, L.n_in, c.n_heads, c.n_kv_heads, c.qk_norm ? L.q_norm : nullptr,
+                                c.qk_norm ? L.k_norm : nullptr, c.eps, m->rope, m->rope_dim, c.max_seq, pos0, S,
+                                gated, L.k_cache, L.v_cache, QB, s));
+      for (int t0 = 0; t0 < S; t0 += TA)
+        KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, c.max_seq, pos0, t0,
+                                    std::min(TA, S - t0), n_chunks, PO, PML, gated ? QKV : nullptr, L.n_in, Xq, Xd,
+                                    s));
+      k_out = nq;
+    }
+    KTRY(hh_gemm_launch(m->wfmt, L.w_out, d, k_out, Xq, Xd, S, T, s));
     KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
     KTRY(hh_norm_q8_rows_launch(H, L.ffn_norm, c.eps, d, S, Xq, Xd, s));
     KTRY(hh_gemm_launch(m->wfmt, L.w_gu, 2 * F, d, Xq, Xd, S, GU, s));
@@ -451,7 +493,6 @@ int prefill_dense(hh_model* m, const uint32_t* toks, int S, int pos0) {
     KTRY(hh_gemm_launch(m->wfmt, L.w_down, d, F, Xq, Xd, S, T, s));
     KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
   }
-  (void)wt;
   return HH_OK;
 }
 
@@ -1024,12 +1065,13 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
   st.update = 1;
   st.pen = pen;
   HIP_TRY(hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, s));
-  // prompt: dense models prefill all but the last token in one batched pass;
-  // the last prompt token runs the decode step, which yields the first
-  // generated token.  Hybrids feed the prompt token by token (qwen35.rs:1693-1700).
+  // prompt: all but the last token in one batched pass (the reference feeds
+  // hybrids token by token, qwen35.rs:1693-1700; the batched GDN pass leaves
+  // the same state); the last prompt token runs the decode step, which yields
+  // the first generated token.
   int fed = 0;
-  if (m->cfg.arch == 0 && m->cfg.kv_type == HH_F32 && m->batched_prefill && n_prompt >= 2) {
-    KTRY(prefill_dense(m, m->prompt, n_prompt - 1, start_pos));
+  if (m->cfg.kv_type == HH_F32 && m->batched_prefill && n_prompt >= 2) {
+    KTRY(prefill_batched(m, m->prompt, n_prompt - 1, start_pos));
     fed = n_prompt - 1;
     st.pos = start_pos + fed;
     st.step = fed;
@@ -1097,7 +1139,6 @@ int hh_model_time_stages(hh_model* m, int layer, int iters, double* out_ms, int 
 int hh_model_prefill(hh_model* m, const uint32_t* tokens, int n, int start_pos) {
   if (!m || !tokens) return fail(HH_ERR_INVALID, "null argument");
   if (n <= 0) return fail(HH_ERR_INVALID, "Empty prompt");
-  if (m->cfg.arch != 0) return fail(HH_ERR_INVALID, "batched prefill covers the dense architecture only");
   if (m->cfg.kv_type != HH_F32) return fail(HH_ERR_DTYPE, "batched prefill writes an f32 KV cache only");
   if (start_pos < 0 || start_pos + n > m->cfg.max_seq) return fail(HH_ERR_RANGE, "sequence exceeds max_seq");
   for (int i = 0; i < n; ++i)
@@ -1108,7 +1149,7 @@ int hh_model_prefill(hh_model* m, const uint32_t* tokens, int n, int start_pos) 
   HIP_TRY(hipMalloc(&dt, sizeof(uint32_t) * n));
   HIP_TRY(hipMemcpyAsync(dt, tokens, sizeof(uint32_t) * n, hipMemcpyHostToDevice, s));
   HIP_TRY(hipEventRecord(m->evp, s));
-  int rc = prefill_dense(m, dt, n, start_pos);
+  int rc = prefill_batched(m, dt, n, start_pos);
   HIP_TRY(hipEventRecord(m->ev2, s));
   HIP_TRY(hipStreamSynchronize(s));
   hipFree(dt);

@@ -464,7 +464,7 @@ class Model:
         return dict(zip(self.STAGES, out.tolist()))
 
     def prefill(self, tokens: Sequence[int], start_pos: int = 0) -> None:
-        """Batched prefill (dense): K/V for tokens at start_pos.., no logits."""
+        """Batched prefill: K/V (and GDN state) for tokens at start_pos.., no logits."""
         t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
         _check(self.lib.hh_model_prefill(self.h, t.ctypes.data, len(t), start_pos))
 

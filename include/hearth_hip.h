@@ -185,13 +185,16 @@ int hh_model_forward(hh_model* m, uint32_t token, int pos, float* logits_host,
 int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int start_pos, int n_gen,
                       float repeat_pen, uint32_t* out_tokens, float* last_logits_host);
 
-/* Batched prefill of a dense model (LlamaModel::forward_batch, mod.rs:899-1221):
- * runs tokens[0..n) at positions start_pos.. through every layer with the
- * int8-MFMA GEMM (hh_gemm_q8) and writes their K/V; computes no logits (the
- * reference computes only the last token's, mod.rs:1201-1218: feed that token
- * to hh_model_forward).  Each layer's arithmetic restates the decode step's, so
- * the cache equals the one token-by-token decoding leaves.  hh_model_generate
- * uses it for all prompt tokens but the last on dense models. */
+/* Batched prefill (LlamaModel::forward_batch, mod.rs:899-1221): runs
+ * tokens[0..n) at positions start_pos.. through every layer with the int8-MFMA
+ * GEMM (hh_gemm_q8) and writes their K/V; computes no logits (the reference
+ * computes only the last token's, mod.rs:1201-1218: feed that token to
+ * hh_model_forward).  On qwen35 hybrids the GDN layers run their per-token
+ * prep in parallel and the recurrence in token order; the reference has no
+ * batched hybrid path (qwen35.rs:1693-1700 feeds prompts token by token).  Each
+ * layer's arithmetic restates the decode step's, so the KV cache and recurrent
+ * state equal the ones token-by-token decoding leaves.  hh_model_generate uses
+ * it for all prompt tokens but the last.  HH_ERR_DTYPE for a Q8_0 KV cache. */
 int hh_model_prefill(hh_model* m, const uint32_t* tokens, int n, int start_pos);
 
 /* Device time (ms) of the last prefill: hh_model_prefill, or the prompt phase of

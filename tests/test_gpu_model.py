@@ -165,23 +165,29 @@ def _model_with_env(ctx, cfg, seed, env):
 
 @pytest.mark.parametrize("cfg,n_prompt", [(TINY, 9), (TINY.replace(wtype=GGML_Q1_0), 40),
                                           (CONFIGS["8b-q2"].replace(n_layers=2, max_seq=640), 300),
-                                          (TINY.replace(wtype=GGML_PTQ1_0), 33)],
-                         ids=["dense-q2", "dense-q1", "8b-2layer-300", "dense-ptq1"])
+                                          (TINY.replace(wtype=GGML_PTQ1_0), 33),
+                                          (TINY_HYB, 3), (TINY_HYB, 9), (TINY_HYB.replace(wtype=GGML_PQ2_0), 37),
+                                          (CONFIGS["9b-hybrid-q2"].replace(n_layers=4, max_seq=640), 300)],
+                         ids=["dense-q2", "dense-q1", "8b-2layer-300", "dense-ptq1", "hybrid-2", "hybrid-8",
+                              "hybrid-pq2-36", "9b-4layer-300"])
 def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
-    """forward_batch on the MFMA GEMM leaves the same KV cache as feeding the
-    prompt one token at a time: the first generated token's logits and the next
-    tokens are identical, and match the device-order oracle."""
+    """forward_batch on the MFMA GEMM leaves the same KV cache (and, on the
+    hybrids, the same conv windows and GDN states) as feeding the prompt one
+    token at a time: the first generated token's logits and the next tokens are
+    identical, and match the device-order oracle.  hybrid-2 prefills fewer
+    tokens than the conv window holds."""
     print(f"prefill {cfg.d_model} {cfg.n_layers} n={n_prompt}", flush=True)
+    pen = 1.1 if cfg.arch == 0 else 1.0
     prompt = [oracle.synth_token(11, i, cfg.vocab) for i in range(n_prompt)]
     mb = _model_with_env(ctx, cfg, 13, {"HH_BATCHED_PREFILL": "1"})
     mt = _model_with_env(ctx, cfg, 13, {"HH_BATCHED_PREFILL": "0"})
-    tb, lb = mb.generate(prompt, 8, repeat_pen=1.1, want_logits=True)
-    tt, lt = mt.generate(prompt, 8, repeat_pen=1.1, want_logits=True)
+    tb, lb = mb.generate(prompt, 8, repeat_pen=pen, want_logits=True)
+    tt, lt = mt.generate(prompt, 8, repeat_pen=pen, want_logits=True)
     assert list(tb) == list(tt)
     assert np.array_equal(lb, lt)
     if n_prompt <= 40:
         o = oracle.OracleModel(cfg, seed=13, threads=16, order=oracle.OracleModel.DEVICE)
-        tw, lw = o.generate(prompt, 8, repeat_pen=1.1, want_logits=True)
+        tw, lw = o.generate(prompt, 8, repeat_pen=pen, want_logits=True)
         assert list(tb) == list(tw)
         assert np.array_equal(lb, lw)
         o.close()
@@ -189,14 +195,15 @@ def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
     mt.close()
 
 
-def test_prefill_then_forward(ctx):
-    """hh_model_prefill(prompt[:-1]) then hh_model_forward(last token) equals
-    generate's first step."""
-    cfg = TINY
-    from hearth_amd import Model
-    prompt = [5, 77, 1023, 4000, 12, 9]
+@pytest.mark.parametrize("cfg", [TINY, TINY_HYB], ids=["dense", "hybrid"])
+def test_prefill_then_forward(ctx, cfg):
+    """hh_model_prefill(prompt[:-1]) in two calls (the second continues from the
+    first's cache, conv windows and states) then hh_model_forward(last token)
+    equals feeding every token through the decode step."""
+    prompt = [5, 77, 1023, 4000, 12, 9, 300, 2, 4001, 18, 19]
     m = _model_with_env(ctx, cfg, 4, {"HH_BATCHED_PREFILL": "1"})
-    m.prefill(prompt[:-1], 0)
+    m.prefill(prompt[:2], 0)
+    m.prefill(prompt[2:-1], 2)
     lg, am = m.forward(prompt[-1], len(prompt) - 1)
     m2 = _model_with_env(ctx, cfg, 4, {"HH_BATCHED_PREFILL": "0"})
     for p, t in enumerate(prompt[:-1]):
