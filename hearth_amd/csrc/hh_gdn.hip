@@ -247,65 +247,88 @@ __global__ __launch_bounds__(256) void k_gdn_conv_advance(GdnArgs a) {
   for (int t = 0; t < K - 1; ++t) cs[t] = nw[t];
 }
 
-// Batched prefill recurrence: workgroup h runs k_gdn_rec's per-token
-// arithmetic for tokens 0 .. S-1 in order with the head's state held in
-// registers, and writes o (before the gated norm) to o_rows[s][v_dim].  The
-// next token's inputs are loaded while the current one is computed.
-__global__ __launch_bounds__(1024) void k_gdn_rec_rows(GdnArgs a) {
+// Batched prefill recurrence.  A head's state columns evolve independently,
+// so workgroup (h, jb) owns columns 32 jb .. 32 jb + 31 of head h (4 waves,
+// one per SIMD) and runs k_gdn_rec's per-token arithmetic for tokens 0 .. S-1
+// in order, the state held in registers: lane (ic, jj) keeps rows
+// 16 ic .. 16 ic + 15 of column j, the column dots sum the 8 row-chunk
+// partials in chunk order, exactly as the decode kernel.  o (before the gated
+// norm) goes to o_rows[s][v_dim].  Inputs are staged per block of TB tokens:
+// the next block's k/q, v, g and beta are loaded into registers while the
+// current block runs, then k/q are written to the other LDS buffer.
+constexpr int REC_TB = 8;
+__global__ __launch_bounds__(256) void k_gdn_rec_rows(GdnArgs a) {
   const int tid = threadIdx.x;
-  constexpr int hd = 128;
-  const int h = blockIdx.x;
-  const int jj = tid & 31, ic = (tid >> 5) & 7, jb = tid >> 8;
+  constexpr int hd = 128, TB = REC_TB;
+  const int h = blockIdx.x >> 2, jb = blockIdx.x & 3;
+  const int jj = tid & 31, ic = tid >> 5;
   const int j = jb * 32 + jj;
   const int kg = h % a.n_k;
   const int kdim = a.n_k * hd, vdim = a.n_v * hd, S = a.S;
   float* St = a.state + (size_t)h * hd * hd;
-  __shared__ float part[2][4][8][33];
-  __shared__ float kv_s[2][hd];
+  __shared__ float part[2][8][33];
+  __shared__ float kvb[2][TB][2 * hd];   // per token: k[0..127], q[128..255]
   float sreg[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) sreg[r] = St[(size_t)(ic * 16 + r) * hd + j];
-  const float* qk0 = a.qk + (size_t)kg * hd + (tid & (hd - 1)) + (tid < hd ? kdim : 0);
-  // token 0's inputs
-  float nkq = tid < 2 * hd ? qk0[0] : 0.0f;
-  float nvj = a.vconv[(size_t)h * hd + j];
-  float ng = a.ab[h], nb = a.ab[a.n_v + h];
+  // lane tid < 128 carries k[tid], lanes 128.. carry q[tid - 128]
+  const float* kq0 = a.qk + (size_t)kg * hd + (tid & (hd - 1)) + (tid < hd ? kdim : 0);
+  const float* v0 = a.vconv + (size_t)h * hd + j;
+  float nkq[TB], nv[TB], ng[TB], nb[TB];
+  auto load_block = [&](int blk) {
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      const size_t sl = (size_t)min(blk * TB + t, S - 1);   // unconditional loads
+      nkq[t] = kq0[sl * 2 * kdim];
+      nv[t] = v0[sl * vdim];
+      ng[t] = a.ab[sl * 2 * a.n_v + h];
+      nb[t] = a.ab[sl * 2 * a.n_v + a.n_v + h];
+    }
+  };
+  load_block(0);
+  float cv[TB], cg[TB], cb[TB];
   const float inv_hd = 1.0f / sqrtf((float)hd);
-  for (int s = 0; s < S; ++s) {
-    const float kq = nkq, vj = nvj, g = ng, b = nb;
-    if (s + 1 < S) {
-      const size_t n = (size_t)(s + 1);
-      if (tid < 2 * hd) nkq = qk0[n * 2 * kdim];
-      nvj = a.vconv[n * vdim + (size_t)h * hd + j];
-      ng = a.ab[n * 2 * a.n_v + h];
-      nb = a.ab[n * 2 * a.n_v + a.n_v + h];
+  const int n_blk = (S + TB - 1) / TB;
+  for (int blk = 0; blk < n_blk; ++blk) {
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      kvb[blk & 1][t][tid] = nkq[t];
+      cv[t] = nv[t];
+      cg[t] = ng[t];
+      cb[t] = nb[t];
     }
-    // lanes 0..127 carry k, 128..255 carry q
-    if (tid < 2 * hd) kv_s[tid >> 7][tid & (hd - 1)] = kq;
-    const float decay = hx_exp(g);
+    if (blk + 1 < n_blk) load_block(blk + 1);
     __syncthreads();
-    float dp = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dp += sreg[r] * kv_s[0][ic * 16 + r];
-    part[0][jb][ic][jj] = dp;
-    __syncthreads();
-    float dot = 0.0f;
+    for (int t = 0; t < TB; ++t) {
+      const int s = blk * TB + t;
+      if (s >= S) break;   // uniform
+      const float* kk = kvb[blk & 1][t];
+      const float* qq = kk + hd;
+      float dp = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) dot += part[0][jb][c][jj];
-    const float bd = b * (vj - dot);
-    float op = 0.0f;
+      for (int r = 0; r < 16; ++r) dp += sreg[r] * kk[ic * 16 + r];
+      part[0][ic][jj] = dp;
+      const float decay = hx_exp(cg[t]);
+      __syncthreads();
+      float dot = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      sreg[r] = sreg[r] * decay + kv_s[0][ic * 16 + r] * bd;
-      op += sreg[r] * kv_s[1][ic * 16 + r];
-    }
-    part[1][jb][ic][jj] = op;
-    __syncthreads();
-    if (ic == 0) {
-      float o = 0.0f;
+      for (int c = 0; c < 8; ++c) dot += part[0][c][jj];
+      const float bd = cb[t] * (cv[t] - dot);
+      float op = 0.0f;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) o += part[1][jb][c][jj];
-      a.o_rows[(size_t)s * vdim + (size_t)h * hd + j] = o * inv_hd;
+      for (int r = 0; r < 16; ++r) {
+        sreg[r] = sreg[r] * decay + kk[ic * 16 + r] * bd;
+        op += sreg[r] * qq[ic * 16 + r];
+      }
+      part[1][ic][jj] = op;
+      __syncthreads();
+      if (ic == 0) {
+        float o = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) o += part[1][c][jj];
+        a.o_rows[(size_t)s * vdim + (size_t)h * hd + j] = o * inv_hd;
+      }
     }
   }
 #pragma unroll
@@ -367,7 +390,7 @@ int hh_gdn_rows_launch(const GdnArgs& a, hipStream_t s) {
   if (hipGetLastError() != hipSuccess) return 1;
   hipLaunchKernelGGL(k_gdn_conv_advance, dim3(n_conv_wg), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
-  hipLaunchKernelGGL(k_gdn_rec_rows, dim3(a.n_v), dim3(1024), 0, s, a);
+  hipLaunchKernelGGL(k_gdn_rec_rows, dim3(a.n_v * 4), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
   hipLaunchKernelGGL(k_gdn_gated_rows, dim3((a.n_v + 3) / 4, a.S), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;
