@@ -127,6 +127,34 @@ def kv_q8_leg(ctx, cfg, seed, kv_seed, tok0, K, W) -> dict:
             "note": "same model and prompt with a Q8_0 KV cache (an option of the reference, not its default)"}
 
 
+def hybrid_leg(ctx, n_prompt: int, K: int, W: int) -> dict:
+    """The 9B-shaped qwen35 hybrid (24 Gated-DeltaNet + 8 gated-attention
+    layers, Q2_0): batched prefill of an n_prompt-token prompt (the GDN layers'
+    recurrence in token order on the device), then greedy decode.  The
+    reference feeds hybrid prompts token by token (qwen35.rs:1693-1700)."""
+    from hearth_amd import Model, CONFIGS
+    cfg = CONFIGS["9b-hybrid-q2"]
+    cfg = cfg.replace(max_seq=max(cfg.max_seq, n_prompt + K + W + 16))
+    m = Model(ctx, cfg)
+    m.synthesize(2027)
+    prompt = [(i * 7919 + 13) % cfg.vocab for i in range(n_prompt)]
+    m.generate(prompt[:64], 2, repeat_pen=1.0)          # warm-up (scratch, code)
+    m.reset()
+    toks, _ = m.generate(prompt, W + K + 1, repeat_pen=1.0)
+    pf_ms = m.last_prefill_ms()
+    dec_ms = m.last_decode_ms() / (W + K)
+    m.close()
+    print(f"[bench] 9B hybrid: prefill {n_prompt} tokens {pf_ms:.1f} ms ({n_prompt / (pf_ms * 1e-3):.0f} tok/s), "
+          f"decode {dec_ms:.4f} ms/step ({1000.0 / dec_ms:.1f} tok/s)", file=sys.stderr, flush=True)
+    return {"model": "9B-shaped qwen35 hybrid Q2_0 (32 layers, full attention every 4th)",
+            "prefill_tokens": n_prompt, "prefill_ms": round(pf_ms, 2),
+            "prefill_tok_per_s": round(n_prompt / (pf_ms * 1e-3), 1),
+            "decode_tok_per_s": round(1000.0 / dec_ms, 2), "decode_ms_per_step": round(dec_ms, 4),
+            "first_tokens": [int(t) for t in toks[:8]],
+            "note": "prompt through the batched prefill (bit-identical to token-by-token decode), then decode "
+                    "from the prefilled state; prefill time is the prompt phase of generate"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +166,7 @@ def main():
     ap.add_argument("--no-kv-q8", action="store_true", help="skip the Q8_0 KV-cache decode leg")
     ap.add_argument("--prefill-tokens", type=int, default=2048,
                     help="batched-prefill leg after the decode measurement (0 = skip)")
+    ap.add_argument("--no-hybrid", action="store_true", help="skip the 9B hybrid prefill + decode leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs one GPU per process: bench.py measures --gpus 1 only; "
@@ -206,6 +235,8 @@ def main():
         out["kv_q8"] = kv_q8_leg(ctx, cfg, seed, kv_seed, tok0, K, W)
     if args.prefill_tokens > 0:
         out["prefill"] = prefill_leg(m, cfg, args.prefill_tokens)
+    if not args.no_hybrid:
+        out["hybrid"] = hybrid_leg(ctx, 2048, K, W)
     if not args.no_cpu:
         try:
             out["cpu_baseline"] = cpu_baseline(m, cfg, seed, kv_seed, tok0, args.cpu_budget)
