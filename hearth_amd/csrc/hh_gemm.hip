@@ -33,7 +33,10 @@ constexpr int NTG = 512;       // lanes per workgroup (8 waves, two per SIMD)
 constexpr int TM = 128;        // tokens per workgroup
 constexpr int TN = 64;         // rows per workgroup
 constexpr int KS = 128;        // columns per step
-constexpr int AROW = KS + 16;  // LDS bytes per token / weight row (16-byte aligned, staggered banks)
+// LDS bytes per token / weight row: 34 dwords (= 2 mod 32 banks), so the 16
+// rows of an MFMA operand read (8 bytes per lane) fall on distinct bank pairs;
+// rows are 8-byte aligned, so tile stores are 8 bytes wide.
+constexpr int AROW = KS + 8;
 
 // Activations arrive split: xq = int8 [seq][K], xd = f32 [seq][K/32] (the
 // Q8_0 scale of each 32-block).  Per step a lane copies two 16-byte pieces of
@@ -41,7 +44,7 @@ constexpr int AROW = KS + 16;  // LDS bytes per token / weight row (16-byte alig
 struct Stage {
   int8_t a[TM * AROW];     // activations, int8
   int8_t w[TN * AROW];     // weights widened to int8 (code - 1, or +-1)
-  float da[TM * 4];        // activation scale per (token, sub-block)
+  float da[4 * TM];        // activation scale per (sub-block, token)
   float dw[TN * 4];        // weight scale per row (Q2/Q1: [0]; Q8: per sub-block)
 };
 
@@ -128,9 +131,11 @@ HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int idx = tid + NTG * i, t = idx >> 3, piece = idx & 7;
-    *(uint4*)(st.a + t * AROW + 16 * piece) = R.a[i];
+    uint2* dst = (uint2*)(st.a + t * AROW + 16 * piece);
+    dst[0] = make_uint2(R.a[i].x, R.a[i].y);
+    dst[1] = make_uint2(R.a[i].z, R.a[i].w);
   }
-  st.da[tid] = R.ad;                                // [t][sub], t = tid / 4
+  st.da[(tid & 3) * TM + (tid >> 2)] = R.ad;        // loaded as (t = tid / 4, sub = tid % 4)
   constexpr int CU = w_code_units<FMT>();
 #pragma unroll
   for (int i = 0; i < w_regs<FMT>(); ++i) {
@@ -163,8 +168,9 @@ HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
           *(uint32_t*)(wr + 124) = trit_to_i8x4(__builtin_amdgcn_perm(t[3], t[2], 0x06040200u));
         }
       } else if constexpr (FMT == FMT_Q1) {
-        *(uint4*)(st.w + rr * AROW + 16 * u) = make_uint4(q1_spread4(v & 0xfu), q1_spread4((v >> 4) & 0xfu),
-                                                          q1_spread4((v >> 8) & 0xfu), q1_spread4((v >> 12) & 0xfu));
+        uint2* dst = (uint2*)(st.w + rr * AROW + 16 * u);
+        dst[0] = make_uint2(q1_spread4(v & 0xfu), q1_spread4((v >> 4) & 0xfu));
+        dst[1] = make_uint2(q1_spread4((v >> 8) & 0xfu), q1_spread4((v >> 12) & 0xfu));
       } else {
         *(uint16_t*)(st.w + rr * AROW + 32 * (u / 16) + 2 * (u % 16)) = (uint16_t)v;
       }
@@ -191,24 +197,26 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
 #pragma unroll
     for (int r = 0; r < 4; ++r) { sum[t][r] = 0.0f; bacc[t][r] = 0.0f; }
 
-  Regs<FMT> R;
-  stage_load<FMT>(R, w, xq, xd, n, seq, K, r0, s0, 0);
-  stage_store<FMT>(st[0], R);
+  // Two register sets: at the end of step kb, step kb + 1 (loaded two steps
+  // earlier) is written to the free LDS buffer and the global loads of step
+  // kb + 3 are issued into the register set just freed, so every load has two
+  // steps' compute to land.
+  Regs<FMT> R0, R1;
+  stage_load<FMT>(R0, w, xq, xd, n, seq, K, r0, s0, 0);
+  if (nsteps > 1) stage_load<FMT>(R1, w, xq, xd, n, seq, K, r0, s0, 1);
+  stage_store<FMT>(st[0], R0);
+  if (nsteps > 2) stage_load<FMT>(R0, w, xq, xd, n, seq, K, r0, s0, 2);
   __syncthreads();
   const int arow = 16 * wid + (lane & 15);   // A operand token (within the tile)
   const int kg = 8 * (lane >> 4);            // k offset within a sub-block
   const int tok0 = 16 * wid + 4 * (lane >> 4);
-  for (int kb = 0; kb < nsteps; ++kb) {
-    const int cur = kb & 1;
-    const bool more = kb + 1 < nsteps;
-    if (more) stage_load<FMT>(R, w, xq, xd, n, seq, K, r0, s0, kb + 1);
-    const Stage& S = st[cur];
+  auto step = [&](int kb, Regs<FMT>& Rn) {   // Rn holds step kb + 1
+    const Stage& S = st[kb & 1];
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
       const long a = *(const long*)(S.a + arow * AROW + sub * 32 + kg);
-      float da[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) da[r] = S.da[(tok0 + r) * 4 + sub];
+      const float4 da4 = *(const float4*)(S.da + sub * TM + tok0);
+      const float da[4] = {da4.x, da4.y, da4.z, da4.w};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int col = 16 * t + (lane & 15);
@@ -220,8 +228,11 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
 #pragma unroll
           for (int r = 0; r < 4; ++r) sum[t][r] += ((float)c[r] * dw) * da[r];
         } else {
+          // exact product: |c| <= 32 * 128 * 2 = 2^13 and da is an f16 value
+          // (<= 11 significant bits), so c * da fits f32's 24 bits and the
+          // fma equals bacc + (float)c * da rounded once, as the scalar order
 #pragma unroll
-          for (int r = 0; r < 4; ++r) bacc[t][r] += (float)c[r] * da[r];
+          for (int r = 0; r < 4; ++r) bacc[t][r] = fmaf((float)c[r], da[r], bacc[t][r]);
         }
       }
     }
@@ -236,8 +247,13 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
         }
       }
     }
-    if (more) stage_store<FMT>(st[cur ^ 1], R);
+    if (kb + 1 < nsteps) stage_store<FMT>(st[(kb + 1) & 1], Rn);
+    if (kb + 3 < nsteps) stage_load<FMT>(Rn, w, xq, xd, n, seq, K, r0, s0, kb + 3);
     __syncthreads();
+  };
+  for (int kb = 0; kb < nsteps; kb += 2) {
+    step(kb, R1);
+    if (kb + 1 < nsteps) step(kb + 1, R0);
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
