@@ -167,6 +167,8 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=2048,
                     help="batched-prefill leg after the decode measurement (0 = skip)")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the 9B hybrid prefill + decode leg")
+    ap.add_argument("--hybrid-only", action="store_true",
+                    help="run only the 9B hybrid leg and print its JSON (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs one GPU per process: bench.py measures --gpus 1 only; "
@@ -174,6 +176,9 @@ def main():
         sys.exit(2)
 
     from hearth_amd import Ctx, Model, CONFIGS
+    if args.hybrid_only:
+        print(json.dumps({"hybrid": hybrid_leg(Ctx(0), 2048, args.steps, args.warmup)}), flush=True)
+        return
     cfg = CONFIGS["8b-q2"]
     if args.layers:
         cfg = cfg.replace(n_layers=args.layers)
