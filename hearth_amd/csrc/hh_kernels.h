@@ -82,11 +82,12 @@ int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd,
 int hh_add_rows_launch(float* H, const float* T, int64_t n, hipStream_t s);
 int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_kv, const float* q_norm,
                          const float* k_norm, float eps, const float* rope, int rope_dim, int max_seq, int pos0, int S,
-                         int gated, float* k_cache, float* v_cache, float* QB, hipStream_t s);
+                         int gated, int kv_q8, float* k_cache, float* v_cache, float* QB, hipStream_t s);
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
                            int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
-                           const float* gate, int gate_row, int8_t* yq, float* yd, hipStream_t s);
-// gate: qwen35 gated attention's projection rows (gate_row floats apart), or null
+                           const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, hipStream_t s);
+// gate: qwen35 gated attention's projection rows (gate_row floats apart), or null;
+// kv_q8: the caches hold Q8_0 rows (quantized on write, dequantized on load)
 
 // Batched Q8_0 GEMM on int8 MFMA (prefill): out[s*n + r], K % 128 == 0, activations
 // split (int8 xq[seq][K], f32 xd[seq][K/32]); hh_q8_split_launch converts standard Q8_0 rows.

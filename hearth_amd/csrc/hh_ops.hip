@@ -594,7 +594,7 @@ __global__ void k_add_rows(float* __restrict__ H, const float* __restrict__ T, i
 // the key's per-head RMSNorm + RoPE on float4 slices of LPR lanes (the split
 // kernel's slice_norm / slice_rope), K and V written at pos0 + s, the
 // rotated q kept for the attention pass.  One LPR-lane group per head.
-template <int HD>
+template <int HD, bool KV8>
 __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QKV, int n_in, int n_heads, int n_kv,
                                                     const float* __restrict__ q_norm, const float* __restrict__ k_norm,
                                                     float eps, const float* __restrict__ rope, int rope_dim,
@@ -625,9 +625,16 @@ __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QK
     x = slice_rope(x, sn, cs, 4 * c, rope_dim);
   }
   if (is_k) {
-    const size_t off = ((size_t)kvh * max_seq + pos) * HD + 4 * c;
-    *(float4*)(k_cache + off) = x;
-    *(float4*)(v_cache + off) = *(const float4*)(row + kv0 + (size_t)n_kv * HD + (size_t)kvh * HD + 4 * c);
+    const float4 v = *(const float4*)(row + kv0 + (size_t)n_kv * HD + (size_t)kvh * HD + 4 * c);
+    if constexpr (KV8) {   // quantized on write exactly as the decode step's kv_q8_store
+      const size_t r = (size_t)kvh * max_seq + pos;
+      kv_q8_store(x, KvQ8(k_cache, n_kv, max_seq, HD), r, HD, c, true);
+      kv_q8_store(v, KvQ8(v_cache, n_kv, max_seq, HD), r, HD, c, true);
+    } else {
+      const size_t off = ((size_t)kvh * max_seq + pos) * HD + 4 * c;
+      *(float4*)(k_cache + off) = x;
+      *(float4*)(v_cache + off) = v;
+    }
   } else {
     *(float4*)(QB + (size_t)s * n_heads * HD + (size_t)qh * HD + 4 * c) = x;
   }
@@ -638,7 +645,7 @@ __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QK
 // runs the decode arithmetic (scores, chunk softmax, P.V and their reduction
 // order) once per token of the tile whose position reaches the chunk.
 // Partials: PO[((sl*n_kv + kvh)*n_chunks + c)*G + h][HD], PML likewise x2.
-template <int HD, int NTA>
+template <int HD, int NTA, bool KV8>
 __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restrict__ QB, const float* __restrict__ k_cache,
                                                             const float* __restrict__ v_cache, int n_heads, int n_kv,
                                                             int max_seq, int pos0, int S, int t0, int TT, int n_chunks,
@@ -666,8 +673,14 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
     kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     vr[i] = kr[i];
     if (j < np_max) {
-      kr[i] = *(const float4*)(kg + (size_t)(p0 + j) * HD);
-      vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
+      if constexpr (KV8) {
+        const size_t r = (size_t)kvh * max_seq + p0 + j;
+        kr[i] = KvQ8(const_cast<float*>(k_cache), n_kv, max_seq, HD).load(r, HD, cc);
+        vr[i] = KvQ8(const_cast<float*>(v_cache), n_kv, max_seq, HD).load(r, HD, cc);
+      } else {
+        kr[i] = *(const float4*)(kg + (size_t)(p0 + j) * HD);
+        vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
+      }
     }
   }
   const float inv_sqrt = 1.0f / sqrtf((float)HD);
@@ -1171,41 +1184,47 @@ int hh_add_rows_launch(float* H, const float* T, int64_t n, hipStream_t s) {
 
 int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_kv, const float* q_norm,
                          const float* k_norm, float eps, const float* rope, int rope_dim, int max_seq, int pos0, int S,
-                         int gated, float* k_cache, float* v_cache, float* QB, hipStream_t s) {
+                         int gated, int kv_q8, float* k_cache, float* v_cache, float* QB, hipStream_t s) {
   const int G = n_heads / n_kv;
-  if (hd == 128 && G + 1 <= 512 / 32)
-    hipLaunchKernelGGL(k_prefill_qk<128>, dim3(S, n_kv), dim3(512), 0, s, QKV, n_in, n_heads, n_kv, q_norm, k_norm,
-                       eps, rope, rope_dim, max_seq, pos0, gated, k_cache, v_cache, QB);
-  else if (hd == 256 && G + 1 <= 512 / 64)
-    hipLaunchKernelGGL(k_prefill_qk<256>, dim3(S, n_kv), dim3(512), 0, s, QKV, n_in, n_heads, n_kv, q_norm, k_norm,
-                       eps, rope, rope_dim, max_seq, pos0, gated, k_cache, v_cache, QB);
-  else
+  const dim3 g(S, n_kv), b(512);
+#define HH_PQK(HDV, KV)                                                                                          \
+  hipLaunchKernelGGL((k_prefill_qk<HDV, KV>), g, b, 0, s, QKV, n_in, n_heads, n_kv, q_norm, k_norm, eps, rope, \
+                     rope_dim, max_seq, pos0, gated, k_cache, v_cache, QB)
+  if (hd == 128 && G + 1 <= 512 / 32) {
+    if (kv_q8) HH_PQK(128, true); else HH_PQK(128, false);
+  } else if (hd == 256 && G + 1 <= 512 / 64) {
+    if (kv_q8) HH_PQK(256, true); else HH_PQK(256, false);
+  } else {
     return 1;
+  }
+#undef HH_PQK
   return ok();
 }
 
 // Attention for tokens [t0, t0 + n) of a prefill; PO/PML hold n tokens' partials.
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
                            int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
-                           const float* gate, int gate_row, int8_t* yq, float* yd, hipStream_t s) {
+                           const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, hipStream_t s) {
   const int G = n_heads / n_kv, TT = 16;
   if (G > 8 || n_kv * G != n_heads) return 1;
   const size_t split_lds = 4 * ((size_t)G * (8192 / hd) + 2 * G + 4 + (ATTN_NT / 64) * 4 * (size_t)hd);
   const size_t merge_lds = 4 * ((size_t)n_chunks + 256 + 4);
   dim3 g1(n_chunks, n_kv, (n + TT - 1) / TT), g2(n * n_heads, hd / 64);
+#define HH_PSPLIT(HDV, KV)                                                                                       \
+  hipLaunchKernelGGL((k_attn_prefill_split<HDV, ATTN_NT, KV>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, \
+                     v_cache, n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML)
   if (hd == 128) {
-    hipLaunchKernelGGL((k_attn_prefill_split<128, ATTN_NT>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, v_cache,
-                       n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML);
+    if (kv_q8) HH_PSPLIT(128, true); else HH_PSPLIT(128, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
                        t0, gate, gate_row, yq, yd);
   } else if (hd == 256) {
-    hipLaunchKernelGGL((k_attn_prefill_split<256, ATTN_NT>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, v_cache,
-                       n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML);
+    if (kv_q8) HH_PSPLIT(256, true); else HH_PSPLIT(256, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
                        t0, gate, gate_row, yq, yd);
   } else {
     return 1;
   }
+#undef HH_PSPLIT
   return ok();
 }
 

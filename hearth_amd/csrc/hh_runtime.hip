@@ -408,6 +408,7 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
   const int TA = 128;                              // attention tokens per pass
   const int n_chunks = m->attn_splits, G = c.n_heads / c.n_kv_heads;
   const bool hyb = c.arch == 1;
+  const int kv8 = c.kv_type == HH_Q8_0;
   const int kdim = hyb ? c.ssm_n_k_heads * c.ssm_head_dim : 0, vdim = hyb ? c.ssm_n_v_heads * c.ssm_head_dim : 0;
   int n_in_max = 0;
   for (const Layer& L : m->layers) n_in_max = std::max(n_in_max, L.n_in);
@@ -478,11 +479,11 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       const int gated = hyb && c.attn_out_gate;
       KTRY(hh_prefill_qk_launch(hd, QKV, L.n_in, c.n_heads, c.n_kv_heads, c.qk_norm ? L.q_norm : nullptr,
                                 c.qk_norm ? L.k_norm : nullptr, c.eps, m->rope, m->rope_dim, c.max_seq, pos0, S,
-                                gated, L.k_cache, L.v_cache, QB, s));
+                                gated, kv8, L.k_cache, L.v_cache, QB, s));
       for (int t0 = 0; t0 < S; t0 += TA)
         KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, c.max_seq, pos0, t0,
-                                    std::min(TA, S - t0), n_chunks, PO, PML, gated ? QKV : nullptr, L.n_in, Xq, Xd,
-                                    s));
+                                    std::min(TA, S - t0), n_chunks, PO, PML, gated ? QKV : nullptr, L.n_in, kv8,
+                                    Xq, Xd, s));
       k_out = nq;
     }
     KTRY(hh_gemm_launch(m->wfmt, L.w_out, d, k_out, Xq, Xd, S, T, s));
@@ -1070,7 +1071,7 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
   // the same state); the last prompt token runs the decode step, which yields
   // the first generated token.
   int fed = 0;
-  if (m->cfg.kv_type == HH_F32 && m->batched_prefill && n_prompt >= 2) {
+  if (m->batched_prefill && n_prompt >= 2) {
     KTRY(prefill_batched(m, m->prompt, n_prompt - 1, start_pos));
     fed = n_prompt - 1;
     st.pos = start_pos + fed;
@@ -1139,7 +1140,6 @@ int hh_model_time_stages(hh_model* m, int layer, int iters, double* out_ms, int 
 int hh_model_prefill(hh_model* m, const uint32_t* tokens, int n, int start_pos) {
   if (!m || !tokens) return fail(HH_ERR_INVALID, "null argument");
   if (n <= 0) return fail(HH_ERR_INVALID, "Empty prompt");
-  if (m->cfg.kv_type != HH_F32) return fail(HH_ERR_DTYPE, "batched prefill writes an f32 KV cache only");
   if (start_pos < 0 || start_pos + n > m->cfg.max_seq) return fail(HH_ERR_RANGE, "sequence exceeds max_seq");
   for (int i = 0; i < n; ++i)
     if (tokens[i] >= (uint32_t)m->cfg.vocab) return fail(HH_ERR_RANGE, "prompt token out of range");

@@ -194,7 +194,8 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
  * batched hybrid path (qwen35.rs:1693-1700 feeds prompts token by token).  Each
  * layer's arithmetic restates the decode step's, so the KV cache and recurrent
  * state equal the ones token-by-token decoding leaves.  hh_model_generate uses
- * it for all prompt tokens but the last.  HH_ERR_DTYPE for a Q8_0 KV cache. */
+ * it for all prompt tokens but the last.  A Q8_0 KV cache is quantized on
+ * write exactly as the decode step writes it. */
 int hh_model_prefill(hh_model* m, const uint32_t* tokens, int n, int start_pos);
 
 /* Device time (ms) of the last prefill: hh_model_prefill, or the prompt phase of

@@ -167,15 +167,18 @@ def _model_with_env(ctx, cfg, seed, env):
                                           (CONFIGS["8b-q2"].replace(n_layers=2, max_seq=640), 300),
                                           (TINY.replace(wtype=GGML_PTQ1_0), 33),
                                           (TINY_HYB, 3), (TINY_HYB, 9), (TINY_HYB.replace(wtype=GGML_PQ2_0), 37),
-                                          (CONFIGS["9b-hybrid-q2"].replace(n_layers=4, max_seq=640), 300)],
+                                          (CONFIGS["9b-hybrid-q2"].replace(n_layers=4, max_seq=640), 300),
+                                          (TINY.replace(kv_type=8), 9), (TINY_HYB.replace(kv_type=8), 9),
+                                          (CONFIGS["8b-q2"].replace(n_layers=2, max_seq=640, kv_type=8), 300)],
                          ids=["dense-q2", "dense-q1", "8b-2layer-300", "dense-ptq1", "hybrid-2", "hybrid-8",
-                              "hybrid-pq2-36", "9b-4layer-300"])
+                              "hybrid-pq2-36", "9b-4layer-300", "dense-kvq8", "hybrid-kvq8", "8b-kvq8-300"])
 def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
     """forward_batch on the MFMA GEMM leaves the same KV cache (and, on the
     hybrids, the same conv windows and GDN states) as feeding the prompt one
     token at a time: the first generated token's logits and the next tokens are
     identical, and match the device-order oracle.  hybrid-2 prefills fewer
-    tokens than the conv window holds."""
+    tokens than the conv window holds; the kvq8 cases write a Q8_0 cache
+    (quantized on write as the decode step does)."""
     print(f"prefill {cfg.d_model} {cfg.n_layers} n={n_prompt}", flush=True)
     pen = 1.1 if cfg.arch == 0 else 1.0
     prompt = [oracle.synth_token(11, i, cfg.vocab) for i in range(n_prompt)]
@@ -266,11 +269,3 @@ def test_q8_0_kv_prefilled_8b_shape(ctx, oracle):
     assert np.array_equal(lg, lw)
 
 
-def test_q8_0_kv_rejects_batched_prefill(ctx):
-    from hearth_amd import HHError, Model
-    m = Model(ctx, TINY.replace(kv_type=8))
-    m.synthesize(1)
-    with pytest.raises(HHError) as e:
-        m.prefill([1, 2, 3])
-    assert e.value.status == 2
-    m.close()
