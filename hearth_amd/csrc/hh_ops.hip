@@ -643,15 +643,15 @@ __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QK
 // Prefill attention, split pass: workgroup (chunk c, kv head, token tile)
 // holds K/V rows of chunk c in registers exactly as k_attn_split does and
 // runs the decode arithmetic (scores, chunk softmax, P.V and their reduction
-// order) once per token of the tile whose position reaches the chunk.
+// order) once per token of the tile whose position reaches the chunk, NTOK
+// tokens per pass.  GMAX bounds the query heads per kv head (registers).
 // Partials: PO[((sl*n_kv + kvh)*n_chunks + c)*G + h][HD], PML likewise x2.
-template <int HD, int NTA, bool KV8>
+template <int HD, int NTA, bool KV8, int GMAX, int NTOK>
 __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restrict__ QB, const float* __restrict__ k_cache,
                                                             const float* __restrict__ v_cache, int n_heads, int n_kv,
                                                             int max_seq, int pos0, int S, int t0, int TT, int n_chunks,
                                                             float* __restrict__ PO, float* __restrict__ PML) {
   constexpr int LPR = HD / 4, RPI = NTA / LPR, C = 8192 / HD, NR = C / RPI, NW = NTA / 64;
-  constexpr int GMAX = 8;
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = blockIdx.x, kvh = blockIdx.y, G = n_heads / n_kv;
@@ -660,9 +660,9 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
   const int np_max = min(C, pos0 + t0 + sl1 - p0);
   if (sl0 >= sl1 || np_max <= 0) return;
   const int sub = tid / LPR, cc = tid % LPR;
-  float* sc = sm;                 // G*C
-  float* ml = sc + G * C;         // 2*G (+pad)
-  float* red = ml + 2 * G + 4;    // NW waves * 4 heads * HD
+  float* sc = sm;                          // NTOK * G * C
+  float* ml = sc + NTOK * G * C;           // NTOK * 2 * G (+pad)
+  float* red = ml + NTOK * 2 * G + 4;      // NTOK * NW waves * 4 heads * HD
   const size_t hstride = (size_t)max_seq * HD;
   const float* kg = k_cache + (size_t)kvh * hstride + 4 * cc;
   const float* vg = v_cache + (size_t)kvh * hstride + 4 * cc;
@@ -686,95 +686,115 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
   const float inv_sqrt = 1.0f / sqrtf((float)HD);
   constexpr int NV = 4 * NR;
   constexpr int KSH = (LPR == 64 ? 6 : 5) - (NV == 32 ? 5 : NV == 16 ? 4 : 3);
-  for (int sl = sl0; sl < sl1; ++sl) {
-    const int s = t0 + sl, seq = pos0 + s + 1;
-    if (p0 >= seq) continue;
-    const int np = min(C, seq - p0);
-    float4 q4[GMAX];
+  // NTOK tokens per pass (each with the decode arithmetic of one token): their
+  // softmax rows spread over all waves and they share the barriers.  Tokens
+  // before the first whose position reaches the chunk skip it.
+  const int sl_first = max(sl0, p0 - pos0 - t0);
+  for (int sl = sl_first; sl < sl1; sl += NTOK) {
+    const int nt = min(NTOK, sl1 - sl);
 #pragma unroll
-    for (int h = 0; h < GMAX; ++h) {
-      q4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (h < G) q4[h] = *(const float4*)(QB + (size_t)s * n_heads * HD + (size_t)(kvh * G + h) * HD + 4 * cc);
-    }
+    for (int u = 0; u < NTOK; ++u) {
+      if (u >= nt) break;   // uniform
+      const int s = t0 + sl + u, np = min(C, pos0 + s + 1 - p0);
+      float4 q4[GMAX];
 #pragma unroll
-    for (int hg = 0; hg < GMAX; hg += 4) {
-      if (hg >= G) break;
-      float v[NV];
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        const float4 qq = q4[hg + hh];
-#pragma unroll
-        for (int i = 0; i < NR; ++i) {
-          float pp = qq.x * kr[i].x;
-          pp = fmaf(qq.y, kr[i].y, pp);
-          pp = fmaf(qq.z, kr[i].z, pp);
-          pp = fmaf(qq.w, kr[i].w, pp);
-          v[hh * NR + i] = pp;
-        }
+      for (int h = 0; h < GMAX; ++h) {
+        q4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (h < G) q4[h] = *(const float4*)(QB + (size_t)s * n_heads * HD + (size_t)(kvh * G + h) * HD + 4 * cc);
       }
-      const float r = ReduceScatter<NV, LPR / 2>::run(v, lane);
-      const int k = (lane & (LPR - 1)) >> KSH;
-      const int h = hg + k / NR, j = (k % NR) * RPI + sub;
-      if (h < G && (lane & ((1 << KSH) - 1)) == 0) sc[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
+      float* scu = sc + u * G * C;
+#pragma unroll
+      for (int hg = 0; hg < GMAX; hg += 4) {
+        if (hg >= G) break;
+        float v[NV];
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh) {
+          const float4 qq = hg + hh < GMAX ? q4[hg + hh] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+          for (int i = 0; i < NR; ++i) {
+            float pp = qq.x * kr[i].x;
+            pp = fmaf(qq.y, kr[i].y, pp);
+            pp = fmaf(qq.z, kr[i].z, pp);
+            pp = fmaf(qq.w, kr[i].w, pp);
+            v[hh * NR + i] = pp;
+          }
+        }
+        const float r = ReduceScatter<NV, LPR / 2>::run(v, lane);
+        const int k = (lane & (LPR - 1)) >> KSH;
+        const int h = hg + k / NR, j = (k % NR) * RPI + sub;
+        if (h < G && (lane & ((1 << KSH) - 1)) == 0) scu[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
+      }
     }
     __syncthreads();
-    for (int h = wid; h < G; h += NW) {
-      float x = lane < C ? sc[h * C + lane] : -INFINITY;
+    for (int pr = wid; pr < nt * G; pr += NW) {
+      const int u = pr / G, h = pr % G;
+      const int np = min(C, pos0 + t0 + sl + u + 1 - p0);
+      float* row = sc + (u * G + h) * C;
+      float x = lane < C ? row[lane] : -INFINITY;
       float m = wave_max(x);
       float e = (lane < np) ? hx_exp(x - m) : 0.0f;
       float l = wave_sum(e);
-      if (lane < C) sc[h * C + lane] = e;
-      if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
+      if (lane < C) row[lane] = e;
+      if (lane == 0) { ml[(u * G + h) * 2] = m; ml[(u * G + h) * 2 + 1] = l; }
     }
     __syncthreads();
-    const size_t pbase = ((size_t)(sl * n_kv + kvh) * n_chunks + c) * G;
     for (int hg = 0; hg < G; hg += 4) {
-      float acc[16];
 #pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-        if (hg + hh < G) {
-          const float* eh = sc + (hg + hh) * C + sub;
+      for (int u = 0; u < NTOK; ++u) {
+        if (u >= nt) break;
+        float acc[16];
 #pragma unroll
-          for (int i = 0; i < NR; ++i) {
-            const float e = eh[i * RPI];
-            o0 = fmaf(e, vr[i].x, o0);
-            o1 = fmaf(e, vr[i].y, o1);
-            o2 = fmaf(e, vr[i].z, o2);
-            o3 = fmaf(e, vr[i].w, o3);
+        for (int hh = 0; hh < 4; ++hh) {
+          float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+          if (hg + hh < G) {
+            const float* eh = sc + (u * G + hg + hh) * C + sub;
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+              const float e = eh[i * RPI];
+              o0 = fmaf(e, vr[i].x, o0);
+              o1 = fmaf(e, vr[i].y, o1);
+              o2 = fmaf(e, vr[i].z, o2);
+              o3 = fmaf(e, vr[i].w, o3);
+            }
           }
+          acc[hh * 4 + 0] = o0; acc[hh * 4 + 1] = o1; acc[hh * 4 + 2] = o2; acc[hh * 4 + 3] = o3;
         }
-        acc[hh * 4 + 0] = o0; acc[hh * 4 + 1] = o1; acc[hh * 4 + 2] = o2; acc[hh * 4 + 3] = o3;
-      }
-      if constexpr (LPR == 32) {
-        const bool up = (lane & 32) != 0;
+        float* redu = red + u * NW * 4 * HD;
+        if constexpr (LPR == 32) {
+          const bool up = (lane & 32) != 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          float send = up ? acc[k] : acc[k + 8];
-          float keep = up ? acc[k + 8] : acc[k];
-          float x = keep + __shfl_xor(send, 32, 64);
-          const int kk = k + (up ? 8 : 0);
-          red[(wid * 4 + (kk >> 2)) * HD + 4 * cc + (kk & 3)] = x;
+          for (int k = 0; k < 8; ++k) {
+            float send = up ? acc[k] : acc[k + 8];
+            float keep = up ? acc[k + 8] : acc[k];
+            float x = keep + __shfl_xor(send, 32, 64);
+            const int kk = k + (up ? 8 : 0);
+            redu[(wid * 4 + (kk >> 2)) * HD + 4 * cc + (kk & 3)] = x;
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 16; ++k) redu[(wid * 4 + (k >> 2)) * HD + 4 * cc + (k & 3)] = acc[k];
         }
-      } else {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) red[(wid * 4 + (k >> 2)) * HD + 4 * cc + (k & 3)] = acc[k];
       }
       __syncthreads();
-      for (int idx = tid; idx < 4 * HD; idx += NTA) {
-        const int h = hg + idx / HD;
+      for (int idx = tid; idx < nt * 4 * HD; idx += NTA) {
+        const int u = idx / (4 * HD), r4 = idx % (4 * HD);
+        const int h = hg + r4 / HD;
         if (h < G) {
+          const float* redu = red + u * NW * 4 * HD;
           float t[NW];
 #pragma unroll
-          for (int w = 0; w < NW; ++w) t[w] = red[w * 4 * HD + idx];
-          PO[(pbase + h) * HD + (idx % HD)] = pairwise_tree<NW>(t);
+          for (int w = 0; w < NW; ++w) t[w] = redu[w * 4 * HD + r4];
+          const size_t pbase = ((size_t)((sl + u) * n_kv + kvh) * n_chunks + c) * G;
+          PO[(pbase + h) * HD + (r4 % HD)] = pairwise_tree<NW>(t);
         }
       }
       __syncthreads();
     }
-    if (tid < G) {
-      PML[(pbase + tid) * 2] = ml[2 * tid];
-      PML[(pbase + tid) * 2 + 1] = ml[2 * tid + 1];
+    if (tid < nt * G) {
+      const int u = tid / G, h = tid % G;
+      const size_t pbase = ((size_t)((sl + u) * n_kv + kvh) * n_chunks + c) * G;
+      PML[(pbase + h) * 2] = ml[(u * G + h) * 2];
+      PML[(pbase + h) * 2 + 1] = ml[(u * G + h) * 2 + 1];
     }
   }
 }
@@ -1205,25 +1225,33 @@ int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
                            int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
                            const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, hipStream_t s) {
+  // tokens per split pass: 4 at head_dim 128, 1 at 256 (measured on the 8B and
+  // 9B/27B shapes; more tokens per pass cost occupancy at 256)
+  const int NTOK = hd == 128 ? 4 : 1;
   const int G = n_heads / n_kv, TT = 16;
   if (G > 8 || n_kv * G != n_heads) return 1;
-  const size_t split_lds = 4 * ((size_t)G * (8192 / hd) + 2 * G + 4 + (ATTN_NT / 64) * 4 * (size_t)hd);
+  const size_t split_lds =
+      4 * (NTOK * ((size_t)G * (8192 / hd) + 2 * G + (ATTN_NT / 64) * 4 * (size_t)hd) + 4);
   const size_t merge_lds = 4 * ((size_t)n_chunks + 256 + 4);
   dim3 g1(n_chunks, n_kv, (n + TT - 1) / TT), g2(n * n_heads, hd / 64);
-#define HH_PSPLIT(HDV, KV)                                                                                       \
-  hipLaunchKernelGGL((k_attn_prefill_split<HDV, ATTN_NT, KV>), g1, dim3(ATTN_NT), split_lds, s, QB, k_cache, \
-                     v_cache, n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, PML)
+#define HH_PSPLIT(HDV, KV, GM)                                                                              \
+  hipLaunchKernelGGL((k_attn_prefill_split<HDV, ATTN_NT, KV, GM, HDV == 128 ? 4 : 1>), g1, dim3(ATTN_NT),      \
+                     split_lds, s, QB, k_cache, v_cache, n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, \
+                     PML)
+#define HH_PSPLIT_G(HDV, KV) \
+  do { if (G <= 4) HH_PSPLIT(HDV, KV, 4); else HH_PSPLIT(HDV, KV, 8); } while (0)
   if (hd == 128) {
-    if (kv_q8) HH_PSPLIT(128, true); else HH_PSPLIT(128, false);
+    if (kv_q8) HH_PSPLIT_G(128, true); else HH_PSPLIT_G(128, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
                        t0, gate, gate_row, yq, yd);
   } else if (hd == 256) {
-    if (kv_q8) HH_PSPLIT(256, true); else HH_PSPLIT(256, false);
+    if (kv_q8) HH_PSPLIT_G(256, true); else HH_PSPLIT_G(256, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
                        t0, gate, gate_row, yq, yd);
   } else {
     return 1;
   }
+#undef HH_PSPLIT_G
 #undef HH_PSPLIT
   return ok();
 }
