@@ -145,8 +145,8 @@ typedef struct {
                              through the dequantized rows as attention_q8_0, ops.rs:946-1030) */
 } hh_model_config;
 
-/* Allocates every weight (native GGUF block layout, uploaded once), the f32 KV
- * cache ([layer][kv_head][max_seq][hd], kvcache.rs:11-39), the recurrent state
+/* Allocates every weight (native GGUF block layout, uploaded once), the KV
+ * cache (f32 or Q8_0 rows, [layer][kv_head][max_seq][hd], kvcache.rs:11-57), the recurrent state
  * and the step buffers.  Replaces LlamaModel::load's GPU branch (mod.rs:238-282,
  * model/gpu.rs:8-50). */
 int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out);
