@@ -248,30 +248,48 @@ __global__ __launch_bounds__(256) void k_gdn_conv_advance(GdnArgs a) {
 }
 
 // Batched prefill recurrence.  A head's state columns evolve independently,
-// so workgroup (h, jb) owns columns 32 jb .. 32 jb + 31 of head h (4 waves,
-// one per SIMD) and runs k_gdn_rec's per-token arithmetic for tokens 0 .. S-1
-// in order, the state held in registers: lane (ic, jj) keeps rows
-// 16 ic .. 16 ic + 15 of column j, the column dots sum the 8 row-chunk
-// partials in chunk order, exactly as the decode kernel.  o (before the gated
-// norm) goes to o_rows[s][v_dim].  Inputs are staged per block of TB tokens:
-// the next block's k/q, v, g and beta are loaded into registers while the
-// current block runs, then k/q are written to the other LDS buffer.
+// so workgroup (h, jb) owns columns 32 jb .. 32 jb + 31 of head h, 8 per wave,
+// and runs k_gdn_rec's per-token arithmetic for tokens 0 .. S-1 in order with
+// the state in registers: lane (column jj, row chunk ic) of a wave keeps rows
+// 16 ic .. 16 ic + 15 of column j, its column's 8 chunks in 8 adjacent lanes.
+// The column dots add the 8 chunk partials in chunk order, exactly as the
+// decode kernel does through LDS, here with in-row lane shifts (no barrier per
+// token).  o (before the gated norm) goes to o_rows[s][v_dim].  Inputs are
+// staged per block of TB tokens: the next block's k/q, v, g and beta are
+// loaded into registers while the current block runs.
 constexpr int REC_TB = 8;
+template <int K> HH_DEV float from_lane_plus(float v) {   // lane i <- lane i + K (same 16-lane row)
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 | K, 0xF, 0xF, false));
+}
+HH_DEV float sum8_in_order(float p) {   // lanes 8g: ((((0 + p0) + p1) + ...) + p7) of lanes 8g .. 8g+7
+  float s = 0.0f;
+  s += p;
+  s += from_lane_plus<1>(p);
+  s += from_lane_plus<2>(p);
+  s += from_lane_plus<3>(p);
+  s += from_lane_plus<4>(p);
+  s += from_lane_plus<5>(p);
+  s += from_lane_plus<6>(p);
+  s += from_lane_plus<7>(p);
+  return s;
+}
+HH_DEV float from_group_base8(float v) {   // every lane <- lane (lane & ~7)
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x0018));
+}
 __global__ __launch_bounds__(256) void k_gdn_rec_rows(GdnArgs a) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   constexpr int hd = 128, TB = REC_TB;
   const int h = blockIdx.x >> 2, jb = blockIdx.x & 3;
-  const int jj = tid & 31, ic = tid >> 5;
-  const int j = jb * 32 + jj;
+  const int ic = lane & 7, jj = lane >> 3;
+  const int j = jb * 32 + wid * 8 + jj;
   const int kg = h % a.n_k;
   const int kdim = a.n_k * hd, vdim = a.n_v * hd, S = a.S;
   float* St = a.state + (size_t)h * hd * hd;
-  __shared__ float part[2][8][33];
   __shared__ float kvb[2][TB][2 * hd];   // per token: k[0..127], q[128..255]
   float sreg[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) sreg[r] = St[(size_t)(ic * 16 + r) * hd + j];
-  // lane tid < 128 carries k[tid], lanes 128.. carry q[tid - 128]
+  // staging lane tid < 128 carries k[tid], lanes 128.. carry q[tid - 128]
   const float* kq0 = a.qk + (size_t)kg * hd + (tid & (hd - 1)) + (tid < hd ? kdim : 0);
   const float* v0 = a.vconv + (size_t)h * hd + j;
   float nkq[TB], nv[TB], ng[TB], nb[TB];
@@ -298,37 +316,35 @@ __global__ __launch_bounds__(256) void k_gdn_rec_rows(GdnArgs a) {
       cb[t] = nb[t];
     }
     if (blk + 1 < n_blk) load_block(blk + 1);
-    __syncthreads();
+    __syncthreads();   // the other buffer was last read a whole block ago
+    // the block's outputs are stored after its tokens, so token t's output
+    // chain can overlap token t + 1's dot chain
+    const int nt = min(TB, S - blk * TB);
+    float ob[TB], dec[TB];
+#pragma unroll
+    for (int t = 0; t < TB; ++t) dec[t] = hx_exp(cg[t]);
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
-      const int s = blk * TB + t;
-      if (s >= S) break;   // uniform
-      const float* kk = kvb[blk & 1][t];
+      if (t >= nt) break;   // uniform
+      const float* kk = kvb[blk & 1][t] + ic * 16;
       const float* qq = kk + hd;
       float dp = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp += sreg[r] * kk[ic * 16 + r];
-      part[0][ic][jj] = dp;
-      const float decay = hx_exp(cg[t]);
-      __syncthreads();
-      float dot = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) dot += part[0][c][jj];
+      for (int r = 0; r < 16; ++r) dp += sreg[r] * kk[r];
+      const float dot = from_group_base8(sum8_in_order(dp));
       const float bd = cb[t] * (cv[t] - dot);
       float op = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        sreg[r] = sreg[r] * decay + kk[ic * 16 + r] * bd;
-        op += sreg[r] * qq[ic * 16 + r];
+        sreg[r] = sreg[r] * dec[t] + kk[r] * bd;
+        op += sreg[r] * qq[r];
       }
-      part[1][ic][jj] = op;
-      __syncthreads();
-      if (ic == 0) {
-        float o = 0.0f;
+      ob[t] = sum8_in_order(op);
+    }
+    if (ic == 0) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) o += part[1][c][jj];
-        a.o_rows[(size_t)s * vdim + (size_t)h * hd + j] = o * inv_hd;
-      }
+      for (int t = 0; t < TB; ++t)
+        if (t < nt) a.o_rows[(size_t)(blk * TB + t) * vdim + (size_t)h * hd + j] = ob[t] * inv_hd;
     }
   }
 #pragma unroll
