@@ -94,6 +94,27 @@ def test_8b_shaped_prefilled_kv(ctx, oracle):
     assert np.array_equal(lg, lw)
 
 
+@pytest.mark.parametrize("cfg,kv_type", [(CONFIGS["8b-q2"].replace(n_layers=1, max_seq=8192), 0),
+                                         (CONFIGS["8b-q2"].replace(n_layers=1, max_seq=8192), 8),
+                                         (CONFIGS["9b-hybrid-q2"].replace(n_layers=4, max_seq=8192), 0)],
+                         ids=["8b-f32", "8b-kvq8", "9b-hybrid"])
+def test_long_context_decode(ctx, oracle, cfg, kv_type):
+    """Decode at 7936 prefilled positions: 124 attention chunks per kv head at
+    head_dim 128 (248 at 256), so the merge walks more partials than a wave
+    has lanes.  Logits and tokens equal the device-order oracle."""
+    cfg = cfg.replace(kv_type=kv_type)
+    m, o = make(ctx, oracle, cfg, seed=4)
+    m.prefill_kv_synthetic(41, 7936)
+    o.prefill_kv_synthetic(41, 7936)
+    tok0 = oracle.synth_token(4, 0, cfg.vocab)
+    pen = 1.1 if cfg.arch == 0 else 1.0
+    toks, lg = m.generate([tok0], 8, start_pos=7936, repeat_pen=pen, want_logits=True)
+    tw, lw = o.generate([tok0], 8, start_pos=7936, repeat_pen=pen, want_logits=True)
+    assert list(toks) == list(tw)
+    assert np.array_equal(lg, lw)
+    o.close()
+
+
 @pytest.mark.parametrize("cfg", [TINY, TINY_HYB], ids=["dense", "hybrid"])
 def test_reference_order_spread(ctx, oracle, cfg):
     """Against the reference-order oracle: first-step logits within 5e-2.  The
