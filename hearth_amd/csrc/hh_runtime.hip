@@ -401,12 +401,18 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
 // tile; GDN layers run the per-token prep in parallel and the recurrence in
 // token order per v-head (the state stays in registers).  The result is the
 // state that feeding the tokens one at a time leaves, bit for bit.
+#ifndef PF_ATTN_BYTES
+#define PF_ATTN_BYTES ((size_t)2 << 30)
+#endif
 int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
   const hh_model_config& c = m->cfg;
   hipStream_t s = m->ctx->stream;
   const int d = c.d_model, hd = c.head_dim, nq = c.n_heads * hd, F = c.d_ffn;
-  const int TA = 128;                              // attention tokens per pass
   const int n_chunks = m->attn_splits, G = c.n_heads / c.n_kv_heads;
+  // attention tokens per pass: as many as keep the split partials within
+  // PF_ATTN_BYTES (all of them up to a few thousand tokens), in 16-token tiles
+  const size_t part_per_tok = (size_t)c.n_kv_heads * n_chunks * G * (hd + 2) * 4;
+  const int TA = std::max(16, std::min((S + 15) / 16 * 16, (int)(PF_ATTN_BYTES / part_per_tok) / 16 * 16));
   const bool hyb = c.arch == 1;
   const int kv8 = c.kv_type == HH_Q8_0;
   const int kdim = hyb ? c.ssm_n_k_heads * c.ssm_head_dim : 0, vdim = hyb ? c.ssm_n_v_heads * c.ssm_head_dim : 0;
