@@ -261,3 +261,45 @@ def test_gemm_errors(ctx):
     with pytest.raises(HHError) as e:
         ctx.gemm_q8(2, w, 4, 128, w, 2, y)
     assert e.value.status == 2
+
+
+def _random_weights(t, n_rows, n_cols, rng):
+    """Arbitrary code bytes with finite f16 block scales of random magnitude."""
+    be, bb = {8: (32, 34), 41: (128, 18), 42: (128, 34), 43: (128, 18), 142: (128, 34), 143: (128, 28)}[t]
+    nb = n_rows * n_cols // be
+    w = rng.integers(0, 256, nb * bb, dtype=np.uint8)
+    off = 26 if t == 143 else 0
+    sc = (rng.uniform(-2, 2, nb) * 10.0 ** rng.integers(-3, 2, nb)).astype(np.float16).view(np.uint16)
+    blocks = w.reshape(nb, bb)
+    blocks[:, off] = sc & 0xFF
+    blocks[:, off + 1] = sc >> 8
+    return w
+
+
+from hypothesis import given, settings, strategies as hst   # noqa: E402
+
+
+@settings(max_examples=25, deadline=None)
+@given(hst.sampled_from([8, 41, 42, 43, 142, 143]), hst.integers(1, 300), hst.integers(1, 16),
+       hst.integers(1, 40), hst.integers(0, 2 ** 31))
+def test_gemv_and_gemm_random_bytes(ctx, oracle, t, n_rows, kb, seq, seed):
+    """Hypothesis-drawn format, shape and bytes (arbitrary codes, random-magnitude
+    scales, activations spanning several decades): the decode GEMV and the
+    prefill GEMM equal the scalar DotFn bit for bit."""
+    n_cols = kb * 256
+    print(f"random t={t} rows={n_rows} cols={n_cols} seq={seq} seed={seed}", flush=True)
+    rng = np.random.default_rng(seed)
+    w = _random_weights(t, n_rows, n_cols, rng)
+    x = (rng.standard_normal(seq * n_cols) * 10.0 ** rng.uniform(-2, 2)).astype(np.float32)
+    xq = np.concatenate([oracle.quantize_q8_0(x[s * n_cols:(s + 1) * n_cols]) for s in range(seq)])
+    qs = n_cols // 32 * 34
+    want = [oracle.gemv(t, w, n_rows, n_cols, xq[s * qs:(s + 1) * qs]) for s in range(seq)]
+    y = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
+    ctx.gemv_q8(t, dev(w), n_rows, n_cols, dev(xq[:qs]), y)
+    assert np.array_equal(host(y), want[0])
+    if n_cols % 128 == 0:
+        out = torch.zeros(seq * n_rows, dtype=torch.float32, device="cuda")
+        ctx.gemm_q8(t, dev(w), n_rows, n_cols, dev(xq), seq, out)
+        got = host(out).reshape(seq, n_rows)
+        for s in range(seq):
+            assert np.array_equal(got[s], want[s]), s
