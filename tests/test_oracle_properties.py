@@ -19,7 +19,7 @@ from hypothesis import given, settings, strategies as st
 GGML_Q8_0, GGML_Q1_0, GGML_Q2_0, GGML_Q1_0_G128, GGML_PQ2_0, GGML_PTQ1_0 = 8, 41, 42, 43, 142, 143
 BLOCK = {GGML_Q1_0: (128, 18), GGML_Q1_0_G128: (128, 18), GGML_Q2_0: (128, 34), GGML_PQ2_0: (128, 34),
          GGML_PTQ1_0: (128, 28)}
-SETTINGS = settings(max_examples=40, deadline=None)
+SETTINGS = settings(max_examples=40, deadline=None, derandomize=True)   # deterministic suite
 
 
 def _f16(b0, b1):
@@ -71,7 +71,7 @@ floats = st.floats(min_value=-1e4, max_value=1e4, allow_nan=False, allow_infinit
 
 
 @SETTINGS
-@given(st.lists(floats, min_size=32, max_size=32 * 8).filter(lambda v: len(v) % 32 == 0))
+@given(st.integers(min_value=1, max_value=8).flatmap(lambda nb: st.lists(floats, min_size=32 * nb, max_size=32 * nb)))
 def test_q8_0_bounds_and_idempotence(oracle, vals):
     x = np.array(vals, np.float32)
     q = oracle.quantize_q8_0(x)
