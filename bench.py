@@ -127,6 +127,54 @@ def kv_q8_leg(ctx, cfg, seed, kv_seed, tok0, K, W) -> dict:
             "note": "same model and prompt with a Q8_0 KV cache (an option of the reference, not its default)"}
 
 
+def _generate_leg(ctx, name: str, cfg, seed: int, n_prompt: int, n_gen: int, pen: float) -> dict:
+    """Seeded prompt through generate (batched prefill of all prompt tokens but
+    the last, then the decode graph); prefill and decode timed separately on
+    the device."""
+    from hearth_amd import Model
+    m = Model(ctx, cfg)
+    m.synthesize(seed)
+    rng = np.random.default_rng(seed)
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab, n_prompt)]
+    m.generate(prompt[:16], 2, repeat_pen=pen)          # warm-up (scratch, code)
+    m.reset()
+    toks, _ = m.generate(prompt, n_gen, repeat_pen=pen)
+    pf_ms = m.last_prefill_ms()
+    dec_ms = m.last_decode_ms() / max(1, n_gen - 1)
+    m.close()
+    print(f"[bench] {name}: prompt {n_prompt} tokens {pf_ms:.1f} ms ({n_prompt / (pf_ms * 1e-3):.0f} tok/s), "
+          f"decode {dec_ms:.4f} ms/step ({1000.0 / dec_ms:.1f} tok/s)", file=sys.stderr, flush=True)
+    return {"prompt_tokens": n_prompt, "prompt_ms": round(pf_ms, 2),
+            "prompt_tok_per_s": round(n_prompt / (pf_ms * 1e-3), 1), "decode_steps": n_gen - 1,
+            "decode_tok_per_s": round(1000.0 / dec_ms, 2), "decode_ms_per_step": round(dec_ms, 4),
+            "first_tokens": [int(t) for t in toks[:8]]}
+
+
+def config_legs(ctx) -> dict:
+    """BASELINE configs[0], [1], [3], [4] on the device (seeded synthetic weights).
+    The prompt phase includes the last prompt token's decode step."""
+    from hearth_amd import CONFIGS, microbench
+    out = {}
+    c0 = CONFIGS["1.7b-q1"]
+    out["cfg0_1.7b_q1"] = _generate_leg(ctx, "1.7B Q1_0", c0.replace(max_seq=max(c0.max_seq, 128)), 2025, 16,
+                                        50, 1.1)
+    out["cfg0_1.7b_q1"]["workload"] = "1.7B-shaped Q1_0 dense, 16-token prompt, 50 greedy tokens"
+    g = microbench.run(reps=1000, formats=("Q1_0", "Q2_0"), shapes=microbench.SHAPES[:3])
+    out["cfg1_gemv"] = [{k: r[k] for k in ("format", "n", "k", "us", "GB/s", "frac_peak")} for r in g]
+    for r in g:
+        print(f"[bench] GEMV {r['format']} {r['n']}x{r['k']}: {r['us']} us {r['GB/s']} GB/s", file=sys.stderr,
+              flush=True)
+    c3 = CONFIGS["9b-hybrid-q2"]
+    out["cfg3_9b_hybrid"] = _generate_leg(ctx, "9B hybrid Q2_0", c3.replace(max_seq=max(c3.max_seq, 1024)), 2027,
+                                          512, 129, 1.0)
+    out["cfg3_9b_hybrid"]["workload"] = "9B-shaped qwen35 hybrid Q2_0, 512-token prompt, 128 greedy decode steps"
+    c4 = CONFIGS["27b-hybrid-pq2"].replace(max_seq=8192)
+    out["cfg4_27b_hybrid"] = _generate_leg(ctx, "27B hybrid PQ2_0", c4, 2028, 2048, 65, 1.0)
+    out["cfg4_27b_hybrid"]["workload"] = ("27B-shaped qwen35 hybrid PQ2_0, 2048-token batched prefill, 64 greedy "
+                                         "decode steps, 8192 context")
+    return out
+
+
 def hybrid_leg(ctx, n_prompt: int, K: int, W: int) -> dict:
     """The 9B-shaped qwen35 hybrid (24 Gated-DeltaNet + 8 gated-attention
     layers, Q2_0): batched prefill of an n_prompt-token prompt (the GDN layers'
@@ -167,6 +215,8 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=2048,
                     help="batched-prefill leg after the decode measurement (0 = skip)")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the 9B hybrid prefill + decode leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the BASELINE configs[0,1,3,4] legs (1.7B Q1_0, GEMV microbench, 9B and 27B hybrids)")
     ap.add_argument("--hybrid-only", action="store_true",
                     help="run only the 9B hybrid leg and print its JSON (profiling)")
     args = ap.parse_args()
@@ -175,6 +225,11 @@ def main():
                                    "see DESIGN.md for how the decode path would shard"}))
         sys.exit(2)
 
+    if not args.no_configs:
+        # the GEMV microbench leg allocates through torch, whose bundled HIP
+        # runtime must initialize before the library's (system ROCm) one
+        import torch
+        torch.cuda.init()
     from hearth_amd import Ctx, Model, CONFIGS
     if args.hybrid_only:
         print(json.dumps({"hybrid": hybrid_leg(Ctx(0), 2048, args.steps, args.warmup)}), flush=True)
@@ -242,6 +297,8 @@ def main():
         out["prefill"] = prefill_leg(m, cfg, args.prefill_tokens)
     if not args.no_hybrid:
         out["hybrid"] = hybrid_leg(ctx, 2048, K, W)
+    if not args.no_configs:
+        out["configs"] = config_legs(ctx)
     if not args.no_cpu:
         try:
             out["cpu_baseline"] = cpu_baseline(m, cfg, seed, kv_seed, tok0, args.cpu_budget)

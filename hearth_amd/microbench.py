@@ -21,14 +21,16 @@ SHAPES = [(6144, 2048), (2048, 6144), (151936, 2048), (24576, 4096), (4096, 1228
 PEAK_GBS = 8000.0
 
 
-def run(reps: int = 1000, ring_bytes: int = 600 << 20, seed: int = 1):
+def run(reps: int = 1000, ring_bytes: int = 600 << 20, seed: int = 1, formats=None, shapes=None):
     import torch
     from hearth_amd import Ctx, GGML_Q1_0, GGML_Q2_0, GGML_PTQ1_0, row_bytes
     ctx = Ctx(0)
     out = []
     rng = np.random.default_rng(seed)
     for t, tname in ((GGML_Q1_0, "Q1_0"), (GGML_Q2_0, "Q2_0"), (GGML_PTQ1_0, "PTQ1_0")):
-        for n, k in SHAPES:
+        if formats is not None and tname not in formats:
+            continue
+        for n, k in (shapes or SHAPES):
             wb = n * row_bytes(t, k)
             copies = max(2, -(-ring_bytes // wb))
             ring = torch.randint(0, 256, (copies, wb), dtype=torch.uint8, device="cuda")
