@@ -408,7 +408,14 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
   const hh_model_config& c = m->cfg;
   hipStream_t s = m->ctx->stream;
   const int d = c.d_model, hd = c.head_dim, nq = c.n_heads * hd, F = c.d_ffn;
-  const int n_chunks = m->attn_splits, G = c.n_heads / c.n_kv_heads;
+  // the chunks the prompt reaches (the partials' chunk stride, shared by the
+  // split and merge passes), not every chunk of the cache
+  // (rounded up to 3 mod 8: the split grid's workgroup ids x + n_chunks * y
+  // then put each kv head's chunk x on a different XCD of the round-robin
+  // dispatch; measured against the neighbouring strides)
+  int n_chunks = (pos0 + S + m->attn_chunk - 1) / m->attn_chunk;
+  n_chunks += (3 - n_chunks % 8 + 8) % 8;
+  const int G = c.n_heads / c.n_kv_heads;
   // attention tokens per pass: as many as keep the split partials within
   // PF_ATTN_BYTES (all of them up to a few thousand tokens), in 16-token tiles
   const size_t part_per_tok = (size_t)c.n_kv_heads * n_chunks * G * (hd + 2) * 4;
