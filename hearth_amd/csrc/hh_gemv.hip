@@ -782,20 +782,24 @@ __global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
   int* bis = (int*)(bvs + 16);
 
   const int gw = blockIdx.x * (NT / 64) + wv, W = gridDim.x * (NT / 64);
-  auto load_row = [&](uint32_t (&wr)[U][DW], int r) {
+  // a row's repetition count is loaded with its weights (every lane, one
+  // address): loaded later, its wait would also wait for the next row's units
+  const int* cnt_src = p.counts ? p.counts : (const int*)p.w;
+  auto load_row = [&](uint32_t (&wr)[U][DW], int& cnt, int r) {
     r = min(r, n - 1);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = min(lane + 64 * u, P - 1);
       load_unit<FMT>(wr[u], p.w + ((size_t)r * P + t) * UB);
     }
+    cnt = cnt_src[p.counts ? r : 0];
   };
   const int rule = p.rule;
   const float pen = st->pen;
   const bool do_pen = rule == 0 && !(fabsf(pen - 1.0f) < 1e-6f);
   float bv = -INFINITY;
   int bi = (rule == 0) ? -1 : 0x7fffffff;
-  auto row = [&](const uint32_t (&wr)[U][DW], int r) {
+  auto row = [&](const uint32_t (&wr)[U][DW], int cnt, int r) {
     float q = 0.0f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -811,8 +815,7 @@ __global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
     if (lane == 0) {
       if (p.y) p.y[r] = v;
       if (do_pen) {
-        const int c = p.counts[r];
-        for (int k = 0; k < c; ++k) v = (v > 0.0f) ? v / pen : v * pen;   // lib.rs:26-40
+        for (int k = 0; k < cnt; ++k) v = (v > 0.0f) ? v / pen : v * pen;   // lib.rs:26-40
       }
       bool better = (rule == 0) ? (v > bv || (v == bv && r > bi)) : (v > bv || (v == bv && r < bi));
       if (v != v) better = false;
@@ -823,14 +826,15 @@ __global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
   ActStage<FMT, PRO_RMSNORM> act;
   act.issue(p);
   uint32_t wa[U][DW], wb[U][DW];
-  load_row(wa, gw);
+  int ca, cb;
+  load_row(wa, ca, gw);
   act.store(p, aq, ds, red);
   __syncthreads();
   for (int r = gw; r < n; r += 2 * W) {
-    load_row(wb, r + W);
-    row(wa, r);
-    load_row(wa, r + 2 * W);
-    if (r + W < n) row(wb, r + W);
+    load_row(wb, cb, r + W);
+    row(wa, ca, r);
+    load_row(wa, ca, r + 2 * W);
+    if (r + W < n) row(wb, cb, r + W);
   }
   if (lane == 0) { bvs[wv] = bv; bis[wv] = bi; }
   __syncthreads();
