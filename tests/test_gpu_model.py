@@ -13,7 +13,7 @@ do to each other."""
 import numpy as np
 import pytest
 
-from hearth_amd.lib import ModelConfig, GGML_Q1_0, GGML_Q2_0, GGML_PQ2_0, GGML_PTQ1_0, CONFIGS
+from hearth_amd.lib import ModelConfig, GGML_Q1_0, GGML_Q2_0, GGML_Q1_0_G128, GGML_PQ2_0, GGML_PTQ1_0, CONFIGS
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -52,8 +52,9 @@ def test_synthesized_bytes_bit_exact(ctx, oracle, cfg):
         assert np.array_equal(got, want), n
 
 
-@pytest.mark.parametrize("cfg", [TINY, TINY.replace(wtype=GGML_Q1_0), TINY_HYB, TINY.replace(wtype=GGML_PTQ1_0)],
-                         ids=["dense-q2", "dense-q1", "hybrid-q2", "dense-ptq1"])
+@pytest.mark.parametrize("cfg", [TINY, TINY.replace(wtype=GGML_Q1_0), TINY_HYB, TINY.replace(wtype=GGML_PTQ1_0),
+                                 TINY.replace(wtype=GGML_Q1_0_G128), TINY_HYB.replace(wtype=GGML_Q1_0)],
+                         ids=["dense-q2", "dense-q1", "hybrid-q2", "dense-ptq1", "dense-q1g128", "hybrid-q1"])
 def test_forward_logits_parity(ctx, oracle, cfg):
     m, o = make(ctx, oracle, cfg, seed=5)
     for pos, tok in enumerate([17, 400, 9, 4095, 0, 1234]):
