@@ -281,7 +281,7 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   const int sub = tid / LPR, c = tid % LPR;
   float* sc = sm;                 // G*C
   float* ml = sc + G * C;         // 2*G (+pad)
-  float* red = ml + 2 * G + 4;    // NW waves * 4 heads * HD
+  float* red = ml + ((2 * G + 4 + 3) & ~3);   // NW waves * 4 heads * HD (16-byte aligned)
   const size_t hstride = (size_t)a.max_seq * HD;
   const float* kg = a.k_cache + (size_t)kvh * hstride + 4 * c;
   const float* vg = a.v_cache + (size_t)kvh * hstride + 4 * c;
@@ -419,17 +419,24 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
     if constexpr (LPR == 32) {
       // the two row groups of this wave: lanes < 32 keep heads 0-1, others 2-3
       const bool up = (lane & 32) != 0;
+      float xs[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         float send = up ? acc[k] : acc[k + 8];
         float keep = up ? acc[k + 8] : acc[k];
-        float x = keep + __shfl_xor(send, 32, 64);
-        const int kk = k + (up ? 8 : 0);
-        red[(wid * 4 + (kk >> 2)) * HD + 4 * c + (kk & 3)] = x;
+        xs[k] = keep + __shfl_xor(send, 32, 64);
       }
+      // values kk = k (+ 8 on the upper half) go to row wid*4 + kk/4, column
+      // 4c + kk%4: two 16-byte writes per lane (scalar writes at a 4-dword
+      // lane stride would conflict 4 ways)
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+        *(float4*)(red + (wid * 4 + g + (up ? 2 : 0)) * HD + 4 * c) =
+            make_float4(xs[4 * g], xs[4 * g + 1], xs[4 * g + 2], xs[4 * g + 3]);
     } else {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) red[(wid * 4 + (k >> 2)) * HD + 4 * c + (k & 3)] = acc[k];
+      for (int g = 0; g < 4; ++g)
+        *(float4*)(red + (wid * 4 + g) * HD + 4 * c) = make_float4(acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]);
     }
     __syncthreads();
     for (int idx = tid; idx < 4 * HD; idx += NTA) {
@@ -662,7 +669,7 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
   const int sub = tid / LPR, cc = tid % LPR;
   float* sc = sm;                          // NTOK * G * C
   float* ml = sc + NTOK * G * C;           // NTOK * 2 * G (+pad)
-  float* red = ml + NTOK * 2 * G + 4;      // NTOK * NW waves * 4 heads * HD
+  float* red = ml + ((NTOK * 2 * G + 4 + 3) & ~3);   // NTOK * NW waves * 4 heads * HD (16-byte aligned)
   const size_t hstride = (size_t)max_seq * HD;
   const float* kg = k_cache + (size_t)kvh * hstride + 4 * cc;
   const float* vg = v_cache + (size_t)kvh * hstride + 4 * cc;
@@ -762,17 +769,22 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
         float* redu = red + u * NW * 4 * HD;
         if constexpr (LPR == 32) {
           const bool up = (lane & 32) != 0;
+          float xs[8];
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
             float send = up ? acc[k] : acc[k + 8];
             float keep = up ? acc[k + 8] : acc[k];
-            float x = keep + __shfl_xor(send, 32, 64);
-            const int kk = k + (up ? 8 : 0);
-            redu[(wid * 4 + (kk >> 2)) * HD + 4 * cc + (kk & 3)] = x;
+            xs[k] = keep + __shfl_xor(send, 32, 64);
           }
+#pragma unroll
+          for (int g = 0; g < 2; ++g)   // two 16-byte writes per lane, as the decode split
+            *(float4*)(redu + (wid * 4 + g + (up ? 2 : 0)) * HD + 4 * cc) =
+                make_float4(xs[4 * g], xs[4 * g + 1], xs[4 * g + 2], xs[4 * g + 3]);
         } else {
 #pragma unroll
-          for (int k = 0; k < 16; ++k) redu[(wid * 4 + (k >> 2)) * HD + 4 * cc + (k & 3)] = acc[k];
+          for (int g = 0; g < 4; ++g)
+            *(float4*)(redu + (wid * 4 + g) * HD + 4 * cc) =
+                make_float4(acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]);
         }
       }
       __syncthreads();
@@ -1108,7 +1120,7 @@ int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
   const int G = a.n_heads / a.n_kv;
   if (a.hd != 128 && a.hd != 256) return 1;
   if (a.chunk != 8192 / a.hd || a.n_kv * G != a.n_heads || G > 8) return 1;
-  const size_t split_lds = 4 * ((size_t)G * a.chunk + 2 * G + 4 + (ATTN_NT / 64) * 4 * (size_t)a.hd);
+  const size_t split_lds = 4 * ((size_t)G * a.chunk + 2 * G + 8 + (ATTN_NT / 64) * 4 * (size_t)a.hd);
   const size_t merge_lds = 4 * ((size_t)a.max_splits + 256 + 4);
   const dim3 g(a.max_splits, a.n_kv), b(ATTN_NT);
   if (a.hd == 128) {
@@ -1231,7 +1243,7 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
   const int G = n_heads / n_kv, TT = 16;
   if (G > 8 || n_kv * G != n_heads) return 1;
   const size_t split_lds =
-      4 * (NTOK * ((size_t)G * (8192 / hd) + 2 * G + (ATTN_NT / 64) * 4 * (size_t)hd) + 4);
+      4 * (NTOK * ((size_t)G * (8192 / hd) + 2 * G + (ATTN_NT / 64) * 4 * (size_t)hd) + 8);
   const size_t merge_lds = 4 * ((size_t)n_chunks + 256 + 4);
   dim3 g1(n_chunks, n_kv, (n + TT - 1) / TT), g2(n * n_heads, hd / 64);
 #define HH_PSPLIT(HDV, KV, GM)                                                                              \
