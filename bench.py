@@ -28,7 +28,7 @@ PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the fused gate+up GEMV from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE on this kernel (x 1.9999 and x 1.0 from a 512 MiB copy's counts):
 # profiles/decode_8b_q2_hbm_traffic.txt.  Re-measure when the kernel changes.
-GATE_UP_TRAFFIC_BYTES = 27_290_000
+GATE_UP_TRAFFIC_BYTES = 27_275_000
 METRIC = "decode tok/s @bs1, 8B Q2_0 2k ctx; Q1/Q2 GEMV HBM GB/s vs peak"
 
 
