@@ -72,7 +72,14 @@ def cpu_baseline(model, cfg, seed, kv_seed, tok0, budget_s: float):
             break
     o.close()
     avx2 = bool(orc.load().ho_have_avx2())
+    host = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            host = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), host)
+    except OSError:
+        pass
     return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "host_cpu": host, "nproc": os.cpu_count(),
             "sample": f"{n} decode steps of the 8B Q2_0 config from pos 2048 (f32 KV), "
                       f"{'AVX2 LUT' if avx2 else 'scalar'} Q2_0 arm, {threads} threads, {el:.1f} s"}
 
@@ -159,10 +166,15 @@ def config_legs(ctx) -> dict:
     out["cfg0_1.7b_q1"] = _generate_leg(ctx, "1.7B Q1_0", c0.replace(max_seq=max(c0.max_seq, 128)), 2025, 16,
                                         50, 1.1)
     out["cfg0_1.7b_q1"]["workload"] = "1.7B-shaped Q1_0 dense, 16-token prompt, 50 greedy tokens"
+    out["hbm_copy"] = microbench.copy_bandwidth()
+    print(f"[bench] HBM copy {out['hbm_copy']['MiB']} MiB: {out['hbm_copy']['GB/s']} GB/s (read + write)",
+          file=sys.stderr, flush=True)
     g = microbench.run(reps=1000, formats=("Q1_0", "Q2_0"), shapes=microbench.SHAPES[:3])
-    out["cfg1_gemv"] = [{k: r[k] for k in ("format", "n", "k", "us", "GB/s", "frac_peak")} for r in g]
+    out["cfg1_gemv"] = [{k: r[k] for k in ("format", "n", "k", "us", "GB/s", "frac_peak", "cache_resident_us",
+                                           "cache_resident_GB/s")} for r in g]
     for r in g:
-        print(f"[bench] GEMV {r['format']} {r['n']}x{r['k']}: {r['us']} us {r['GB/s']} GB/s", file=sys.stderr,
+        print(f"[bench] GEMV {r['format']} {r['n']}x{r['k']}: {r['us']} us {r['GB/s']} GB/s "
+              f"(cache-resident {r['cache_resident_us']} us {r['cache_resident_GB/s']} GB/s)", file=sys.stderr,
               flush=True)
     c3 = CONFIGS["9b-hybrid-q2"]
     out["cfg3_9b_hybrid"] = _generate_leg(ctx, "9B hybrid Q2_0", c3.replace(max_seq=max(c3.max_seq, 1024)), 2027,
