@@ -154,7 +154,7 @@ def _generate_leg(ctx, name: str, cfg, seed: int, n_prompt: int, n_gen: int, pen
     return {"prompt_tokens": n_prompt, "prompt_ms": round(pf_ms, 2),
             "prompt_tok_per_s": round(n_prompt / (pf_ms * 1e-3), 1), "decode_steps": n_gen - 1,
             "decode_tok_per_s": round(1000.0 / dec_ms, 2), "decode_ms_per_step": round(dec_ms, 4),
-            "first_tokens": [int(t) for t in toks[:8]]}
+            "repeat_pen": pen, "first_tokens": [int(t) for t in toks[:8]]}
 
 
 def config_legs(ctx) -> dict:
