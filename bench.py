@@ -234,7 +234,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs one GPU per process: bench.py measures --gpus 1 only; "
-                                   "see DESIGN.md for how the decode path would shard"}))
+                                   "multi-GPU sharding (LM head by vocab rows, layers by pipeline stage) is not built"}))
         sys.exit(2)
 
     if not args.no_configs:

@@ -127,12 +127,11 @@ __global__ __launch_bounds__(256) void k_embed(int type, const uint8_t* __restri
 // kvh = qh / (n_heads/n_kv); qwen35.rs:1495-1640 with the q|gate split and
 // sigmoid gate).  Split over the sequence: workgroup (s, kvh) owns positions
 // [s*C, s*C+C) for the G query heads of kv head kvh, with C*hd = 8192 so a
-// chunk of K and of V is 32 KB each, staged through LDS.  Prep (per-head
+// chunk of K and of V is 32 KB each (f32), held in registers.  Prep (per-head
 // RMSNorm mod.rs:551-578, RoPE :582-593, KV write :596-605) is fused: every
 // workgroup normalises its q heads; the one holding `pos` also writes K/V.
-// The last workgroup of a kv head (device counter) merges the splits
-// (max-rescaled sums), applies the qwen35 gate, and emits the packed Q8_0
-// input of attn_output.
+// A second kernel merges the splits (max-rescaled sums), applies the qwen35
+// gate, and emits the packed Q8_0 input of attn_output.
 // ---------------------------------------------------------------------------
 // A lane's float4 column slice x[4c .. 4c+3] of one head (c < LPR = HD/4;
 // every LPR-lane group holds the whole head).  Per-head RMSNorm
