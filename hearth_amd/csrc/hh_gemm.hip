@@ -12,10 +12,10 @@
 //   Q8:    sum += ((float)i * dw) * da     (32-weight blocks)
 // so each output equals the decode GEMV's bit for bit.
 //
-// Tiling: a 512-lane workgroup owns 128 tokens x 64 rows; wave w owns tokens
-// [16w, 16w+16) and all 64 rows as four 16x16 MFMA tiles.  Per 128-column
-// step the workgroup stages the activation bytes and scales of its 128 tokens
-// and the weight blocks of its 64 rows in LDS, the weight codes widened to
+// Tiling: a 512-lane workgroup owns 128 tokens x TN rows (64 or 96); wave w
+// owns tokens [16w, 16w+16) and all TN rows as TN/16 16x16 MFMA tiles.  Per
+// 128-column step the workgroup stages the activation bytes and scales of its
+// 128 tokens and the weight blocks of its TN rows in LDS, the weight codes widened to
 // int8 (code - 1, or +-1 per sign bit) once as they are stored
 // (double-buffered: the next step's global loads are issued before this
 // step's MFMAs).  Activations come split (int8 rows + f32 block scales), so
@@ -31,7 +31,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int NTG = 512;       // lanes per workgroup (8 waves, two per SIMD)
 constexpr int TM = 128;        // tokens per workgroup
-constexpr int TN = 64;         // rows per workgroup
+// rows per workgroup: TN (a template argument) = 64, or 96 for the large-N
+// launches of the non-Q8 formats (96 rows hold 6 MFMA tiles per wave within
+// the 256 registers of two waves per SIMD; Q8_0 would spill)
 constexpr int KS = 128;        // columns per step
 // LDS bytes per token / weight row: 34 dwords (= 2 mod 32 banks), so the 16
 // rows of an MFMA operand read (8 bytes per lane) fall on distinct bank pairs;
@@ -41,7 +43,7 @@ constexpr int AROW = KS + 8;
 // Activations arrive split: xq = int8 [seq][K], xd = f32 [seq][K/32] (the
 // Q8_0 scale of each 32-block).  Per step a lane copies two 16-byte pieces of
 // the 128 x 128 int8 tile and one scale; weight roles are wave-uniform.
-struct Stage {
+template <int TN> struct Stage {
   int8_t a[TM * AROW];     // activations, int8
   int8_t w[TN * AROW];     // weights widened to int8 (code - 1, or +-1)
   float da[4 * TM];        // activation scale per (sub-block, token)
@@ -82,18 +84,18 @@ template <int FMT> HH_DEV constexpr int w_code_units() {
 }
 template <int FMT> HH_DEV constexpr int w_block_bytes() { return FMT == FMT_Q1 ? 18 : FMT == FMT_PT ? 28 : 34; }
 template <int FMT> HH_DEV constexpr int w_scale_off() { return FMT == FMT_PT ? 26 : 0; }
-template <int FMT> HH_DEV constexpr int w_regs() { return (TN * w_code_units<FMT>() + NTG - 1) / NTG; }
+template <int FMT, int TN> HH_DEV constexpr int w_regs() { return (TN * w_code_units<FMT>() + NTG - 1) / NTG; }
 template <int FMT> HH_DEV constexpr int w_scales() { return FMT == FMT_Q8 ? 4 : 1; }   // per row per step
 
-template <int FMT> struct Regs {
+template <int FMT, int TN> struct Regs {
   uint4 a[2];
   float ad;
-  uint32_t w[w_regs<FMT>()];
+  uint32_t w[w_regs<FMT, TN>()];
   uint32_t ws;
 };
 
-template <int FMT>
-HH_DEV void stage_load(Regs<FMT>& R, const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
+template <int FMT, int TN>
+HH_DEV void stage_load(Regs<FMT, TN>& R, const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
                        const float* __restrict__ xd, int n, int seq, int K, int r0, int s0, int kb) {
   const int tid = threadIdx.x;
 #pragma unroll
@@ -111,7 +113,7 @@ HH_DEV void stage_load(Regs<FMT>& R, const uint8_t* __restrict__ w, const int8_t
   const size_t row_bytes = (size_t)K / (FMT == FMT_Q8 ? 32 : 128) * w_block_bytes<FMT>();
   const size_t step_bytes = FMT == FMT_Q8 ? 136 : w_block_bytes<FMT>();
 #pragma unroll
-  for (int i = 0; i < w_regs<FMT>(); ++i) {
+  for (int i = 0; i < w_regs<FMT, TN>(); ++i) {
     const int idx = min(tid + NTG * i, TN * CU - 1);
     const int rr = idx / CU, u = idx % CU, r = min(r0 + rr, n - 1);
     const uint8_t* base = w + (size_t)r * row_bytes + (size_t)kb * step_bytes;
@@ -125,8 +127,8 @@ HH_DEV void stage_load(Regs<FMT>& R, const uint8_t* __restrict__ w, const int8_t
   }
 }
 
-template <int FMT>
-HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
+template <int FMT, int TN>
+HH_DEV void stage_store(Stage<TN>& st, const Regs<FMT, TN>& R) {
   const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -138,9 +140,9 @@ HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
   st.da[(tid & 3) * TM + (tid >> 2)] = R.ad;        // loaded as (t = tid / 4, sub = tid % 4)
   constexpr int CU = w_code_units<FMT>();
 #pragma unroll
-  for (int i = 0; i < w_regs<FMT>(); ++i) {
+  for (int i = 0; i < w_regs<FMT, TN>(); ++i) {
     const int idx = tid + NTG * i;
-    if (idx < TN * CU) {   // Q2: 1024, Q1: 512, Q8: 4096, PTQ1_0: 448 (lanes 448.. idle)
+    if (idx < TN * CU) {   // TN = 64: Q2 1024, Q1 512, Q8 4096, PTQ1_0 448 (lanes 448.. idle)
       const int rr = idx / CU, u = idx % CU;
       const uint32_t v = R.w[i];
       if constexpr (FMT == FMT_Q2) {
@@ -182,18 +184,19 @@ HH_DEV void stage_store(Stage& st, const Regs<FMT>& R) {
   }
 }
 
-template <int FMT>
+template <int FMT, int TN>
 __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, const int8_t* __restrict__ xq,
                                               const float* __restrict__ xd, float* __restrict__ out, int n, int K,
                                               int seq) {
 #pragma clang fp contract(off)
-  __shared__ Stage st[2];
+  __shared__ Stage<TN> st[2];
+  constexpr int NTT = TN / 16;   // MFMA tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int r0 = blockIdx.x * TN, s0 = blockIdx.y * TM;
   const int nsteps = K / KS;
-  float sum[4][4], bacc[4][4];
+  float sum[NTT][4], bacc[NTT][4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < NTT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) { sum[t][r] = 0.0f; bacc[t][r] = 0.0f; }
 
@@ -201,24 +204,24 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
   // earlier) is written to the free LDS buffer and the global loads of step
   // kb + 3 are issued into the register set just freed, so every load has two
   // steps' compute to land.
-  Regs<FMT> R0, R1;
-  stage_load<FMT>(R0, w, xq, xd, n, seq, K, r0, s0, 0);
-  if (nsteps > 1) stage_load<FMT>(R1, w, xq, xd, n, seq, K, r0, s0, 1);
-  stage_store<FMT>(st[0], R0);
-  if (nsteps > 2) stage_load<FMT>(R0, w, xq, xd, n, seq, K, r0, s0, 2);
+  Regs<FMT, TN> R0, R1;
+  stage_load<FMT, TN>(R0, w, xq, xd, n, seq, K, r0, s0, 0);
+  if (nsteps > 1) stage_load<FMT, TN>(R1, w, xq, xd, n, seq, K, r0, s0, 1);
+  stage_store<FMT, TN>(st[0], R0);
+  if (nsteps > 2) stage_load<FMT, TN>(R0, w, xq, xd, n, seq, K, r0, s0, 2);
   __syncthreads();
   const int arow = 16 * wid + (lane & 15);   // A operand token (within the tile)
   const int kg = 8 * (lane >> 4);            // k offset within a sub-block
   const int tok0 = 16 * wid + 4 * (lane >> 4);
-  auto step = [&](int kb, Regs<FMT>& Rn) {   // Rn holds step kb + 1
-    const Stage& S = st[kb & 1];
+  auto step = [&](int kb, Regs<FMT, TN>& Rn) {   // Rn holds step kb + 1
+    const Stage<TN>& S = st[kb & 1];
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
       const long a = *(const long*)(S.a + arow * AROW + sub * 32 + kg);
       const float4 da4 = *(const float4*)(S.da + sub * TM + tok0);
       const float da[4] = {da4.x, da4.y, da4.z, da4.w};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < NTT; ++t) {
         const int col = 16 * t + (lane & 15);
         const long b = *(const long*)(S.w + col * AROW + sub * 32 + kg);
         v4i c = {0, 0, 0, 0};
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
     }
     if constexpr (FMT != FMT_Q8) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < NTT; ++t) {
         const float dw = S.dw[(16 * t + (lane & 15)) * 4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -247,8 +250,8 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
         }
       }
     }
-    if (kb + 1 < nsteps) stage_store<FMT>(st[(kb + 1) & 1], Rn);
-    if (kb + 3 < nsteps) stage_load<FMT>(Rn, w, xq, xd, n, seq, K, r0, s0, kb + 3);
+    if (kb + 1 < nsteps) stage_store<FMT, TN>(st[(kb + 1) & 1], Rn);
+    if (kb + 3 < nsteps) stage_load<FMT, TN>(Rn, w, xq, xd, n, seq, K, r0, s0, kb + 3);
     __syncthreads();
   };
   for (int kb = 0; kb < nsteps; kb += 2) {
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
     if (kb + 1 < nsteps) step(kb + 1, R0);
   }
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < NTT; ++t) {
     const int r = r0 + 16 * t + (lane & 15);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -282,14 +285,21 @@ __global__ void k_q8_split(const uint8_t* __restrict__ x, int64_t nblocks, int8_
 int hh_gemm_launch(int fmt, const uint8_t* w, int n, int K, const int8_t* xq, const float* xd, int seq, float* out,
                    hipStream_t s) {
   if (K % KS != 0 || n <= 0 || seq <= 0) return 1;
-  dim3 grid((n + TN - 1) / TN, (seq + TM - 1) / TM);
+  // 96-row tiles where they still give >= 1024 workgroups (8B / 27B FFN
+  // gate+up: +6-7%); 64 otherwise (96 made the 27B down, N = 5120, 7% slower)
+  const long tiles96 = (long)((n + 95) / 96) * ((seq + TM - 1) / TM);
+  const bool wide = fmt != FMT_Q8 && tiles96 >= 1024;
+  const int TNv = wide ? 96 : 64;
+  dim3 grid((n + TNv - 1) / TNv, (seq + TM - 1) / TM);
+#define HH_GEMM(F, T) hipLaunchKernelGGL((k_gemm<F, T>), grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq)
   switch (fmt) {
-    case FMT_Q2: hipLaunchKernelGGL(k_gemm<FMT_Q2>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
-    case FMT_Q1: hipLaunchKernelGGL(k_gemm<FMT_Q1>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
-    case FMT_Q8: hipLaunchKernelGGL(k_gemm<FMT_Q8>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
-    case FMT_PT: hipLaunchKernelGGL(k_gemm<FMT_PT>, grid, dim3(NTG), 0, s, w, xq, xd, out, n, K, seq); break;
+    case FMT_Q2: if (wide) HH_GEMM(FMT_Q2, 96); else HH_GEMM(FMT_Q2, 64); break;
+    case FMT_Q1: if (wide) HH_GEMM(FMT_Q1, 96); else HH_GEMM(FMT_Q1, 64); break;
+    case FMT_Q8: HH_GEMM(FMT_Q8, 64); break;
+    case FMT_PT: if (wide) HH_GEMM(FMT_PT, 96); else HH_GEMM(FMT_PT, 64); break;
     default: return 1;
   }
+#undef HH_GEMM
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
