@@ -770,6 +770,11 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   }
   HIP_TRY(hipSetDevice(ctx->device));
   hh_model* m = new hh_model();
+  // every early return below releases what was allocated so far
+  struct Guard {
+    hh_model* m;
+    ~Guard() { if (m) hh_model_destroy(m); }
+  } guard{m};
   m->ctx = ctx;
   m->cfg = c;
   m->wfmt = wf;
@@ -791,7 +796,7 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   m->arena_bytes = align256(off);
   hipError_t e = hipMalloc(&m->arena, m->arena_bytes);
   if (e != hipSuccess) {
-    delete m;
+    m->arena = nullptr;
     return fail(HH_ERR_OOM, "weight arena allocation failed (" + std::to_string(m->arena_bytes) + " bytes)");
   }
   for (size_t i = 0; i < m->tensors.size(); ++i) m->tensors[i].d = m->arena + offs[i];
@@ -844,14 +849,14 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   m->kv_bytes = cache_bytes * 2 * (size_t)n_attn;
   if (m->kv_bytes) {
     e = hipMalloc(&m->kv, m->kv_bytes);
-    if (e != hipSuccess) { hh_model_destroy(m); return fail(HH_ERR_OOM, "KV cache allocation failed"); }
+    if (e != hipSuccess) { m->kv = nullptr; return fail(HH_ERR_OOM, "KV cache allocation failed"); }
   }
   size_t rec_per = 0;
   if (c.arch == 1) {
     rec_per = (size_t)c.ssm_n_v_heads * c.ssm_head_dim * c.ssm_head_dim + (size_t)conv_dim * (c.ssm_conv_kernel - 1);
     m->rec_bytes = sizeof(float) * rec_per * (size_t)n_gdn;
     e = hipMalloc(&m->rec, m->rec_bytes);
-    if (e != hipSuccess) { hh_model_destroy(m); return fail(HH_ERR_OOM, "recurrent state allocation failed"); }
+    if (e != hipSuccess) { m->rec = nullptr; return fail(HH_ERR_OOM, "recurrent state allocation failed"); }
   }
   if (m->kv) HIP_TRY(hipMemset(m->kv, 0, m->kv_bytes));
   if (m->rec) HIP_TRY(hipMemset(m->rec, 0, m->rec_bytes));
@@ -926,7 +931,8 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   }
   HIP_TRY(hipDeviceSynchronize());
   int rc = capture(m);
-  if (rc) { std::string msg = g_err; hh_model_destroy(m); return fail(rc, "graph capture: " + msg); }
+  if (rc) return fail(rc, "graph capture: " + std::string(g_err));
+  guard.m = nullptr;
   *out = m;
   return HH_OK;
 }

@@ -316,6 +316,51 @@ int ho_dequantize(int type, const uint8_t* w, int64_t n, float* out) {
 /* dot kernels                                                               */
 /* ------------------------------------------------------------------------- */
 
+/* Exact int32 sub-block dots (32 elements) for the scalar-order kernels below.
+ * The integer sum is exact in any order, so it is computed with AVX2 byte
+ * multiply-adds from per-byte expansion tables; only the fp32 combine above it
+ * has to follow the reference's order.  q2lut[b] = the four 2-bit codes of byte
+ * b as bytes (LSB first); q1lut[b] = the eight bits of b as 0/1 bytes. */
+static uint32_t q2lut[256];
+static uint64_t q1lut[256];
+__attribute__((constructor)) static void init_luts(void) {
+  for (int b = 0; b < 256; b++) {
+    uint32_t v = 0;
+    for (int k = 0; k < 4; k++) v |= (uint32_t)((b >> (2 * k)) & 3) << (8 * k);
+    q2lut[b] = v;
+    uint64_t u = 0;
+    for (int k = 0; k < 8; k++) u |= (uint64_t)((b >> k) & 1) << (8 * k);
+    q1lut[b] = u;
+  }
+}
+static inline int32_t hsum_i32x8(__m256i v) {
+  __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+  s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4E));
+  s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xB1));
+  return _mm_cvtsi128_si32(s);
+}
+/* sum_i u[i] * a[i] - bias * sum_i a[i], u unsigned bytes (0..3) */
+static inline int32_t udot32(__m256i u, const int8_t* a, int bias) {
+  const __m256i ones8 = _mm256_set1_epi8(1), ones16 = _mm256_set1_epi16(1);
+  __m256i av = _mm256_loadu_si256((const __m256i*)a);
+  __m256i p = _mm256_madd_epi16(_mm256_maddubs_epi16(u, av), ones16);
+  __m256i s = _mm256_madd_epi16(_mm256_maddubs_epi16(ones8, av), ones16);
+  return hsum_i32x8(p) - bias * hsum_i32x8(s);
+}
+/* sum (code - 1) * a over one 32-element sub-block (8 code bytes) */
+static inline int32_t sub_dot_q2(const uint8_t* q, const int8_t* a) {
+  __m256i u = _mm256_setr_epi32((int)q2lut[q[0]], (int)q2lut[q[1]], (int)q2lut[q[2]], (int)q2lut[q[3]],
+                                (int)q2lut[q[4]], (int)q2lut[q[5]], (int)q2lut[q[6]], (int)q2lut[q[7]]);
+  return udot32(u, a, 1);
+}
+/* sum (bit ? +1 : -1) * a = 2 * sum bit * a - sum a over one sub-block (4 bit bytes) */
+static inline int32_t sub_dot_q1(const uint8_t* q, const int8_t* a) {
+  __m256i u = _mm256_setr_epi64x((long long)q1lut[q[0]], (long long)q1lut[q[1]], (long long)q1lut[q[2]],
+                                 (long long)q1lut[q[3]]);
+  u = _mm256_add_epi8(u, u);
+  return udot32(u, a, 1);
+}
+
 /* q2_0.rs:537-574 scalar Q2_0 x Q8_0. */
 float ho_dot_q2_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n) {
   int64_t blocks = n / 128;
@@ -329,12 +374,7 @@ float ho_dot_q2_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n) {
       const uint8_t* ab = a + (b * 4 + sub) * 34;
       float a_scale = rd_f16(ab);
       const int8_t* av = (const int8_t*)(ab + 2);
-      const uint8_t* qsub = qs + sub * 8;
-      int32_t dot = 0;
-      for (int i = 0; i < 32; i++) {
-        int code = (qsub[i / 4] >> (2 * (i % 4))) & 3;
-        dot += (code - 1) * (int32_t)av[i];
-      }
+      int32_t dot = sub_dot_q2(qs + sub * 8, av);   /* sum (code - 1) * a, exact */
       block_acc += (float)dot * a_scale;
     }
     sum += block_acc * w_scale;
@@ -378,12 +418,7 @@ float ho_dot_q1_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n) {
       const uint8_t* ab = a + (b * 4 + sub) * 34;
       float a_scale = rd_f16(ab);
       const int8_t* av = (const int8_t*)(ab + 2);
-      const uint8_t* bsub = bits + sub * 4;
-      int32_t dot = 0;
-      for (int i = 0; i < 32; i++) {
-        int bit = (bsub[i / 8] >> (i % 8)) & 1;
-        dot += (bit ? 1 : -1) * (int32_t)av[i];
-      }
+      int32_t dot = sub_dot_q1(bits + sub * 4, av);  /* sum (bit ? 1 : -1) * a, exact */
       block_acc += (float)dot * a_scale;
     }
     sum += block_acc * w_scale;
@@ -400,8 +435,12 @@ float ho_dot_q8_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n) {
     float d1 = rd_f16(a + b * 34);
     const int8_t* wv = (const int8_t*)(w + b * 34 + 2);
     const int8_t* av = (const int8_t*)(a + b * 34 + 2);
-    int32_t sumi = 0;
-    for (int i = 0; i < 32; i++) sumi += (int32_t)wv[i] * (int32_t)av[i];
+    /* exact int32 sum of the 32 products (int8 widened to int16, then madd) */
+    __m256i w0 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)wv));
+    __m256i w1 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(wv + 16)));
+    __m256i a0 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)av));
+    __m256i a1 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(av + 16)));
+    int32_t sumi = hsum_i32x8(_mm256_add_epi32(_mm256_madd_epi16(w0, a0), _mm256_madd_epi16(w1, a1)));
     sumf += (float)sumi * d0 * d1;
   }
   return sumf;
@@ -1310,6 +1349,7 @@ static void dev_head_gemv(int type, const uint8_t* w, int64_t rows, int64_t K, c
 
 /* LM head in the model's order. */
 static void head_mm(ho_model* m, const float* x, float* logits) {
+  if (!logits) return; /* a prompt token whose logits nobody reads */
   const tensor_t* w = m->output;
   ho_quantize_q8_0(x, w->cols, m->q8);
   if (m->order) dev_head_gemv(w->type, w->data, w->rows, w->cols, m->q8, logits, m->n_threads);
@@ -1622,7 +1662,7 @@ int ho_generate(ho_model* m, const uint32_t* prompt, int n_prompt, int start_pos
   uint32_t* past = (uint32_t*)xcalloc((size_t)n_gen + 2, sizeof(uint32_t));
   int n_past = 0, rc = 0;
   for (int i = 0; i < n_prompt; i++) {
-    rc = ho_forward(m, prompt[i], start_pos + i, logits);
+    rc = ho_forward(m, prompt[i], start_pos + i, i + 1 < n_prompt ? NULL : logits);
     if (rc) goto done;
   }
   past[n_past++] = prompt[n_prompt - 1];

@@ -1,0 +1,82 @@
+"""GPU parity at the BASELINE.json model geometries that the other model tests
+only slice: configs[0] (the full 1.7B Q1_0 dense model) and configs[4] (the
+27B PQ2_0 hybrid geometry, a few layers, batched prefill at 8192 context).
+
+Bars: tokens and logits bit-identical to the device-order oracle (the HIP
+kernels' fp32 grouping), and, against the reference-order oracle, every greedy
+step teacher-forced on the reference's own sequence picks the reference's
+token or one the reference's own scalar and AVX2 arms cannot tell apart
+(tests/tokcheck.py)."""
+import numpy as np
+import pytest
+
+from hearth_amd.lib import CONFIGS
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def _prompt(oracle, seed, n, vocab):
+    return [oracle.synth_token(seed, i, vocab) for i in range(n)]
+
+
+@pytest.fixture(scope="module")
+def m17(ctx):
+    from hearth_amd import Model
+    m = Model(ctx, CONFIGS["1.7b-q1"])
+    m.synthesize(1)
+    yield m
+    m.close()
+
+
+def test_config0_1p7b_q1_device_order(ctx, oracle, m17):
+    """d 2048, 28 layers, 16/8 x 128, ffn 6144, vocab 151936, Q1_0
+    layers, Q8_0 embedding/head; 16-token seeded prompt, 50 greedy tokens with
+    the sampler's default repetition penalty 1.1 (core/sampler.rs:18)."""
+    cfg = CONFIGS["1.7b-q1"]
+    prompt = _prompt(oracle, 1, 16, cfg.vocab)
+    print("config0 device-order generate", flush=True)
+    m17.reset()
+    toks, lg = m17.generate(prompt, 50, repeat_pen=1.1, want_logits=True)
+    o = oracle.OracleModel(cfg, seed=1, threads=16, order=oracle.OracleModel.DEVICE)
+    tw, lw = o.generate(prompt, 50, repeat_pen=1.1, want_logits=True)
+    o.close()
+    assert list(toks) == list(tw)
+    assert np.array_equal(lg, lw)
+
+
+def test_config0_1p7b_q1_reference_order(ctx, oracle, m17):
+    """configs[0] against the reference-order oracle: 50 greedy steps (penalty
+    1.1), teacher-forced on the reference's sequence."""
+    from tokcheck import reference_run, check_candidate
+    cfg = CONFIGS["1.7b-q1"]
+    prompt = _prompt(oracle, 1, 16, cfg.vocab)
+    print("config0 reference run", flush=True)
+    seq, ref_logits, spread = reference_run(oracle, cfg, 1, prompt, 50, threads=16, pen=1.1)
+    m17.reset()
+    div = check_candidate(cfg, seq, ref_logits, spread, len(prompt), lambda t, p: m17.forward(t, p)[0],
+                          oracle=oracle, pen=1.1)
+    print(f"config0: arm spread {spread:.3g}, divergences {div}", flush=True)
+    assert len(div) <= 5
+
+
+def test_config4_27b_pq2_prefill_decode(ctx, oracle):
+    """configs[4] geometry (d 5120, ffn 17408, 24/4 x 256 attention with the
+    gate, GDN 16 k / 32 v x 128, vocab 248320, PQ2_0) with 4 layers (3 GDN + 1
+    full attention) at max_seq 8192: a 320-token batched prefill on the MFMA
+    GEMM, then 16 greedy decode steps.  Tokens and final logits equal the
+    device-order oracle fed token by token."""
+    from hearth_amd import Model
+    cfg = CONFIGS["27b-hybrid-pq2"].replace(n_layers=4, max_seq=8192)
+    m = Model(ctx, cfg)
+    m.synthesize(13)
+    prompt = _prompt(oracle, 11, 320, cfg.vocab)
+    print("config4 generate (batched prefill)", flush=True)
+    toks, lg = m.generate(prompt, 16, repeat_pen=1.0, want_logits=True)
+    assert m.last_prefill_ms() > 0
+    m.close()
+    o = oracle.OracleModel(cfg, seed=13, threads=16, order=oracle.OracleModel.DEVICE)
+    tw, lw = o.generate(prompt, 16, repeat_pen=1.0, want_logits=True)
+    o.close()
+    assert list(toks) == list(tw)
+    assert np.array_equal(lg, lw)

@@ -7,9 +7,9 @@ The oracle runs in its device association order (the HIP kernels' reduction
 grouping, same mathematics): GEMVs, quantization, norms, attention and the GDN
 step then agree bit for bit, so the logits are compared for equality as well as
 against the 1e-3 bar.  The reference-order oracle is compared at a looser bar
-in test_reference_order_spread: there every reduction regroups, which moves
-logits by Q8_0 rounding flips, as the reference's own scalar and AVX2 GEMV arms
-do to each other."""
+in test_reference_order_spread and tests/test_golden.py: there every reduction
+regroups, which moves logits by Q8_0 rounding flips, as the reference's own
+scalar and AVX2 GEMV arms do to each other."""
 import numpy as np
 import pytest
 
@@ -116,16 +116,28 @@ def test_long_context_decode(ctx, oracle, cfg, kv_type):
     o.close()
 
 
+@pytest.mark.parametrize("seed", [9, 10, 11])
 @pytest.mark.parametrize("cfg", [TINY, TINY_HYB], ids=["dense", "hybrid"])
-def test_reference_order_spread(ctx, oracle, cfg):
-    """Against the reference-order oracle: first-step logits within 5e-2.  The
-    reference's own scalar vs AVX2 GEMV arms differ by up to 1.3e-2 on these
-    models (measured with the oracle's two arms); regrouping every reduction
-    (norms, attention, GDN) as well gives up to 2.5e-2 on the hybrid."""
-    m, o = make(ctx, oracle, cfg, seed=9, order=0)
-    lg, _ = m.forward(123, 0)
-    lw = o.forward(123, 0)
-    assert rel(lg, lw) < 5e-2
+def test_reference_order_spread(ctx, oracle, cfg, seed):
+    """Against the reference-order oracle over 8 decode steps: the device's
+    logits are as close to the reference's scalar arm as the reference's own
+    AVX2 arm is.  Every regrouped fp32 sum can flip a Q8_0 rounding of a later
+    activation, so neither the AVX2 arm nor the device holds 1e-3 on whole-model
+    logits once such a flip occurs; the bar is max(1e-3, 1.25 x the AVX2 arm's
+    largest relative deviation over the same 8 steps)."""
+    from hearth_amd import Model
+    m = Model(ctx, cfg)
+    m.synthesize(seed)
+    ref = oracle.OracleModel(cfg, seed=seed, threads=16, arm=0, order=0)
+    avx = oracle.OracleModel(cfg, seed=seed, threads=16, arm=1, order=0)
+    arms, dev = [], []
+    for pos, t in enumerate([123, 5, 900, 17, 3000, 44, 1, 2]):
+        lr = ref.forward(t, pos)
+        arms.append(rel(avx.forward(t, pos), lr))
+        dev.append(rel(m.forward(t, pos)[0], lr))
+    print(f"seed {seed}: AVX2 arm {np.round(arms, 4)}, device {np.round(dev, 4)}", flush=True)
+    assert max(dev) <= max(1e-3, 1.25 * max(arms)), (dev, arms)
+    m.close()
 
 
 def test_model_errors(ctx):
@@ -198,7 +210,8 @@ def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
     """forward_batch on the MFMA GEMM leaves the same KV cache (and, on the
     hybrids, the same conv windows and GDN states) as feeding the prompt one
     token at a time: the first generated token's logits and the next tokens are
-    identical, and match the device-order oracle.  hybrid-2 prefills fewer
+    identical, and match the device-order oracle (at 300 tokens too: the
+oracle skips the LM head for prompt tokens).  hybrid-2 prefills fewer
     tokens than the conv window holds; the kvq8 cases write a Q8_0 cache
     (quantized on write as the decode step does)."""
     print(f"prefill {cfg.d_model} {cfg.n_layers} n={n_prompt}", flush=True)
@@ -210,12 +223,11 @@ def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
     tt, lt = mt.generate(prompt, 8, repeat_pen=pen, want_logits=True)
     assert list(tb) == list(tt)
     assert np.array_equal(lb, lt)
-    if n_prompt <= 40:
-        o = oracle.OracleModel(cfg, seed=13, threads=16, order=oracle.OracleModel.DEVICE)
-        tw, lw = o.generate(prompt, 8, repeat_pen=pen, want_logits=True)
-        assert list(tb) == list(tw)
-        assert np.array_equal(lb, lw)
-        o.close()
+    o = oracle.OracleModel(cfg, seed=13, threads=16, order=oracle.OracleModel.DEVICE)
+    tw, lw = o.generate(prompt, 8, repeat_pen=pen, want_logits=True)
+    assert list(tb) == list(tw)
+    assert np.array_equal(lb, lw)
+    o.close()
     mb.close()
     mt.close()
 
