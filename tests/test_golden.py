@@ -99,7 +99,7 @@ def test_golden_gpu_model_hybrid(ctx, oracle, seed):
     sys.path.insert(0, os.path.join(HERE, "golden"))
     import make_golden
     from hearth_amd import Model
-    from tokcheck import reference_run, check_candidate
+    from tokcheck import reference_run, check_candidate, ambiguous_steps
     cfg = make_golden.HYBRID
     m = Model(ctx, cfg)
     m.synthesize(seed)
@@ -112,6 +112,8 @@ def test_golden_gpu_model_hybrid(ctx, oracle, seed):
     if seed == int(G["seed"][0]):
         assert np.array_equal(np.asarray(seq[len(prompt):]), G["hybrid_tokens"])
     div = check_candidate(cfg, seq, ref_logits, spread, len(prompt), lambda t, p: m.forward(t, p)[0])
-    print(f"seed {seed}: arm spread {spread:.3g}, divergences {div}", flush=True)
-    assert len(div) <= 4
+    amb = ambiguous_steps(ref_logits, spread)
+    print(f"seed {seed}: arm spread {spread:.3g}, ambiguous steps {amb}, "
+          f"AVX2-arm divergences {reference_run.avx_divergences}, divergences {div}", flush=True)
+    assert len(div) <= amb
     m.close()

@@ -48,7 +48,7 @@ def test_config0_1p7b_q1_device_order(ctx, oracle, m17):
 def test_config0_1p7b_q1_reference_order(ctx, oracle, m17):
     """configs[0] against the reference-order oracle: 50 greedy steps (penalty
     1.1), teacher-forced on the reference's sequence."""
-    from tokcheck import reference_run, check_candidate
+    from tokcheck import reference_run, check_candidate, ambiguous_steps
     cfg = CONFIGS["1.7b-q1"]
     prompt = _prompt(oracle, 1, 16, cfg.vocab)
     print("config0 reference run", flush=True)
@@ -56,8 +56,10 @@ def test_config0_1p7b_q1_reference_order(ctx, oracle, m17):
     m17.reset()
     div = check_candidate(cfg, seq, ref_logits, spread, len(prompt), lambda t, p: m17.forward(t, p)[0],
                           oracle=oracle, pen=1.1)
-    print(f"config0: arm spread {spread:.3g}, divergences {div}", flush=True)
-    assert len(div) <= 5
+    amb = ambiguous_steps(ref_logits, spread)
+    print(f"config0: arm spread {spread:.3g}, ambiguous steps {amb}, "
+          f"AVX2-arm divergences {reference_run.avx_divergences}, divergences {div}", flush=True)
+    assert len(div) <= amb
 
 
 def test_config4_27b_pq2_prefill_decode(ctx, oracle):

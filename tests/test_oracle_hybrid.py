@@ -141,10 +141,12 @@ def test_hybrid_device_order_tokens_vs_reference_order(oracle, seed):
     import sys, os
     sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
     import make_golden
-    from tokcheck import reference_run, check_candidate
+    from tokcheck import reference_run, check_candidate, ambiguous_steps
     cfg = make_golden.HYBRID
     seq, ref_logits, spread = reference_run(oracle, cfg, seed, make_golden.PROMPT, 32)
     dev = oracle.OracleModel(cfg, seed=seed, threads=4, order=oracle.OracleModel.DEVICE)
     div = check_candidate(cfg, seq, ref_logits, spread, len(make_golden.PROMPT), dev.forward)
-    print(f"seed {seed}: arm spread {spread:.3g}, divergences {div}")
-    assert len(div) <= 4
+    amb = ambiguous_steps(ref_logits, spread)
+    print(f"seed {seed}: arm spread {spread:.3g}, ambiguous steps {amb}, "
+          f"AVX2-arm divergences {reference_run.avx_divergences}, divergences {div}", flush=True)
+    assert len(div) <= amb

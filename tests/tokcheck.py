@@ -58,6 +58,7 @@ def reference_run(oracle, cfg, seed, prompt, n_gen, threads=4, pen=1.0, prefille
     seq = list(prompt)
     past = [prompt[-1]]
     logits, spread = [], 0.0
+    avx_div = 0
     for i in range(len(prompt) + n_gen - 1):
         pos = prefilled + i
         need = i >= len(prompt) - 1
@@ -67,13 +68,25 @@ def reference_run(oracle, cfg, seed, prompt, n_gen, threads=4, pen=1.0, prefille
             spread = max(spread, float(np.abs(lr.astype(np.float64) - la).max()))
             logits.append(_penalized(oracle, lr, past, pen))
             tok = _pick(oracle, cfg, lr, past, pen)
+            avx_div += int(_pick(oracle, cfg, la, past, pen) != tok)
             seq.append(tok)
             past.append(tok)
         else:
             avx.lib.ho_forward(avx.h, seq[i], pos, None)
     ref.close()
     avx.close()
+    reference_run.avx_divergences = avx_div
     return seq, logits, spread
+
+
+def ambiguous_steps(ref_logits, spread):
+    """Steps whose reference top-2 gap is below the arm spread: the only steps
+    at which a divergence is accepted."""
+    n = 0
+    for lr in ref_logits:
+        top2 = np.partition(np.asarray(lr, np.float64), -2)[-2:]
+        n += int(top2[1] - top2[0] <= spread)
+    return n
 
 
 def check_candidate(cfg, seq, ref_logits, spread, n_prompt, forward, oracle=None, pen=1.0, prefilled=0):
