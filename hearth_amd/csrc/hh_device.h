@@ -253,6 +253,38 @@ HH_DEV float block_sumsq_f4(const float* __restrict__ x, int K, float* red16) {
   return tree16(red16);
 }
 
+// ---- Hadamard fold (qwen35.rs:51-118) ----
+// Normalized Sylvester Walsh-Hadamard transform of every `blk`-element chunk
+// of x[K] (K % blk == 0) in LDS, by all NTH lanes of the workgroup:
+// butterflies h = 1, 2, 4, ..., blk/2 with x[i] = a + b, x[i + h] = a - b for
+// every i with bit h clear, then x *= 1/sqrt(blk).  Each output is the same
+// sequence of IEEE additions as the reference's in-place loop, so the result
+// is bit-identical.  Starts and ends with a workgroup barrier.
+template <int NTH> HH_DEV void lds_wht(float* x, int K, int blk) {
+  const int tid = threadIdx.x;
+  for (int h = 1; h < blk; h <<= 1) {
+    __syncthreads();
+    for (int p = tid; p < K / 2; p += NTH) {
+      const int i = ((p & ~(h - 1)) << 1) | (p & (h - 1));
+      const float a = x[i], b = x[i + h];
+      x[i] = a + b;
+      x[i + h] = a - b;
+    }
+  }
+  __syncthreads();
+  const float sc = 1.0f / sqrtf((float)blk);
+  for (int i = tid; i < K; i += NTH) x[i] = x[i] * sc;
+  __syncthreads();
+}
+
+// Slot of element e of a GDN head-major vector in the grouped order the
+// ssm_out fold was computed in (qwen35.rs:1452-1478): head h = r * nk + kg
+// moves to head slot kg * rep + r.
+HH_DEV int grouped_pos(int e, int hd, int nk, int rep) {
+  const int h = e / hd;
+  return ((h % nk) * rep + h / nk) * hd + (e - h * hd);
+}
+
 // ---- counter-based seeded generator (shared definition with the CPU checker) ----
 HH_DEV uint64_t mix64(uint64_t x) {
   x ^= x >> 30;

@@ -219,6 +219,10 @@ __global__ __launch_bounds__(1024) void k_gdn_rec(GdnArgs a) {
     const float nv = vals[k] * inv * nw[k];
     const float z = zg[k];
     const float o = nv * (z / (1.0f + hx_exp(-z)));
+    if (a.out_f32) {   // folded model: ssm_out's prologue permutes, rotates and quantizes
+      a.out_f32[h * hd + dd] = o;
+      continue;
+    }
     const float am = group_max<32>(fabsf(o));
     const float sc = q8_scale(am);
     const int q = q8_round_r(o, sc, q8_rcp(sc));
@@ -372,6 +376,10 @@ __global__ __launch_bounds__(256) void k_gdn_gated_rows(GdnArgs a) {
     const float nv = vals[k] * inv * a.ssm_norm[dd];
     const float zz = z[dd];
     const float y = nv * (zz / (1.0f + hx_exp(-zz)));
+    if (a.y_rows) {   // folded model: k_rot_q8_rows permutes, rotates and quantizes
+      a.y_rows[(size_t)s * vdim + h * hd + dd] = y;
+      continue;
+    }
     const float am = group_max<32>(fabsf(y));
     const float sc = q8_scale(am);
     const int q = q8_round_r(y, sc, q8_rcp(sc));

@@ -29,7 +29,7 @@
 
 namespace {
 
-enum { PRO_PACKED = 0, PRO_RMSNORM = 1, PRO_STDQ8 = 2 };
+enum { PRO_PACKED = 0, PRO_RMSNORM = 1, PRO_STDQ8 = 2, PRO_NORMROT = 3, PRO_F32ROT = 4 };
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
 
 constexpr uint32_t M2 = 0x03030303u;
@@ -447,7 +447,94 @@ template <int FMT> HH_DEV void std_store(const GemvArgs& p, const StdRegs& r, in
   }
 }
 
+// PRO_NORMROT / PRO_F32ROT: the prologues of a Hadamard-folded matmul
+// (qwen35.rs:914-941, `mm(.., had = true)`): the f32 input (rms_norm(x, w), or
+// x itself, optionally moved to the GDN grouped head order of qwen35.rs:1452-1478)
+// times the signs goes to an LDS buffer, the WHT runs per had_block chunk
+// (lds_wht), and the rotated vector is quantized like norm_finish.  Lane t
+// (of NT) owns the float4s at 4t + 4096c; the sum of squares has the
+// block_sumsq_f4 order (slot t, c ascending; wave sums; tree16), as the
+// unfolded RMSNorm prologue.  K <= ROT_C * 4096.
+constexpr int ROT_C = 5;
+template <int FMT, bool NORM> struct RotStage {
+  float4 x[ROT_C], w[ROT_C];
+  float* buf;   // K floats of LDS, free once the activation is staged
+  HH_DEV void issue(const GemvArgs& p) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < ROT_C; ++c) {
+      const int e = 4 * tid + 4096 * c;
+      if (e < p.K) {
+        x[c] = *(const float4*)(p.x + e);
+        if constexpr (NORM) w[c] = *(const float4*)(p.norm_w + e);
+      }
+    }
+  }
+  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) {
+    const int tid = threadIdx.x, K = p.K;
+    float inv = 1.0f;
+    if constexpr (NORM) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int c = 0; c < ROT_C; ++c)
+        if (4 * tid + 4096 * c < K) ss += x[c].x * x[c].x + x[c].y * x[c].y + x[c].z * x[c].z + x[c].w * x[c].w;
+      ss = wave_sum(ss);
+      if ((tid & 63) == 0) red[tid >> 6] = ss;
+      __syncthreads();
+      inv = 1.0f / sqrtf(tree16(red) / (float)K + p.eps);   // ops.rs:22-23
+    }
+    const bool perm = p.perm_rep > 1;
+#pragma unroll
+    for (int c = 0; c < ROT_C; ++c) {
+      const int e = 4 * tid + 4096 * c;
+      if (e < K) {
+        float v[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
+        if constexpr (NORM) {
+          v[0] = v[0] * inv * w[c].x; v[1] = v[1] * inv * w[c].y;   // ops.rs:29 (x * inv) * w
+          v[2] = v[2] * inv * w[c].z; v[3] = v[3] * inv * w[c].w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = perm ? grouped_pos(e + i, 128, p.perm_nk, p.perm_rep) : e + i;
+          buf[d] = v[i] * p.signs[d];
+        }
+      }
+    }
+    lds_wht<NT>(buf, K, p.had_block);
+#pragma unroll
+    for (int c = 0; c < ROT_C; ++c) {
+      if (4096 * c >= K) break;   // uniform
+      const int e = 4 * tid + 4096 * c;
+      const bool in = e < K;
+      float vv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (in) {
+        const float4 t = *(const float4*)(buf + e);
+        vv[0] = t.x; vv[1] = t.y; vv[2] = t.z; vv[3] = t.w;
+      }
+      float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+      am = group_max<8>(am);
+      const float sc = q8_scale(am), rc = q8_rcp(sc);
+      int qs = 0;
+      uint32_t word = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = q8_round_r(vv[i], sc, rc);
+        qs += q;
+        word |= ((uint32_t)q & 0xffu) << (8 * i);
+      }
+      qs = group_sum_i<8>(qs);
+      if (in) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)(word >> (8 * i));
+        if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
+      }
+    }
+  }
+};
+
 template <int FMT, int PRO> struct ActStage;
+template <int FMT> struct ActStage<FMT, PRO_NORMROT> : RotStage<FMT, true> {};
+template <int FMT> struct ActStage<FMT, PRO_F32ROT> : RotStage<FMT, false> {};
 template <int FMT> struct ActStage<FMT, PRO_RMSNORM> {
   NormRegs r;
   HH_DEV void issue(const GemvArgs& p) { norm_issue(p, r); }
@@ -559,6 +646,8 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   };
 
   ActStage<FMT, PRO> act;
+  if constexpr (PRO == PRO_NORMROT || PRO == PRO_F32ROT)   // K floats after rowsum, 16-byte aligned
+    act.buf = (float*)(((uintptr_t)(rowsum + rows_total) + 15) & ~(uintptr_t)15);
   act.issue(p);                      // activation first (in-order retirement)
   if constexpr (NU > 0 && PRO == PRO_RMSNORM) {
     // Waves 0-3 stage the activation and raise `ready`; every wave computes as
@@ -638,6 +727,10 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
       float sc = q8_scale(am);
       int q = q8_round_r(h, sc, q8_rcp(sc));
       int qs = group_sum_i<32>(q);
+      if (p.y) {   // folded model: the next matmul rotates the f32 vector first
+        if (i < R2) p.y[((int)blockIdx.x + (i >> 5) * (int)gridDim.x) * 32 + (i & 31)] = h;
+        continue;
+      }
       if (i < R2) {
         int e = ((int)blockIdx.x + (i >> 5) * (int)gridDim.x) * 32 + (i & 31);
         p.act_out[perm_pos(p.act_out_fmt, e)] = (uint8_t)(int8_t)q;
@@ -765,7 +858,7 @@ __global__ __launch_bounds__(1024) void k_head_final(GemvArgs p, int n_part) {
 // VGPRs, with no further workgroup barrier.  Lane l holds the row's units
 // l + 64u (u < U); the row value is q_l = sum_u (p_2t + p_2t+1) over its
 // units' block products, then an ascending butterfly over the 64 lanes.
-template <int FMT, int U>
+template <int FMT, int U, int PRO>
 __global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
   constexpr int DW = UnitT<FMT>::DW;
   constexpr int UB = UnitT<FMT>::BYTES;
@@ -823,7 +916,8 @@ __global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
     }
   };
 
-  ActStage<FMT, PRO_RMSNORM> act;
+  ActStage<FMT, PRO> act;
+  if constexpr (PRO == PRO_NORMROT) act.buf = (float*)(bis + 16);   // K floats after the wave bests
   act.issue(p);
   uint32_t wa[U][DW], wb[U][DW];
   int ca, cb;
@@ -856,10 +950,19 @@ template <int FMT>
 int launch_head(GemvArgs a, hipStream_t s, int* n_wg_out) {
   const int n_wg = std::max(1, std::min(256, (a.n_rows + NT / 64 - 1) / (NT / 64)));
   const int nunits = a.K / UnitT<FMT>::EL;
-  const size_t lds = (size_t)nunits * (UnitT<FMT>::EL + 16) + (size_t)nunits * (FMT == FMT_Q8 ? 8 : 20) * 4 + 48 * 4;
-  if (a.P <= 64) hipLaunchKernelGGL((k_head<FMT, 1>), dim3(n_wg), dim3(NT), lds, s, a);
-  else if (a.P <= 128) hipLaunchKernelGGL((k_head<FMT, 2>), dim3(n_wg), dim3(NT), lds, s, a);
-  else return 1;
+  const bool rot = a.had_block > 0;
+  const size_t lds = (size_t)nunits * (UnitT<FMT>::EL + 16) + (size_t)nunits * (FMT == FMT_Q8 ? 8 : 20) * 4 + 48 * 4 +
+                     (rot ? (size_t)a.K * 4 : 0);
+  if (rot && (a.K > ROT_C * 4096 || !a.signs)) return 1;
+  if (a.P <= 64) {
+    if (rot) hipLaunchKernelGGL((k_head<FMT, 1, PRO_NORMROT>), dim3(n_wg), dim3(NT), lds, s, a);
+    else hipLaunchKernelGGL((k_head<FMT, 1, PRO_RMSNORM>), dim3(n_wg), dim3(NT), lds, s, a);
+  } else if (a.P <= 128) {
+    if (rot) hipLaunchKernelGGL((k_head<FMT, 2, PRO_NORMROT>), dim3(n_wg), dim3(NT), lds, s, a);
+    else hipLaunchKernelGGL((k_head<FMT, 2, PRO_RMSNORM>), dim3(n_wg), dim3(NT), lds, s, a);
+  } else {
+    return 1;
+  }
   *n_wg_out = n_wg;
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }
@@ -898,6 +1001,13 @@ int launch_p(const GemvArgs& a, int pro, int epi, int nu, int n_wg, size_t lds, 
       if (epi == EPI_STORE) return launch_u<FMT, PRO_RMSNORM, EPI_STORE>(a, nu, n_wg, lds, s);
       if (epi == EPI_SILU) return launch_u<FMT, PRO_RMSNORM, EPI_SILU>(a, nu, n_wg, lds, s);
       return 1;
+    case PRO_NORMROT:
+      if (epi == EPI_STORE) return launch_u<FMT, PRO_NORMROT, EPI_STORE>(a, nu, n_wg, lds, s);
+      if (epi == EPI_SILU) return launch_u<FMT, PRO_NORMROT, EPI_SILU>(a, nu, n_wg, lds, s);
+      return 1;
+    case PRO_F32ROT:
+      if (epi == EPI_ADD) return launch_u<FMT, PRO_F32ROT, EPI_ADD>(a, nu, n_wg, lds, s);
+      return 1;
   }
   return 1;
 }
@@ -931,8 +1041,17 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   if (a.K % el != 0) return 1;
   a.P = a.K / el;
   int n_wg, rows_total;
+  const bool rot = pro == PRO_NORMROT || pro == PRO_F32ROT;
+  if (rot) {   // folded prologue: whole fold chunks, K <= ROT_C * 4096
+    if (!a.signs || a.had_block < 2 || (a.had_block & (a.had_block - 1)) || a.K % a.had_block || a.K % 1024 ||
+        a.K > ROT_C * 4096)
+      return 1;
+    if (pro == PRO_F32ROT && a.perm_rep > 1 && a.K != a.perm_nk * a.perm_rep * 128) return 1;
+  }
   if (epi == EPI_LOGITS) {   // persistent row-streaming head + finalize
-    if (pro != PRO_RMSNORM || a.K % 1024 != 0 || a.K > NORM_CH * 4096) return 1;
+    if (a.K % 1024 != 0 || a.K > NORM_CH * 4096) return 1;
+    if (pro != PRO_RMSNORM && pro != PRO_NORMROT) return 1;
+    if (pro == PRO_RMSNORM) a.had_block = 0;
     int rc = 1;
     switch (fmt) {
       case FMT_Q2: rc = launch_head<FMT_Q2>(a, s, &n_wg); break;
@@ -953,6 +1072,7 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
     rows_total = a.rows_per_wg;
   }
   size_t lds = hh_gemv_lds(fmt, a.K, rows_total);
+  if (rot) lds += (size_t)a.K * 4 + 16;   // the rotation buffer after rowsum
   const int ni = (rows_total * a.P + NT - 1) / NT;   // units per lane
   const int nu = ni <= 1 ? 1 : ni <= 2 ? 2 : ni <= 4 ? 4 : 0;
   int rc = 1;

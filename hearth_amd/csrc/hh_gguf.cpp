@@ -77,6 +77,15 @@ bool block_of(uint32_t id, uint64_t* el, uint64_t* by) {
   return false;
 }
 
+// qwen35.rs:189-201 meta_int: any integer kind
+bool meta_int(const Meta& m, int64_t* v) {
+  switch (m.type) {
+    case GT_U8: case GT_U16: case GT_U32: case GT_U64: *v = (int64_t)m.u; return true;
+    case GT_I8: case GT_I16: case GT_I32: case GT_I64: *v = m.i; return true;
+  }
+  return false;
+}
+
 struct Reader {
   const uint8_t* p;
   size_t n, pos = 0;
@@ -275,6 +284,64 @@ int ctx_cap(uint64_t declared, uint64_t n_kv_layers, uint64_t n_kv_heads, uint64
   return (int)(declared < cap ? declared : cap);
 }
 
+// The Hadamard fold metadata of a qwen35 file (qwen35.rs:532-620), with the
+// reference loader's checks and messages: block size (0 = unfolded), version 1
+// or 2, the normalized Sylvester transform, sign vectors by width (each width a
+// multiple of the block, values +-1, the widths covering sign_values exactly),
+// a latent token_embd when inverse_weight_names lists it, and the tied-output
+// invariants (version 2, no output.weight, latent token_embd).
+int hadamard_meta(const hh_gguf* g, hh_model_config* c, std::vector<std::pair<int, std::vector<float>>>* signs) {
+  uint32_t hb = 0, ver = 0;
+  g->u32("prism.hadamard.block_size", &hb);
+  g->u32("prism.hadamard.version", &ver);
+  const Meta* tied_m = g->find("prism.hadamard.tied_output");
+  const bool tied = tied_m && tied_m->type == GT_BOOL && tied_m->u != 0;
+  bool latent = false;
+  c->had_block = 0;
+  c->had_flags = 0;
+  if (hb > 0) {
+    if (ver != 1 && ver != 2)
+      return hh_set_error(HH_ERR_INVALID, "qwen35: unsupported prism.hadamard.version " + std::to_string(ver));
+    std::string tr;
+    g->str("prism.hadamard.transform", &tr);
+    if (tr != "normalized-sylvester-walsh-hadamard")
+      return hh_set_error(HH_ERR_INVALID, "qwen35: unsupported hadamard transform " + tr);
+    const Meta* wm = g->find("prism.hadamard.sign_widths");
+    if (!wm || wm->type != GT_ARRAY) return hh_set_error(HH_ERR_INVALID, "qwen35: missing prism.hadamard.sign_widths");
+    const Meta* vm = g->find("prism.hadamard.sign_values");
+    if (!vm || vm->type != GT_ARRAY) return hh_set_error(HH_ERR_INVALID, "qwen35: missing prism.hadamard.sign_values");
+    size_t off = 0;
+    for (const Meta& w : wm->items) {
+      int64_t width = 0;
+      if (!meta_int(w, &width)) return hh_set_error(HH_ERR_INVALID, "qwen35: bad sign width");
+      if (width <= 0 || width % hb || off + (size_t)width > vm->items.size())
+        return hh_set_error(HH_ERR_INVALID, "qwen35: invalid hadamard sign width " + std::to_string(width));
+      std::vector<float> v((size_t)width);
+      for (int64_t k = 0; k < width; ++k) {
+        int64_t x = 0;
+        meta_int(vm->items[off + (size_t)k], &x);
+        if (x != 1 && x != -1) return hh_set_error(HH_ERR_INVALID, "qwen35: hadamard sign values must be +/-1");
+        v[(size_t)k] = (float)x;
+      }
+      off += (size_t)width;
+      signs->push_back({(int)width, std::move(v)});
+    }
+    if (off != vm->items.size()) return hh_set_error(HH_ERR_INVALID, "qwen35: hadamard sign_values length mismatch");
+    const Meta* inv = g->find("prism.hadamard.inverse_weight_names");
+    if (inv && inv->type == GT_ARRAY)
+      for (const Meta& n : inv->items) latent = latent || (n.type == GT_STRING && n.s == "token_embd.weight");
+  }
+  if (tied) {
+    if (ver != 2 || hb == 0) return hh_set_error(HH_ERR_INVALID, "qwen35: tied output requires prism.hadamard version 2");
+    if (g->tensor("output.weight"))
+      return hh_set_error(HH_ERR_INVALID, "qwen35: prism.hadamard.tied_output requires output.weight to be absent");
+    if (!latent) return hh_set_error(HH_ERR_INVALID, "qwen35: prism.hadamard.tied_output requires a latent token_embd");
+  }
+  c->had_block = (int)hb;
+  c->had_flags = (latent ? HH_HAD_LATENT_EMBD : 0) | (tied ? HH_HAD_TIED_OUTPUT : 0);
+  return HH_OK;
+}
+
 int model_config(const hh_gguf* g, int cap_override, hh_model_config* c) {
   std::string arch;
   if (!g->str("general.architecture", &arch)) return hh_set_error(HH_ERR_INVALID, "Missing general.architecture");
@@ -357,10 +424,9 @@ int model_config(const hh_gguf* g, int cap_override, hh_model_config* c) {
     c->ssm_n_v_heads = (int)rank;
     c->ssm_conv_kernel = (int)kernel;
     c->attn_out_gate = 1;
-    uint32_t hb = 0;
-    if (g->u32("prism.hadamard.block_size", &hb) && hb != 0)
-      return hh_set_error(HH_ERR_DTYPE, "qwen35: Hadamard-rotated models (prism.hadamard.*) are not on the "
-                                        "decode path");
+    std::vector<std::pair<int, std::vector<float>>> signs;
+    int rc = hadamard_meta(g, c, &signs);
+    if (rc != HH_OK) return rc;
     for (int i = 0; i < c->n_layers; ++i)
       if ((i + 1) % c->full_attn_interval == 0) {
         c->qk_norm = g->tensor("blk." + std::to_string(i) + ".attn_q_norm.weight") != nullptr;
@@ -504,6 +570,19 @@ int hh_model_load_gguf(hh_ctx* ctx, const char* path, int ctx_cap_override, hh_m
   hh_model* m = nullptr;
   rc = hh_model_create(ctx, &cfg, &m);
   if (rc != HH_OK) return rc;
+  if (cfg.had_block > 0) {
+    std::vector<std::pair<int, std::vector<float>>> signs;
+    hh_model_config tmp = cfg;
+    hadamard_meta(g, &tmp, &signs);
+    for (auto& sv : signs) {
+      rc = hh_model_set_hadamard_signs(m, sv.first, sv.second.data());
+      if (rc != HH_OK) {
+        std::string msg = hh_last_error();
+        hh_model_destroy(m);
+        return hh_set_error(rc, msg);
+      }
+    }
+  }
   // every tensor the model holds must come from the file (a tied LM head
   // reads token_embd, mod.rs:360-364); extra tensors in the file are ignored
   const int n = hh_model_tensor_count(m);

@@ -31,9 +31,17 @@ struct GemvArgs {
   float* part_val;
   int* part_idx;
   int* counter;
+  // Hadamard-folded prologues (PRO_NORMROT, PRO_F32ROT): the activation is
+  // rotated (signs, then the WHT per had_block chunk) before Q8_0
+  const float* signs;   // [K] +-1
+  int had_block;
+  int perm_nk, perm_rep;   // PRO_F32ROT: GDN grouped head order when perm_rep > 1 (head dim 128)
 };
 
-enum { HH_PRO_PACKED = 0, HH_PRO_RMSNORM = 1, HH_PRO_STDQ8 = 2 };
+// PRO_NORMROT: rms_norm(x, norm_w) then the fold, then Q8_0.
+// PRO_F32ROT: an f32 vector x (optionally permuted to grouped head order), the fold, then Q8_0.
+// EPI_SILU with y != null writes silu(g) * u as f32 into y instead of packed Q8_0.
+enum { HH_PRO_PACKED = 0, HH_PRO_RMSNORM = 1, HH_PRO_STDQ8 = 2, HH_PRO_NORMROT = 3, HH_PRO_F32ROT = 4 };
 enum { HH_EPI_STORE = 0, HH_EPI_ADD = 1, HH_EPI_SILU = 2, HH_EPI_LOGITS = 3 };
 
 int hh_fmt_of(int ggml_type);
@@ -74,18 +82,28 @@ int hh_kv_synth_q8_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq
                           hipStream_t s);
 
 // Batched prefill row kernels (hh_ops.hip).
-int hh_embed_rows_launch(int type, const uint8_t* table, int d, const uint32_t* toks, int S, float* H, hipStream_t s);
+// signs/had_block: a latent (folded) table's rows get R^-1 = H D after the lookup (had_block 0: none)
+int hh_embed_rows_launch(int type, const uint8_t* table, int d, const uint32_t* toks, int S, float* H,
+                         const float* signs, int had_block, hipStream_t s);
+// Fold + Q8_0 of f32 rows X[S][K] into the split layout: optional rms_norm(x, w)
+// first (w != null), optional GDN grouped head order (rep > 1), then signs and
+// the WHT per had_block chunk.
+int hh_rot_q8_rows_launch(const float* X, const float* w, float eps, int K, int S, const float* signs, int had_block,
+                          int perm_nk, int perm_rep, int8_t* xq, float* xd, hipStream_t s);
 // Row Q8_0 outputs use the GEMM's split layout: int8 xq[S][K], f32 scales xd[S][K/32].
 int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int S, int8_t* xq, float* xd,
                            hipStream_t s);
-int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, hipStream_t s);
+// yf != null: silu(g) * u rows as f32 [S][F] instead of Q8_0
+int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, float* yf, hipStream_t s);
 int hh_add_rows_launch(float* H, const float* T, int64_t n, hipStream_t s);
 int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_kv, const float* q_norm,
                          const float* k_norm, float eps, const float* rope, int rope_dim, int max_seq, int pos0, int S,
                          int gated, int kv_q8, float* k_cache, float* v_cache, float* QB, hipStream_t s);
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
                            int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
-                           const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, hipStream_t s);
+                           const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, float* yf,
+                           hipStream_t s);
+// yf != null: the merged (gated) rows as f32 [S][n_heads*hd] instead of Q8_0
 // gate: qwen35 gated attention's projection rows (gate_row floats apart), or null;
 // kv_q8: the caches hold Q8_0 rows (quantized on write, dequantized on load)
 
@@ -102,7 +120,7 @@ int hh_rmsnorm_launch(const float* x, const float* w, float eps, int64_t rows, i
 int hh_rope_launch(float* x, int n_heads, int hd, int rope_dim, const float* table, int max_seq, int pos,
                    hipStream_t s);
 int hh_embed_launch(int type, const uint8_t* table, int d, const StepState* st, float* hidden,
-                    hipStream_t s);
+                    const float* signs, int had_block, hipStream_t s);
 int hh_argmax_launch(const float* logits, int64_t n, const int* counts, float pen, int rule,
                      float* part_val, int* part_idx, int* counter, uint32_t* out, hipStream_t s);
 int hh_count_tokens_launch(const uint32_t* past, int64_t n_past, int* counts, hipStream_t s);
@@ -131,6 +149,7 @@ struct GdnArgs {
   float eps;
   uint8_t* act_out;       // packed activation of the gated-norm output (K = v_dim)
   int act_fmt;
+  float* out_f32;         // non-null: the gated-norm output as f32 [v_dim] instead (folded models)
   float* ab;              // scratch [2*n_v]
   float* qk;              // scratch [2*k_dim] conv+silu+l2norm q,k
   float* vconv;           // scratch [v_dim]
@@ -142,6 +161,7 @@ struct GdnArgs {
   float* o_rows;          // [S][v_dim] recurrence outputs
   int8_t* xq;             // [S][v_dim] gated-norm Q8_0 codes (GEMM split layout)
   float* xd;              // [S][v_dim/32] scales
+  float* y_rows;          // non-null: gated-norm rows as f32 [S][v_dim] instead of xq/xd
 };
 int hh_gdn_launch(const GdnArgs& a, hipStream_t s);
 int hh_gdn_rows_launch(const GdnArgs& a, hipStream_t s);

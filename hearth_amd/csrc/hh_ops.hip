@@ -115,11 +115,26 @@ HH_DEV float embed_value(int type, const uint8_t* __restrict__ table, int d, int
   return (float)(bit ? 1 : -1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
 }
 
+// A latent (Hadamard-folded) embedding row gets R^-1 = H D after the lookup
+// (qwen35.rs:1054-1066, hadamard_unrotate :98-110): the WHT per had_block chunk,
+// then the sign pass.  buf: d floats of LDS.
+HH_DEV void embed_row(int type, const uint8_t* __restrict__ table, int d, int tok, float* __restrict__ out,
+                      const float* __restrict__ signs, int had_block, float* buf) {
+  if (had_block <= 0) {
+    for (int i = threadIdx.x; i < d; i += 256) out[i] = embed_value(type, table, d, tok, i);
+    return;
+  }
+  for (int i = threadIdx.x; i < d; i += 256) buf[i] = embed_value(type, table, d, tok, i);
+  lds_wht<256>(buf, d, had_block);
+  for (int i = threadIdx.x; i < d; i += 256) out[i] = buf[i] * signs[i];
+}
+
 // hidden = dequantize(token_embd row), token from the step state.
 __global__ __launch_bounds__(256) void k_embed(int type, const uint8_t* __restrict__ table, int d,
-                                               const StepState* __restrict__ st, float* __restrict__ hidden) {
-  const int tok = st->token;
-  for (int i = threadIdx.x; i < d; i += 256) hidden[i] = embed_value(type, table, d, tok, i);
+                                               const StepState* __restrict__ st, float* __restrict__ hidden,
+                                               const float* __restrict__ signs, int had_block) {
+  extern __shared__ __align__(16) float ebuf[];
+  embed_row(type, table, d, st->token, hidden, signs, had_block, ebuf);
 }
 
 // ---------------------------------------------------------------------------
@@ -542,10 +557,54 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
 // by token.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_embed_rows(int type, const uint8_t* __restrict__ table, int d,
-                                                    const uint32_t* __restrict__ toks, float* __restrict__ H) {
+                                                    const uint32_t* __restrict__ toks, float* __restrict__ H,
+                                                    const float* __restrict__ signs, int had_block) {
+  extern __shared__ __align__(16) float ebuf[];
   const int s = blockIdx.x;
-  const int tok = (int)toks[s];
-  for (int i = threadIdx.x; i < d; i += 256) H[(size_t)s * d + i] = embed_value(type, table, d, tok, i);
+  embed_row(type, table, d, (int)toks[s], H + (size_t)s * d, signs, had_block, ebuf);
+}
+
+// The fold of a matmul input row (qwen35.rs:914-941) then Q8_0 into the GEMM's
+// split layout, for row s = blockIdx.x: optional rms_norm(x, w) first (the
+// k_norm_q8_rows arithmetic), optional GDN grouped head order
+// (qwen35.rs:1452-1478), signs, the WHT per had_block chunk, then per 32-block
+// the Q8_0 of the rotated values.  buf: K floats of LDS.
+__global__ __launch_bounds__(256) void k_rot_q8_rows(const float* __restrict__ X, const float* __restrict__ w,
+                                                     float eps, int K, const float* __restrict__ signs, int had_block,
+                                                     int perm_nk, int perm_rep, int8_t* __restrict__ xq,
+                                                     float* __restrict__ xd) {
+  extern __shared__ __align__(16) float rbuf[];
+  __shared__ float red16[16];
+  const int s = blockIdx.x, tid = threadIdx.x;
+  const float* x = X + (size_t)s * K;
+  float inv = 1.0f;
+  if (w) inv = 1.0f / sqrtf(block_sumsq_f4(x, K, red16) / (float)K + eps);   // ops.rs:22-23
+  for (int e = tid * 4; e < K; e += 1024) {
+    const float4 xv = *(const float4*)(x + e);
+    float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    if (w) {
+      const float4 wv = *(const float4*)(w + e);
+      v[0] = v[0] * inv * wv.x; v[1] = v[1] * inv * wv.y; v[2] = v[2] * inv * wv.z; v[3] = v[3] * inv * wv.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = perm_rep > 1 ? grouped_pos(e + i, 128, perm_nk, perm_rep) : e + i;
+      rbuf[d] = v[i] * signs[d];
+    }
+  }
+  lds_wht<256>(rbuf, K, had_block);
+  for (int e = tid * 4; e < K; e += 1024) {
+    const float4 t = *(const float4*)(rbuf + e);
+    float vv[4] = {t.x, t.y, t.z, t.w};
+    float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+    am = group_max<8>(am);
+    const float sc = q8_scale(am), rc = q8_rcp(sc);
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) word |= ((uint32_t)q8_round_r(vv[i], sc, rc) & 0xffu) << (8 * i);
+    *(uint32_t*)(xq + (size_t)s * K + e) = word;
+    if ((tid & 7) == 0) xd[(size_t)s * (K / 32) + (e >> 5)] = h2f(f2h(sc));
+  }
 }
 
 // rms_norm(x_s, w) then Q8_0 of row s = blockIdx.x into the GEMM's split
@@ -576,13 +635,17 @@ __global__ __launch_bounds__(256) void k_norm_q8_rows(const float* __restrict__ 
 // silu(g) * u of the [gate; up] rows of token s, then Q8_0 into the split
 // layout: the SILU epilogue's arithmetic (ops.rs:240-253, q8_0.rs:20-51).
 __global__ __launch_bounds__(256) void k_silu_q8_rows(const float* __restrict__ GU, int F, int8_t* __restrict__ xq,
-                                                      float* __restrict__ xd) {
+                                                      float* __restrict__ xd, float* __restrict__ yf) {
   const int s = blockIdx.x, tid = threadIdx.x;
   const float* g = GU + (size_t)s * 2 * F;
   for (int i = tid; i < F; i += 256) {   // F % 256 == 0: whole waves
     const float gv = g[i];
     const float sg = gv / (1.0f + hx_exp(-gv));
     const float h = sg * g[F + i];
+    if (yf) {   // folded model: rotated and quantized by k_rot_q8_rows
+      yf[(size_t)s * F + i] = h;
+      continue;
+    }
     const float am = group_max<32>(fabsf(h));
     const float sc = q8_scale(am);
     const int q = q8_round_r(h, sc, q8_rcp(sc));
@@ -817,7 +880,8 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restrict__ PO, const float* __restrict__ PML,
                                                             int n_heads, int n_kv, int n_chunks, int pos0, int t0,
                                                             const float* __restrict__ gate, int gate_row,
-                                                            int8_t* __restrict__ yq, float* __restrict__ yd) {
+                                                            int8_t* __restrict__ yq, float* __restrict__ yd,
+                                                            float* __restrict__ yf) {
   extern __shared__ __align__(16) float wm[];
   float* wts = wm;                         // n_chunks
   float* pw = wm + n_chunks;               // 4 x 64
@@ -874,6 +938,10 @@ __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restr
   if (gate) {   // qwen35.rs:1627-1629, as k_attn_merge
     const float g = gate[(size_t)s * gate_row + (size_t)qh * 2 * HD + HD + d];
     o = o / (1.0f + hx_exp(-g));
+  }
+  if (yf) {   // folded model: rotated and quantized by k_rot_q8_rows
+    yf[(size_t)s * n_heads * HD + qh * HD + d] = o;
+    return;
   }
   const float am = group_max<32>(fabsf(o));
   const float scq = q8_scale(am);
@@ -1110,8 +1178,11 @@ int hh_rope_launch(float* x, int n_heads, int hd, int rope_dim, const float* tab
   return ok();
 }
 
-int hh_embed_launch(int type, const uint8_t* table, int d, const StepState* st, float* hidden, hipStream_t s) {
-  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, type, table, d, st, hidden);
+int hh_embed_launch(int type, const uint8_t* table, int d, const StepState* st, float* hidden,
+                    const float* signs, int had_block, hipStream_t s) {
+  if (had_block > 0 && (d % had_block || !signs)) return 1;
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), had_block > 0 ? (size_t)d * 4 : 0, s, type, table, d, st, hidden,
+                     signs, had_block);
   return ok();
 }
 
@@ -1190,8 +1261,20 @@ int hh_kv_synth_q8_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq
   return ok();
 }
 
-int hh_embed_rows_launch(int type, const uint8_t* table, int d, const uint32_t* toks, int S, float* H, hipStream_t s) {
-  hipLaunchKernelGGL(k_embed_rows, dim3(S), dim3(256), 0, s, type, table, d, toks, H);
+int hh_embed_rows_launch(int type, const uint8_t* table, int d, const uint32_t* toks, int S, float* H,
+                         const float* signs, int had_block, hipStream_t s) {
+  if (had_block > 0 && (d % had_block || !signs)) return 1;
+  hipLaunchKernelGGL(k_embed_rows, dim3(S), dim3(256), had_block > 0 ? (size_t)d * 4 : 0, s, type, table, d, toks, H,
+                     signs, had_block);
+  return ok();
+}
+
+int hh_rot_q8_rows_launch(const float* X, const float* w, float eps, int K, int S, const float* signs, int had_block,
+                          int perm_nk, int perm_rep, int8_t* xq, float* xd, hipStream_t s) {
+  if (K % 1024 != 0 || !signs || had_block < 2 || (had_block & (had_block - 1)) || K % had_block) return 1;
+  if (perm_rep > 1 && K != perm_nk * perm_rep * 128) return 1;
+  hipLaunchKernelGGL(k_rot_q8_rows, dim3(S), dim3(256), (size_t)K * 4, s, X, w, eps, K, signs, had_block, perm_nk,
+                     perm_rep, xq, xd);
   return ok();
 }
 
@@ -1202,9 +1285,9 @@ int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int
   return ok();
 }
 
-int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, hipStream_t s) {
+int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, float* yf, hipStream_t s) {
   if (F % 256 != 0) return 1;
-  hipLaunchKernelGGL(k_silu_q8_rows, dim3(S), dim3(256), 0, s, GU, F, xq, xd);
+  hipLaunchKernelGGL(k_silu_q8_rows, dim3(S), dim3(256), 0, s, GU, F, xq, xd, yf);
   return ok();
 }
 
@@ -1235,7 +1318,8 @@ int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_
 // Attention for tokens [t0, t0 + n) of a prefill; PO/PML hold n tokens' partials.
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
                            int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
-                           const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, hipStream_t s) {
+                           const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, float* yf,
+                           hipStream_t s) {
   // tokens per split pass: 4 at head_dim 128, 1 at 256 (measured on the 8B and
   // 9B/27B shapes; more tokens per pass cost occupancy at 256)
   const int NTOK = hd == 128 ? 4 : 1;
@@ -1254,11 +1338,11 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
   if (hd == 128) {
     if (kv_q8) HH_PSPLIT_G(128, true); else HH_PSPLIT_G(128, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, gate, gate_row, yq, yd);
+                       t0, gate, gate_row, yq, yd, yf);
   } else if (hd == 256) {
     if (kv_q8) HH_PSPLIT_G(256, true); else HH_PSPLIT_G(256, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, gate, gate_row, yq, yd);
+                       t0, gate, gate_row, yq, yd, yf);
   } else {
     return 1;
   }

@@ -175,6 +175,11 @@ struct hh_model {
   uint8_t* pf_buf = nullptr;
   size_t pf_cap = 0;
   int batched_prefill = 1;
+  // Hadamard fold: one device sign vector per folded width (+1 until set), and
+  // the f32 hand-off of the matmul inputs that are rotated in the consumer's prologue
+  float* had_signs = nullptr;
+  std::vector<std::pair<int, size_t>> sign_off;   // width -> float offset in had_signs
+  float* rot_f32 = nullptr;
 };
 
 namespace {
@@ -198,7 +203,9 @@ void declare(hh_model* m) {
   };
   char b[96];
   add("token_embd.weight", c.head_type, c.vocab, d, 0.02f, 0.0f);
-  add("output.weight", c.head_type, c.vocab, d, 0.02f, 0.0f);
+  // a tied head (prism.hadamard.tied_output, qwen35.rs:597-620) has no output.weight
+  if (!(c.arch == 1 && c.had_block > 0 && (c.had_flags & HH_HAD_TIED_OUTPUT)))
+    add("output.weight", c.head_type, c.vocab, d, 0.02f, 0.0f);
   add("output_norm.weight", HH_F32, 1, d, 0.02f, 1.0f);
   int wt = c.wtype;
   for (int i = 0; i < c.n_layers; ++i) {
@@ -248,6 +255,13 @@ int gemv_rows_for(int n_rows, int P) {
 
 int enqueue_step(hh_model* m, hipStream_t s, int only_layer = -1, unsigned stages = ~0u);
 
+// Device sign vector of a folded width (all +1 until hh_model_set_hadamard_signs).
+const float* signs_of(const hh_model* m, int width) {
+  for (auto& so : m->sign_off)
+    if (so.first == width) return m->had_signs + so.second;
+  return nullptr;
+}
+
 int capture(hh_model* m) {
   hipStream_t s = m->ctx->stream;
   if (m->gexec) { hipGraphExecDestroy(m->gexec); m->gexec = nullptr; }
@@ -281,7 +295,15 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
   const hh_model_config& c = m->cfg;
   const int d = c.d_model, hd = c.head_dim, nq = c.n_heads * hd, nkv = c.n_kv_heads * hd;
   const int wf = m->wfmt;
-  if (want(0, -1)) KTRY(hh_embed_launch(c.head_type, m->token_embd->d, d, m->state, m->hidden, s));
+  // Hadamard-folded qwen35 model: every matmul input is rotated before Q8_0
+  // (qwen35.rs:881-970); producers then hand f32 vectors to the next prologue
+  const bool had = c.had_block > 0;
+  const bool latent = had && (c.had_flags & HH_HAD_LATENT_EMBD);
+  const int pro_norm = had ? HH_PRO_NORMROT : HH_PRO_RMSNORM;
+  auto fold = [&](GemvArgs& g, int width) { g.signs = signs_of(m, width); g.had_block = c.had_block; };
+  if (want(0, -1))
+    KTRY(hh_embed_launch(c.head_type, m->token_embd->d, d, m->state, m->hidden, latent ? signs_of(m, d) : nullptr,
+                         latent ? c.had_block : 0, s));
   for (int li = 0; li < c.n_layers; ++li) {
     Layer& L = m->layers[li];
     // input projection(s), RMSNorm + Q8_0 fused into the GEMV prologue
@@ -290,7 +312,8 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
     g.norm_w = L.attn_norm;
     g.eps = c.eps;
     g.y = m->proj;
-    if (want(1, li)) KTRY(hh_gemv_launch(wf, HH_PRO_RMSNORM, HH_EPI_STORE, g, s));
+    if (had) fold(g, d);
+    if (want(1, li)) KTRY(hh_gemv_launch(wf, pro_norm, HH_EPI_STORE, g, s));
     int k_out;
     if (L.gdn) {
       int kdim = c.ssm_n_k_heads * c.ssm_head_dim, vdim = c.ssm_n_v_heads * c.ssm_head_dim;
@@ -318,6 +341,7 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
       ga.ab = m->gdn_scratch;
       ga.qk = m->gdn_scratch + 256;
       ga.vconv = ga.qk + 2 * kdim;
+      if (had) ga.out_f32 = m->rot_f32;
       if (want(2, li)) KTRY(hh_gdn_launch(ga, s));
       k_out = vdim;
     } else {
@@ -347,6 +371,7 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
       aa.act_out = m->act_mid;
       aa.act_fmt = wf;
       aa.kv_q8 = c.kv_type == HH_Q8_0;
+      if (had) { aa.out_f32 = m->rot_f32; aa.act_out = nullptr; }
       if (want(2, li)) KTRY(hh_attn_launch(aa, s));
       k_out = nq;
       (void)nkv;
@@ -354,7 +379,12 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
     GemvArgs o = gemv_base(L.w_out, d, k_out, m->rows_out);
     o.act = m->act_mid;
     o.y = m->hidden;
-    if (want(3, li)) KTRY(hh_gemv_launch(wf, HH_PRO_PACKED, HH_EPI_ADD, o, s));
+    if (had) {
+      o.x = m->rot_f32;
+      fold(o, k_out);
+      if (L.gdn) { o.perm_nk = c.ssm_n_k_heads; o.perm_rep = c.ssm_n_v_heads / c.ssm_n_k_heads; }
+    }
+    if (want(3, li)) KTRY(hh_gemv_launch(wf, had ? HH_PRO_F32ROT : HH_PRO_PACKED, HH_EPI_ADD, o, s));
     GemvArgs gu = gemv_base(L.w_gu, 2 * c.d_ffn, d, m->rows_gu);
     gu.half_rows = c.d_ffn;
     gu.x = m->hidden;
@@ -363,11 +393,13 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
     gu.act_out = m->act_ffn;
     gu.act_out_fmt = wf;
     gu.act_out_k = c.d_ffn;
-    if (want(4, li)) KTRY(hh_gemv_launch(wf, HH_PRO_RMSNORM, HH_EPI_SILU, gu, s));
+    if (had) { fold(gu, d); gu.y = m->rot_f32; }
+    if (want(4, li)) KTRY(hh_gemv_launch(wf, pro_norm, HH_EPI_SILU, gu, s));
     GemvArgs dn = gemv_base(L.w_down, d, c.d_ffn, m->rows_down);
     dn.act = m->act_ffn;
     dn.y = m->hidden;
-    if (want(5, li)) KTRY(hh_gemv_launch(wf, HH_PRO_PACKED, HH_EPI_ADD, dn, s));
+    if (had) { dn.x = m->rot_f32; fold(dn, c.d_ffn); }
+    if (want(5, li)) KTRY(hh_gemv_launch(wf, had ? HH_PRO_F32ROT : HH_PRO_PACKED, HH_EPI_ADD, dn, s));
   }
   GemvArgs h = gemv_base(m->output->d, c.vocab, d, m->rows_head);
   h.x = m->hidden;
@@ -384,7 +416,8 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
   h.part_val = m->head_pv;
   h.part_idx = m->head_pi;
   h.counter = m->counters;
-  if (want(6, -1)) KTRY(hh_gemv_launch(hh_fmt_of(c.head_type), HH_PRO_RMSNORM, HH_EPI_LOGITS, h, s));
+  if (had) fold(h, d);
+  if (want(6, -1)) KTRY(hh_gemv_launch(hh_fmt_of(c.head_type), pro_norm, HH_EPI_LOGITS, h, s));
   return HH_OK;
 }
 
@@ -435,7 +468,8 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
                oPO = take((size_t)TA * c.n_kv_heads * n_chunks * G * hd * 4),
                oPML = take((size_t)TA * c.n_kv_heads * n_chunks * G * 2 * 4),
                oGQK = take(hyb ? (size_t)S * 2 * kdim * 4 : 0), oGV = take(hyb ? (size_t)S * vdim * 4 : 0),
-               oGAB = take(hyb ? (size_t)S * 2 * c.ssm_n_v_heads * 4 : 0), oGO = take(hyb ? (size_t)S * vdim * 4 : 0);
+               oGAB = take(hyb ? (size_t)S * 2 * c.ssm_n_v_heads * 4 : 0), oGO = take(hyb ? (size_t)S * vdim * 4 : 0),
+               oRot = take(c.had_block > 0 ? (size_t)S * std::max(std::max(vdim, nq), F) * 4 : 0);
   if (off > m->pf_cap) {
     if (m->pf_buf) HIP_TRY(hipFree(m->pf_buf));
     m->pf_buf = nullptr;
@@ -453,10 +487,20 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
   float* GU = (float*)(B + oGU);
   float* PO = (float*)(B + oPO);
   float* PML = (float*)(B + oPML);
-  KTRY(hh_embed_rows_launch(c.head_type, m->token_embd->d, d, toks, S, H, s));
+  // Hadamard fold (qwen35.rs:881-970): every matmul input row is rotated
+  // before Q8_0; producers write f32 rows to Rot, k_rot_q8_rows quantizes them
+  const bool had = c.had_block > 0;
+  const bool latent = had && (c.had_flags & HH_HAD_LATENT_EMBD);
+  float* Rot = had ? (float*)(B + oRot) : nullptr;
+  auto norm_rows = [&](const float* w) -> int {
+    if (had) return hh_rot_q8_rows_launch(H, w, c.eps, d, S, signs_of(m, d), c.had_block, 0, 0, Xq, Xd, s);
+    return hh_norm_q8_rows_launch(H, w, c.eps, d, S, Xq, Xd, s);
+  };
+  KTRY(hh_embed_rows_launch(c.head_type, m->token_embd->d, d, toks, S, H, latent ? signs_of(m, d) : nullptr,
+                            latent ? c.had_block : 0, s));
   for (int li = 0; li < c.n_layers; ++li) {
     Layer& L = m->layers[li];
-    KTRY(hh_norm_q8_rows_launch(H, L.attn_norm, c.eps, d, S, Xq, Xd, s));
+    KTRY(norm_rows(L.attn_norm));
     KTRY(hh_gemm_launch(m->wfmt, L.w_in, L.n_in, d, Xq, Xd, S, QKV, s));
     int k_out;
     if (L.gdn) {
@@ -486,7 +530,11 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       ga.o_rows = (float*)(B + oGO);
       ga.xq = Xq;
       ga.xd = Xd;
+      ga.y_rows = Rot;
       KTRY(hh_gdn_rows_launch(ga, s));
+      if (had)
+        KTRY(hh_rot_q8_rows_launch(Rot, nullptr, 0.0f, vdim, S, signs_of(m, vdim), c.had_block, c.ssm_n_k_heads,
+                                   c.ssm_n_v_heads / c.ssm_n_k_heads, Xq, Xd, s));
       k_out = vdim;
     } else {
       const int gated = hyb && c.attn_out_gate;
@@ -496,14 +544,17 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       for (int t0 = 0; t0 < S; t0 += TA)
         KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, c.max_seq, pos0, t0,
                                     std::min(TA, S - t0), n_chunks, PO, PML, gated ? QKV : nullptr, L.n_in, kv8,
-                                    Xq, Xd, s));
+                                    Xq, Xd, Rot, s));
+      if (had)
+        KTRY(hh_rot_q8_rows_launch(Rot, nullptr, 0.0f, nq, S, signs_of(m, nq), c.had_block, 0, 0, Xq, Xd, s));
       k_out = nq;
     }
     KTRY(hh_gemm_launch(m->wfmt, L.w_out, d, k_out, Xq, Xd, S, T, s));
     KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
-    KTRY(hh_norm_q8_rows_launch(H, L.ffn_norm, c.eps, d, S, Xq, Xd, s));
+    KTRY(norm_rows(L.ffn_norm));
     KTRY(hh_gemm_launch(m->wfmt, L.w_gu, 2 * F, d, Xq, Xd, S, GU, s));
-    KTRY(hh_silu_q8_rows_launch(GU, F, S, Xq, Xd, s));
+    KTRY(hh_silu_q8_rows_launch(GU, F, S, Xq, Xd, Rot, s));
+    if (had) KTRY(hh_rot_q8_rows_launch(Rot, nullptr, 0.0f, F, S, signs_of(m, F), c.had_block, 0, 0, Xq, Xd, s));
     KTRY(hh_gemm_launch(m->wfmt, L.w_down, d, F, Xq, Xd, S, T, s));
     KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
   }
@@ -768,6 +819,16 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
         c.ssm_head_dim != 128 || c.ssm_conv_kernel < 2 || c.ssm_conv_kernel > 8)
       return fail(HH_ERR_DIM, "unsupported qwen35 recurrent geometry");
   }
+  if (c.had_block != 0) {
+    // the fold (qwen35.rs:532-610) applies to qwen35 models; every folded
+    // width must hold whole chunks and fit the rotation prologues
+    const int nq_ = c.n_heads * c.head_dim, vd_ = c.ssm_n_v_heads * c.ssm_head_dim;
+    const int ws[4] = {c.d_model, c.d_ffn, nq_, vd_};
+    if (c.arch != 1 || c.had_block < 2 || (c.had_block & (c.had_block - 1)))
+      return fail(HH_ERR_DIM, "had_block must be a power of two on a qwen35 model");
+    for (int w : ws)
+      if (w % c.had_block || w % 1024 || w > 20480) return fail(HH_ERR_DIM, "folded width not a multiple of had_block");
+  }
   HIP_TRY(hipSetDevice(ctx->device));
   hh_model* m = new hh_model();
   // every early return below releases what was allocated so far
@@ -801,7 +862,9 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   }
   for (size_t i = 0; i < m->tensors.size(); ++i) m->tensors[i].d = m->arena + offs[i];
   m->token_embd = find(m, "token_embd.weight");
-  m->output = find(m, "output.weight");
+  m->output = m->cfg.arch == 1 && m->cfg.had_block > 0 && (m->cfg.had_flags & HH_HAD_TIED_OUTPUT)
+                  ? m->token_embd
+                  : find(m, "output.weight");
   m->output_norm = find(m, "output_norm.weight");
   // layers
   int hd = c.head_dim, nq = c.n_heads * hd, nkv = c.n_kv_heads * hd;
@@ -915,6 +978,18 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   HIP_TRY(hipMalloc(&m->attn_po, sizeof(float) * (size_t)c.n_kv_heads * m->attn_splits * G * hd));
   HIP_TRY(hipMalloc(&m->attn_pml, sizeof(float) * (size_t)c.n_kv_heads * m->attn_splits * G * 2));
   HIP_TRY(hipMalloc(&m->gdn_scratch, sizeof(float) * (size_t)(256 + 2 * kdim + vdim + 64)));
+  if (c.had_block > 0) {
+    size_t tot = 0;
+    for (int w : {c.d_model, c.d_ffn, nq, vdim}) {
+      bool seen = w <= 0;
+      for (auto& so : m->sign_off) seen = seen || so.first == w;
+      if (!seen) { m->sign_off.push_back({w, tot}); tot += (size_t)w; }
+    }
+    std::vector<float> ones(tot, 1.0f);
+    HIP_TRY(hipMalloc(&m->had_signs, sizeof(float) * tot));
+    HIP_TRY(hipMemcpy(m->had_signs, ones.data(), sizeof(float) * tot, hipMemcpyHostToDevice));
+    HIP_TRY(hipMalloc(&m->rot_f32, sizeof(float) * (size_t)std::max(std::max(nq, vdim), c.d_ffn)));
+  }
   HIP_TRY(hipMalloc(&m->counts, sizeof(int) * c.vocab));
   HIP_TRY(hipMemset(m->counts, 0, sizeof(int) * c.vocab));
   HIP_TRY(hipMalloc(&m->prompt, sizeof(uint32_t) * (c.max_seq + 8)));
@@ -945,7 +1020,7 @@ int hh_model_destroy(hh_model* m) {
   if (m->graph) hipGraphDestroy(m->graph);
   void* bufs[] = {m->arena, m->kv, m->rec, m->rope, m->hidden, m->proj, m->act_mid, m->act_ffn, m->logits,
                   m->head_pv, m->head_pi, m->counters, m->attn_po, m->attn_pml, m->gdn_scratch, m->counts,
-                  m->prompt, m->out_tokens, m->state};
+                  m->prompt, m->out_tokens, m->state, m->had_signs, m->rot_f32};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (m->ev0) hipEventDestroy(m->ev0);
@@ -954,6 +1029,18 @@ int hh_model_destroy(hh_model* m) {
   if (m->evp) hipEventDestroy(m->evp);
   if (m->pf_buf) hipFree(m->pf_buf);
   delete m;
+  return HH_OK;
+}
+
+int hh_model_set_hadamard_signs(hh_model* m, int width, const float* signs) {
+  if (!m || !signs) return fail(HH_ERR_INVALID, "null argument");
+  if (m->cfg.had_block <= 0) return fail(HH_ERR_INVALID, "model has no Hadamard fold (had_block 0)");
+  for (int i = 0; i < width; ++i)
+    if (signs[i] != 1.0f && signs[i] != -1.0f) return fail(HH_ERR_INVALID, "hadamard sign values must be +/-1");
+  float* dst = const_cast<float*>(signs_of(m, width));
+  if (!dst) return HH_OK;   // a width this model does not fold
+  HIP_TRY(hipSetDevice(m->ctx->device));
+  HIP_TRY(hipMemcpy(dst, signs, sizeof(float) * (size_t)width, hipMemcpyHostToDevice));
   return HH_OK;
 }
 

@@ -65,7 +65,7 @@ class ModelConfigC(C.Structure):
         ("wtype", C.c_int), ("head_type", C.c_int), ("qk_norm", C.c_int),
         ("full_attn_interval", C.c_int), ("ssm_n_k_heads", C.c_int), ("ssm_n_v_heads", C.c_int),
         ("ssm_head_dim", C.c_int), ("ssm_conv_kernel", C.c_int), ("attn_out_gate", C.c_int),
-        ("kv_type", C.c_int),
+        ("kv_type", C.c_int), ("had_block", C.c_int), ("had_flags", C.c_int),
     ]
 
 
@@ -94,6 +94,8 @@ class ModelConfig:
     ssm_conv_kernel: int = 4
     attn_out_gate: int = 0
     kv_type: int = 0        # 0 = f32 KV cache, 8 = Q8_0 rows
+    had_block: int = 0      # qwen35 Hadamard fold block size (0 = no fold)
+    had_flags: int = 0      # 1 = latent token_embd (R^-1 after lookup), 2 = tied output
 
     def to_c(self) -> ModelConfigC:
         return ModelConfigC(*[getattr(self, f[0]) for f in ModelConfigC._fields_])
@@ -154,6 +156,7 @@ _EXPORTS = {
     "hh_model_tensor_info": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_int),
                                         C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_size_t)]),
     "hh_model_synthesize": (C.c_int, [C.c_void_p, C.c_uint64]),
+    "hh_model_set_hadamard_signs": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p]),
     "hh_model_reset": (C.c_int, [C.c_void_p]),
     "hh_model_prefill_kv_synthetic": (C.c_int, [C.c_void_p, C.c_uint64, C.c_int]),
     "hh_model_set_cancel": (C.c_int, [C.c_void_p, C.c_int]),
@@ -426,6 +429,13 @@ class Model:
 
     def prefill_kv_synthetic(self, seed: int, n_pos: int) -> None:
         _check(self.lib.hh_model_prefill_kv_synthetic(self.h, seed, n_pos))
+
+    def set_hadamard_signs(self, width: int, signs: np.ndarray) -> None:
+        """Sign vector of one Hadamard fold width (qwen35.rs:561-586, :843-845)."""
+        s = np.ascontiguousarray(signs, dtype=np.float32)
+        if s.size != width:
+            raise ValueError("signs must hold `width` values")
+        _check(self.lib.hh_model_set_hadamard_signs(self.h, width, s.ctypes.data))
 
     def upload(self, name: str, ggml_type: int, ne0: int, ne1: int, data: np.ndarray) -> None:
         data = np.ascontiguousarray(data)

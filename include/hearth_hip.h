@@ -143,7 +143,13 @@ typedef struct {
   int kv_type;            /* HH_F32 (0): f32 cache (KVStorage::F32, the default); HH_Q8_0: Q8_0 rows
                              (KVStorage::Q8_0, kvcache.rs:41-57, written by write_kv :92-113, read
                              through the dequantized rows as attention_q8_0, ops.rs:946-1030) */
+  int had_block;          /* qwen35 Hadamard fold (prism.hadamard.block_size, qwen35.rs:532-610):
+                             0 = unfolded; else a power of two dividing every folded width */
+  int had_flags;          /* HH_HAD_LATENT_EMBD: token_embd rows get R^-1 after the lookup
+                             (inverse_weight_names holds token_embd.weight); HH_HAD_TIED_OUTPUT:
+                             no output.weight, the head is token_embd (tied_output, version 2) */
 } hh_model_config;
+enum { HH_HAD_LATENT_EMBD = 1, HH_HAD_TIED_OUTPUT = 2 };
 
 /* Allocates every weight (native GGUF block layout, uploaded once), the KV
  * cache (f32 or Q8_0 rows, [layer][kv_head][max_seq][hd], kvcache.rs:11-57), the recurrent state
@@ -161,6 +167,13 @@ int hh_model_download_tensor(hh_model* m, const char* name, void* host_bytes, si
 int hh_model_tensor_count(hh_model* m);
 int hh_model_tensor_info(hh_model* m, int index, const char** name, int* ggml_type, int64_t* ne0,
                          int64_t* ne1, size_t* nbytes);
+/* Sign vector of one fold width (prism.hadamard.sign_widths / sign_values;
+ * the `had_signs` map of qwen35.rs:561-586, looked up by matmul width in
+ * signs_for, :843-845).  A folded width with no sign vector gets no sign pass,
+ * as signs_for() == None.  Widths the model does not fold are accepted and
+ * ignored.  Values must be +1 or -1. */
+int hh_model_set_hadamard_signs(hh_model* m, int width, const float* signs);
+
 /* Fill every tensor on the device from the seeded generator (synthetic weights). */
 int hh_model_synthesize(hh_model* m, uint64_t seed);
 /* Reset KV + recurrent state (fresh session). */

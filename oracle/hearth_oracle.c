@@ -687,6 +687,38 @@ void ho_attention(const float* q, const float* k, const float* v, int seq_len, i
 }
 
 /* ------------------------------------------------------------------------- */
+/* Hadamard fold                                                             */
+/* ------------------------------------------------------------------------- */
+
+/* qwen35.rs:51-68: normalized Sylvester WHT, butterflies h = 1, 2, 4, ... with
+ * x[i] = a + b, x[i|h] = a - b for every i with bit h clear, then x *= 1/sqrt(n). */
+void ho_wht(float* x, int64_t n) {
+  const float s = 1.0f / sqrtf((float)n);
+  for (int64_t h = 1; h < n; h <<= 1)
+    for (int64_t i = 0; i < n; i++)
+      if (!(i & h)) {
+        float a = x[i], b = x[i | h];
+        x[i] = a + b;
+        x[i | h] = a - b;
+      }
+  for (int64_t i = 0; i < n; i++) x[i] *= s;
+}
+
+/* qwen35.rs:75-88: sign pass (when present), then the WHT per block. */
+void ho_hadamard_rotate(float* x, int64_t n, const float* signs, int block) {
+  if (signs)
+    for (int64_t i = 0; i < n; i++) x[i] *= signs[i];
+  for (int64_t o = 0; o + block <= n; o += block) ho_wht(x + o, block);
+}
+
+/* qwen35.rs:98-110: WHT per block first, then the sign pass. */
+void ho_hadamard_unrotate(float* x, int64_t n, const float* signs, int block) {
+  for (int64_t o = 0; o + block <= n; o += block) ho_wht(x + o, block);
+  if (signs)
+    for (int64_t i = 0; i < n; i++) x[i] *= signs[i];
+}
+
+/* ------------------------------------------------------------------------- */
 /* greedy selection                                                          */
 /* ------------------------------------------------------------------------- */
 
@@ -1067,6 +1099,10 @@ struct ho_model {
   uint8_t* q8;
   int n_threads, arm;
   int order; /* 0 = reference association order, 1 = device order */
+  /* Hadamard fold: sign vectors by width (qwen35.rs:843-845), rotation scratch */
+  int n_signs, sign_w[8];
+  float* signs[8];
+  float* rot;
 };
 
 static tensor_t* add_tensor(ho_model* m, const char* name, int type, int64_t rows, int64_t cols,
@@ -1108,7 +1144,9 @@ ho_model* ho_model_new(const ho_config* cfg) {
   m->tensors = (tensor_t*)xcalloc((size_t)(L * 24 + 8), sizeof(tensor_t));
   m->layers = (layer_t*)xcalloc((size_t)L, sizeof(layer_t));
   m->token_embd = add_tensor(m, "token_embd.weight", c->head_type, c->vocab, d, 0.02f, 0.0f);
-  m->output = add_tensor(m, "output.weight", c->head_type, c->vocab, d, 0.02f, 0.0f);
+  /* tied output (prism.hadamard.tied_output): the latent token_embd is the head */
+  m->output = (c->arch == 1 && (c->had_flags & 2)) ? m->token_embd
+                                                   : add_tensor(m, "output.weight", c->head_type, c->vocab, d, 0.02f, 0.0f);
   m->output_norm = add_tensor(m, "output_norm.weight", HO_F32, 1, d, 0.02f, 1.0f);
   int wt = c->wtype;
   int kdim = c->ssm_n_k_heads * c->ssm_head_dim, vdim = c->ssm_n_v_heads * c->ssm_head_dim;
@@ -1179,6 +1217,7 @@ ho_model* ho_model_new(const ho_config* cfg) {
   m->big = (float*)xcalloc(wide * 4, sizeof(float));
   m->scores = (float*)xcalloc((size_t)c->max_seq + 8, sizeof(float));
   m->q8 = (uint8_t*)xcalloc(wide / 32 * 34 + 64, 1);
+  m->rot = (float*)xcalloc(wide, sizeof(float));
   m->n_threads = 1;
   m->arm = 0;
   return m;
@@ -1197,6 +1236,8 @@ void ho_model_free(ho_model* m) {
   free(m->conv_state);
   free(m->hidden); free(m->normed); free(m->q); free(m->k); free(m->v); free(m->attn_out);
   free(m->gate); free(m->up); free(m->tmp); free(m->big); free(m->scores); free(m->q8);
+  free(m->rot);
+  for (int i = 0; i < m->n_signs; i++) free(m->signs[i]);
   free(m);
 }
 
@@ -1314,9 +1355,36 @@ void ho_model_set_threads(ho_model* m, int n_threads, int arm) {
 
 const float* ho_model_hidden(const ho_model* m) { return m->hidden; }
 
+static const float* signs_for(const ho_model* m, int width) {
+  for (int i = 0; i < m->n_signs; i++)
+    if (m->sign_w[i] == width) return m->signs[i];
+  return NULL;
+}
+
+int ho_model_set_signs(ho_model* m, int width, const float* signs) {
+  for (int i = 0; i < m->n_signs; i++)
+    if (m->sign_w[i] == width) { memcpy(m->signs[i], signs, sizeof(float) * (size_t)width); return 0; }
+  if (m->n_signs == 8 || width <= 0) return 1;
+  m->sign_w[m->n_signs] = width;
+  m->signs[m->n_signs] = (float*)xcalloc((size_t)width, sizeof(float));
+  memcpy(m->signs[m->n_signs], signs, sizeof(float) * (size_t)width);
+  m->n_signs++;
+  return 0;
+}
+
+/* The activation a matmul quantizes: x itself, or on a folded qwen35 model its
+ * rotation R x (qwen35.rs:914-941, `mm(.., had = true)`; every hybrid matmul
+ * input is folded). */
+static const float* fold_input(ho_model* m, const float* x, int64_t n) {
+  if (m->cfg.arch != 1 || m->cfg.had_block <= 0) return x;
+  memcpy(m->rot, x, sizeof(float) * (size_t)n);
+  ho_hadamard_rotate(m->rot, n, signs_for(m, (int)n), m->cfg.had_block);
+  return m->rot;
+}
+
 /* matmul.rs:50-378 for the quantized dtypes: quantize_act + par_dot_rows. */
 static void mm(ho_model* m, const tensor_t* w, const float* x, float* out) {
-  ho_quantize_q8_0(x, w->cols, m->q8);
+  ho_quantize_q8_0(fold_input(m, x, w->cols), w->cols, m->q8);
   ho_gemv(w->type, w->data, w->rows, w->cols, m->q8, out, m->n_threads, m->arm);
 }
 
@@ -1351,7 +1419,7 @@ static void dev_head_gemv(int type, const uint8_t* w, int64_t rows, int64_t K, c
 static void head_mm(ho_model* m, const float* x, float* logits) {
   if (!logits) return; /* a prompt token whose logits nobody reads */
   const tensor_t* w = m->output;
-  ho_quantize_q8_0(x, w->cols, m->q8);
+  ho_quantize_q8_0(fold_input(m, x, w->cols), w->cols, m->q8);
   if (m->order) dev_head_gemv(w->type, w->data, w->rows, w->cols, m->q8, logits, m->n_threads);
   else ho_gemv(w->type, w->data, w->rows, w->cols, m->q8, logits, m->n_threads, m->arm);
 }
@@ -1424,7 +1492,7 @@ static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
   return 0;
 }
 
-/* qwen35.rs:1239-1492 gdn_layer (no Hadamard fold). Writes the branch output
+/* qwen35.rs:1239-1492 gdn_layer. Writes the branch output
  * into m->attn_out[0..d). */
 static void gdn_layer(ho_model* m, int li, layer_t* ly) {
   const ho_config* c = &m->cfg;
@@ -1558,6 +1626,15 @@ static void gdn_layer(ho_model* m, int li, layer_t* ly) {
     norm_head(m, m->attn_out + h * hd, (const float*)ly->ssm_norm->data, hd, oh + h * hd);
   ho_silu(z, vdim);
   for (int i = 0; i < vdim; i++) oh[i] *= z[i];
+  if (c->had_block > 0 && nv / nk > 1) {
+    /* :1452-1478: the fold of ssm_out was computed in grouped head order
+     * [hd, rep, nk]: head h = r*nk + kg moves to slot kg*rep + r first */
+    int rep = nv / nk;
+    float* perm = m->up;
+    for (int h = 0; h < nv; h++)
+      memcpy(perm + (size_t)((h % nk) * rep + h / nk) * hd, oh + (size_t)h * hd, sizeof(float) * hd);
+    memcpy(oh, perm, sizeof(float) * vdim);
+  }
   mm(m, ly->ssm_out, oh, m->attn_out);
 }
 
@@ -1621,13 +1698,15 @@ static void attn_layer_q35(ho_model* m, int pos, layer_t* ly) {
   mm(m, ly->attn_output, m->up, m->attn_out);
 }
 
-/* qwen35.rs:1028-1236 forward (had_block_size == 0). */
+/* qwen35.rs:1028-1236 forward, with the Hadamard fold when had_block > 0. */
 static int forward_hybrid(ho_model* m, uint32_t token, int pos, float* logits) {
   const ho_config* c = &m->cfg;
   int d = c->d_model;
   if ((int64_t)token >= m->token_embd->rows || pos >= c->max_seq) return 3;
   ho_dequantize(m->token_embd->type, m->token_embd->data + ho_row_bytes(m->token_embd->type, d) * token,
                 d, m->hidden);
+  /* :1054-1066: a latent table's rows are stored folded by R; the lookup applies R^-1 */
+  if (c->had_block > 0 && (c->had_flags & 1)) ho_hadamard_unrotate(m->hidden, d, signs_for(m, d), c->had_block);
   for (int li = 0; li < c->n_layers; li++) {
     layer_t* ly = &m->layers[li];
     norm_d(m, m->hidden, (const float*)ly->attn_norm->data, d, m->normed);

@@ -65,6 +65,11 @@ void ho_softmax(float* x, int64_t n);                                           
 void ho_attention(const float* q, const float* k, const float* v, int seq_len, int head_dim,
                   float* out, float* scratch);                                    /* :353-406 */
 
+/* ---- Hadamard fold (qwen35.rs:51-118) ---- */
+void ho_wht(float* x, int64_t n);                         /* walsh_hadamard_in_place :51-68 */
+void ho_hadamard_rotate(float* x, int64_t n, const float* signs, int block);   /* :75-88  R = D.H */
+void ho_hadamard_unrotate(float* x, int64_t n, const float* signs, int block); /* :98-110 R^-1 = H.D */
+
 /* ---- greedy selection ---- */
 /* hearth-sampler lib.rs:26-40 + :156-175 (repetition penalty, then LAST max on ties) */
 uint32_t ho_sample_greedy_dense(float* logits, int64_t n, const uint32_t* past, int64_t n_past,
@@ -95,6 +100,10 @@ typedef struct {
   int ssm_n_k_heads, ssm_n_v_heads, ssm_head_dim, ssm_conv_kernel;
   int attn_out_gate;   /* full-attention layers emit [q|gate] per head */
   int kv_type;         /* HO_F32 or HO_Q8_0 (KVStorage, kvcache.rs:6-9) */
+  /* qwen35 Hadamard fold (prism.hadamard.*, qwen35.rs:532-610): block size (0 =
+   * none) and flags: 1 = token_embd is latent (R^-1 after lookup),
+   * 2 = tied output (the head is token_embd; output.weight absent) */
+  int had_block, had_flags;
 } ho_config;
 
 typedef struct ho_model ho_model;
@@ -122,6 +131,9 @@ int ho_forward(ho_model* m, uint32_t token, int pos, float* logits);
 /* Token loop: prompt token-by-token, then n_gen greedy tokens. */
 int ho_generate(ho_model* m, const uint32_t* prompt, int n_prompt, int start_pos, int n_gen,
                 float repeat_pen, uint32_t* out_tokens, float* last_logits);
+/* Sign vector of a fold width (prism.hadamard.sign_widths/_values); widths
+ * without one get no sign pass (signs_for() == None, qwen35.rs:843-845). */
+int ho_model_set_signs(ho_model* m, int width, const float* signs);
 /* Debug taps: copy of the hidden state after the last forward. */
 const float* ho_model_hidden(const ho_model* m);
 

@@ -25,7 +25,7 @@ class HoConfig(C.Structure):
         ("wtype", C.c_int), ("head_type", C.c_int), ("qk_norm", C.c_int),
         ("full_attn_interval", C.c_int), ("ssm_n_k_heads", C.c_int), ("ssm_n_v_heads", C.c_int),
         ("ssm_head_dim", C.c_int), ("ssm_conv_kernel", C.c_int), ("attn_out_gate", C.c_int),
-        ("kv_type", C.c_int),
+        ("kv_type", C.c_int), ("had_block", C.c_int), ("had_flags", C.c_int),
     ]
 
 
@@ -88,6 +88,10 @@ def load() -> C.CDLL:
         "ho_forward": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int, f32p]),
         "ho_generate": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int, C.c_int, C.c_float, u32p, f32p]),
         "ho_model_hidden": (C.c_void_p, [C.c_void_p]),
+        "ho_wht": (None, [f32p, C.c_int64]),
+        "ho_hadamard_rotate": (None, [f32p, C.c_int64, C.c_void_p, C.c_int]),
+        "ho_hadamard_unrotate": (None, [f32p, C.c_int64, C.c_void_p, C.c_int]),
+        "ho_model_set_signs": (C.c_int, [C.c_void_p, C.c_int, f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -161,6 +165,20 @@ def synth_tensor(t: int, seed: int, name: str, rows: int, cols: int, std: float,
     return out
 
 
+def wht(x: np.ndarray) -> np.ndarray:
+    y = np.array(x, dtype=np.float32)
+    load().ho_wht(_p(y), y.size)
+    return y
+
+
+def hadamard_rotate(x: np.ndarray, signs, block: int, inverse: bool = False) -> np.ndarray:
+    y = np.array(x, dtype=np.float32)
+    s = None if signs is None else np.ascontiguousarray(signs, dtype=np.float32)
+    fn = load().ho_hadamard_unrotate if inverse else load().ho_hadamard_rotate
+    fn(_p(y), y.size, None if s is None else _p(s), block)
+    return y
+
+
 def synth_token(seed: int, i: int, vocab: int) -> int:
     return load().ho_synth_token(seed, i, vocab)
 
@@ -188,6 +206,12 @@ class OracleModel:
             self.close()
         except Exception:
             pass
+
+    def set_signs(self, width: int, signs: np.ndarray) -> None:
+        s = np.ascontiguousarray(signs, dtype=np.float32)
+        assert s.size == width
+        assert self.lib.ho_model_set_signs(self.h, width, _p(s)) == 0
+        self._signs = getattr(self, "_signs", []) + [s]
 
     def set_order(self, order: int) -> None:
         self.lib.ho_model_set_order(self.h, order)

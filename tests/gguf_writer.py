@@ -92,3 +92,18 @@ def model_meta(cfg, arch=None, context_length=None, vocab_as_tokens=False):
               (f"{arch}.ssm.inner_size", U32, cfg.ssm_head_dim * cfg.ssm_n_v_heads),
               (f"{arch}.full_attention_interval", U32, cfg.full_attn_interval)]
     return m
+
+
+def hadamard_meta(block, signs, version=1, latent=False, tied=False, transform="normalized-sylvester-walsh-hadamard"):
+    """prism.hadamard.* keys (qwen35.rs:532-610): signs = {width: +-1 array}."""
+    widths = list(signs)
+    values = [int(v) for w in widths for v in signs[w]]
+    m = [("prism.hadamard.block_size", U32, block), ("prism.hadamard.version", U32, version),
+         ("prism.hadamard.transform", STRING, transform),
+         ("prism.hadamard.sign_widths", ARRAY, (U32, widths)),
+         ("prism.hadamard.sign_values", ARRAY, (I8, values))]
+    if latent:
+        m.append(("prism.hadamard.inverse_weight_names", ARRAY, (STRING, ["token_embd.weight"])))
+    if tied:
+        m.append(("prism.hadamard.tied_output", BOOL, 1))
+    return m

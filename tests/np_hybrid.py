@@ -22,6 +22,15 @@ this restatement can tell the mistake apart:
   "khead_div"         v-head h pairs with k-group h // rep instead of h % n_groups
   "rope_full"         RoPE rotates the whole head instead of the first rope_dim dims
   "no_qk_norm"        the q/k head RMSNorms are skipped
+  "no_ssm_perm"       (folded models) ssm_out's input is rotated without the
+                      grouped head permutation
+  "unrotate_as_rotate" (folded models) the latent embedding row gets R instead of R^-1
+
+Folded models (cfg.had_block > 0, qwen35.rs:51-118, :881-970): every matmul
+input x is quantized as R x = WHT_b(signs * x) (normalized Sylvester WHT per
+block, scipy.linalg.hadamard / sqrt(b)); ssm_out's input is first permuted to
+grouped head order (qwen35.rs:1452-1478); a latent embedding row gets
+R^-1 = H D (WHT, then signs); a tied head reads token_embd.
 """
 import numpy as np
 
@@ -29,8 +38,9 @@ from fixtures import np_dequant
 
 
 class NpHybrid:
-    def __init__(self, oracle_model, cfg, mutate=None):
+    def __init__(self, oracle_model, cfg, mutate=None, signs=None):
         self.m, self.c, self.mut = oracle_model, cfg, mutate
+        self.signs = signs or {}
         c = cfg
         self.hd = c.ssm_head_dim
         self.nk, self.nv = c.ssm_n_k_heads, c.ssm_n_v_heads
@@ -65,6 +75,19 @@ class NpHybrid:
     def q8(self, x):
         from oracle import oracle as orc
         return np_dequant(8, orc.quantize_q8_0(x.astype(np.float32)), x.size).astype(np.float64)
+
+    def wht(self, x):
+        import scipy.linalg
+        b = self.c.had_block
+        H = scipy.linalg.hadamard(b).astype(np.float64) / np.sqrt(b)
+        return (x.reshape(-1, b) @ H.T).reshape(-1)
+
+    def mmq(self, x):
+        """The Q8_0 activation a matmul sees: x, or R x on a folded model."""
+        if self.c.had_block:
+            sg = self.signs.get(x.size)
+            x = self.wht(x * sg if sg is not None else x)
+        return self.q8(x)
 
     @staticmethod
     def silu(z):
@@ -125,7 +148,14 @@ class NpHybrid:
             self.S[i][h] = S
         on = np.stack([self.rms(o[h], self.F(p + "ssm_norm.weight")) for h in range(nv)]).reshape(-1)
         on = on * self.silu(z)
-        return self.W(p + "ssm_out.weight", c.d_model, vdim) @ self.q8(on)
+        if self.c.had_block and nv // nk > 1 and self.mut != "no_ssm_perm":
+            rep = nv // nk
+            perm = np.zeros_like(on)
+            for h in range(nv):
+                dst = ((h % nk) * rep + h // nk) * hd
+                perm[dst:dst + hd] = on[h * hd:(h + 1) * hd]
+            on = perm
+        return self.W(p + "ssm_out.weight", c.d_model, vdim) @ self.mmq(on)
 
     def attn(self, i, x, pos):
         c, hd = self.c, self.c.head_dim
@@ -155,22 +185,30 @@ class NpHybrid:
             e = np.exp(s - s.max())
             out[h] = (e / e.sum()) @ Vc[kvh]
         out = out / (1 + np.exp(-gate))
-        return self.W(p + "attn_output.weight", c.d_model, nh * hd) @ self.q8(out.reshape(-1))
+        return self.W(p + "attn_output.weight", c.d_model, nh * hd) @ self.mmq(out.reshape(-1))
 
     def forward(self, tok, pos):
         c, d = self.c, self.c.d_model
         h = self.W("token_embd.weight", c.vocab, d, 8)[tok].copy()
+        if c.had_block and (c.had_flags & 1):
+            sg = self.signs.get(d)
+            if self.mut == "unrotate_as_rotate":
+                h = self.wht(h * sg if sg is not None else h)
+            else:
+                h = self.wht(h)
+                h = h * sg if sg is not None else h
         for i in range(c.n_layers):
             p = f"blk.{i}."
             nrm = self.rms(h, self.F(p + "attn_norm.weight"))
-            x = self.q8(nrm)
+            x = self.mmq(nrm)
             if (i + 1) % c.full_attn_interval != 0:
                 h = h + self.gdn(i, nrm, x)
             else:
                 h = h + self.attn(i, x, pos)
-            x = self.q8(self.rms(h, self.F(p + "post_attention_norm.weight")))
+            x = self.mmq(self.rms(h, self.F(p + "post_attention_norm.weight")))
             g = self.W(p + "ffn_gate.weight", c.d_ffn, d) @ x
             u = self.W(p + "ffn_up.weight", c.d_ffn, d) @ x
-            h = h + self.W(p + "ffn_down.weight", d, c.d_ffn) @ self.q8(self.silu(g) * u)
-        x = self.q8(self.rms(h, self.F("output_norm.weight")))
-        return self.W("output.weight", c.vocab, d, 8) @ x
+            h = h + self.W(p + "ffn_down.weight", d, c.d_ffn) @ self.mmq(self.silu(g) * u)
+        x = self.mmq(self.rms(h, self.F("output_norm.weight")))
+        head = "token_embd.weight" if (c.had_block and (c.had_flags & 2)) else "output.weight"
+        return self.W(head, c.vocab, d, 8) @ x

@@ -212,10 +212,39 @@ def test_config_rejects_off_path_models(tmp_path, L):
     cfg = hl.CONFIGS["8b-q2"]
     with pytest.raises(HHError, match="architecture"):
         _derive(L, _config_file(tmp_path, cfg, name="g.gguf", arch="gemma2"))
+
+
+def test_config_hadamard_fold(tmp_path, L):
+    """prism.hadamard.* (qwen35.rs:532-620): a valid fold sets had_block and the
+    latent/tied flags; each malformed variant fails with the reference's message."""
     h = hl.CONFIGS["9b-hybrid-q2"]
-    had = _config_file(tmp_path, h, name="h.gguf", extra=[("prism.hadamard.block_size", gw.U32, 1024)])
-    with pytest.raises(HHError, match="Hadamard"):
-        _derive(L, had)
+    rng = np.random.default_rng(1)
+    signs = {4096: rng.choice([-1, 1], 4096), 12288: rng.choice([-1, 1], 12288)}
+    ok = _config_file(tmp_path, h, name="h.gguf", extra=gw.hadamard_meta(1024, signs, version=2, latent=True))
+    c = _derive(L, ok)
+    assert c.had_block == 1024 and c.had_flags == 1
+    plain = _derive(L, _config_file(tmp_path, h, name="p.gguf"))
+    assert plain.had_block == 0 and plain.had_flags == 0
+    bad = [
+        (dict(version=3), "unsupported prism.hadamard.version 3"),
+        (dict(transform="dct"), "unsupported hadamard transform dct"),
+        (dict(signs={1000: np.ones(1000)}), "invalid hadamard sign width 1000"),
+        (dict(signs={1024: np.full(1024, 2)}), "sign values must be"),
+        (dict(tied=True, version=2), "requires a latent token_embd"),
+        (dict(tied=True, version=1, latent=True), "requires prism.hadamard version 2"),
+    ]
+    for i, (kw, msg) in enumerate(bad):
+        args = dict(signs=signs, version=1)
+        args.update(kw)
+        sg = args.pop("signs")
+        p = _config_file(tmp_path, h, name=f"b{i}.gguf", extra=gw.hadamard_meta(1024, sg, **args))
+        with pytest.raises(HHError, match=msg):
+            _derive(L, p)
+    # sign_values longer than the widths cover
+    meta = gw.hadamard_meta(1024, signs)
+    meta[4] = ("prism.hadamard.sign_values", gw.ARRAY, (gw.I8, list(meta[4][2][1]) + [1]))
+    with pytest.raises(HHError, match="length mismatch"):
+        _derive(L, _config_file(tmp_path, h, name="m.gguf", extra=meta))
 
 
 def _write_model(m, path, tied=False, f16_norms=False):
