@@ -13,6 +13,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <mutex>
 #include <vector>
 
 #include "../../include/hearth_hip.h"
@@ -181,6 +182,17 @@ struct hh_model {
   std::vector<std::pair<int, size_t>> sign_off;   // width -> float offset in had_signs
   float* rot_f32 = nullptr;
 };
+
+// Scratch of the allocation-free attention entry point (hh_attention_noalloc):
+// the split partials live in this file-scope device array, one copy per GPU,
+// held until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code it is a stand-in, not a device address): each device's
+// address comes from hipGetSymbolAddress at context set-up, with that device
+// current, and is kept in g_scratch_ptr.
+constexpr size_t HH_NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[HH_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];   // by device ordinal
 
 namespace {
 
@@ -574,6 +586,17 @@ int hh_ctx_create(int device_ordinal, hh_ctx** out) {
   HIP_TRY(hipGetDeviceCount(&n));
   if (device_ordinal < 0 || device_ordinal >= n) return fail(HH_ERR_INVALID, "no such device");
   HIP_TRY(hipSetDevice(device_ordinal));
+  if (device_ordinal >= 64) return fail(HH_ERR_INVALID, "device ordinal beyond 63");
+  {
+    // once per device, with the device current: the device address of `scratch`
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device_ordinal]) {
+      void* p = nullptr;
+      hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) return fail(HH_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      g_scratch_ptr[device_ordinal] = p;
+    }
+  }
   hh_ctx* c = new hh_ctx();
   c->device = device_ordinal;
   HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
@@ -770,6 +793,45 @@ int hh_attention(hh_ctx* c, const float* q, const float* k, const float* v, int 
   a.part_o = po;
   a.part_ml = pml;
   a.counters = cnt;
+  a.out_f32 = out;
+  int rc = hh_attn_launch(a, c->stream);
+  if (rc) return fail(HH_ERR_HIP, std::string("attention launch: ") + hipGetErrorString(hipGetLastError()));
+  return HH_OK;
+}
+
+int hh_attention_noalloc(hh_ctx* c, const float* q, const float* k, const float* v, int n_heads, int n_kv, int hd,
+                         int max_seq, int seq_len, float* out) {
+  if (!c || !q || !k || !v || !out) return fail(HH_ERR_INVALID, "null argument");
+  if (n_kv <= 0 || n_heads % n_kv || (hd != 128 && hd != 256))
+    return fail(HH_ERR_DIM, "unsupported attention geometry (head_dim 128 or 256)");
+  if (seq_len <= 0 || seq_len > max_seq) return fail(HH_ERR_RANGE, "seq_len out of range");
+  const int G = n_heads / n_kv;
+  if (G > 16) return fail(HH_ERR_DIM, "too many query heads per kv head");
+  const int chunk = 8192 / hd;
+  const int splits = (seq_len + chunk - 1) / chunk;
+  const size_t need = sizeof(float) * (size_t)n_kv * splits * G * (hd + 2);
+  if (need > HH_NOALLOC_SCRATCH_BYTES)
+    return fail(HH_ERR_RANGE, "attention partials need " + std::to_string(need) +
+                                  " bytes, beyond the 4 MiB scratch of hh_attention_noalloc");
+  void* base = g_scratch_ptr[c->device];
+  if (!base) return fail(HH_ERR_INVALID, "scratch not set up for this device");
+  // every partial that the merge reads is written by the split pass of the
+  // same call, so nothing needs clearing between calls
+  float* po = (float*)base;
+  float* pml = po + (size_t)n_kv * splits * G * hd;
+  AttnArgs a{};
+  a.qkv = q;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv;
+  a.hd = hd;
+  a.k_cache = const_cast<float*>(k);
+  a.v_cache = const_cast<float*>(v);
+  a.max_seq = max_seq;
+  a.fixed_seq = seq_len;
+  a.chunk = chunk;
+  a.max_splits = splits;
+  a.part_o = po;
+  a.part_ml = pml;
   a.out_f32 = out;
   int rc = hh_attn_launch(a, c->stream);
   if (rc) return fail(HH_ERR_HIP, std::string("attention launch: ") + hipGetErrorString(hipGetLastError()));

@@ -145,6 +145,8 @@ _EXPORTS = {
     "hh_rope": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int]),
     "hh_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                 C.c_int, C.c_int, C.c_void_p]),
+    "hh_attention_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                C.c_int, C.c_int, C.c_void_p]),
     "hh_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_float, C.c_int,
                              C.c_void_p]),
     "hh_model_create": (C.c_int, [C.c_void_p, C.POINTER(ModelConfigC), C.POINTER(C.c_void_p)]),
@@ -290,6 +292,11 @@ class Ctx:
     def attention(self, q, k, v, n_heads, n_kv, head_dim, max_seq, seq_len, out) -> None:
         _check(self.lib.hh_attention(self.h, _ptr(q), _ptr(k), _ptr(v), n_heads, n_kv, head_dim, max_seq,
                                      seq_len, _ptr(out)))
+
+    def attention_noalloc(self, q, k, v, n_heads, n_kv, head_dim, max_seq, seq_len, out) -> None:
+        """hh_attention with the partials in the library's fixed per-GPU scratch (no allocation)."""
+        _check(self.lib.hh_attention_noalloc(self.h, _ptr(q), _ptr(k), _ptr(v), n_heads, n_kv, head_dim, max_seq,
+                                             seq_len, _ptr(out)))
 
     def argmax(self, logits, n: int, past, n_past: int, pen: float, rule: int, out) -> None:
         _check(self.lib.hh_argmax(self.h, _ptr(logits), n, _ptr(past), n_past, pen, rule, _ptr(out)))

@@ -120,6 +120,18 @@ int hh_rope(hh_ctx* ctx, float* x, int n_heads, int head_dim, int rope_dim, cons
 int hh_attention(hh_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
                  int n_heads, int n_kv_heads, int head_dim, int max_seq, int seq_len, float* out);
 
+/* hh_attention without any allocation: no counterpart in the reference.  For
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  Same arguments, kernels
+ * and results as hh_attention, but the split partials live in a fixed
+ * per-GPU device array of 4 MiB (n_kv * ceil(seq_len / (8192 / head_dim)) *
+ * (n_heads / n_kv) * (head_dim + 2) floats at most; larger calls fail with
+ * HH_ERR_RANGE).  Every call on one GPU shares that array: calls that overlap
+ * in time on the same GPU (any context or stream) race.  Each call writes every
+ * partial it reads, so the array's previous contents do not matter. */
+int hh_attention_noalloc(hh_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
+                         int n_heads, int n_kv_heads, int head_dim, int max_seq, int seq_len, float* out);
+
 /* Greedy selection.  rule 0 = dense sampler (hearth-sampler lib.rs:26-40 penalty
  * over past tokens, then max_by: LAST max index); rule 1 = qwen35 inline argmax
  * (qwen35.rs:1735-1745: FIRST max, no penalty).  Replaces GpuCompute::argmax_f32
