@@ -25,10 +25,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per launch of the fused gate+up GEMV from rocprofv3 FETCH_SIZE and
-# WRITE_SIZE on this kernel (x 1.9999 and x 1.0 from a 512 MiB copy's counts):
-# profiles/decode_8b_q2_hbm_traffic.txt.  Re-measure when the kernel changes.
-GATE_UP_TRAFFIC_BYTES = 27_275_000
+# HBM bytes per launch come from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+# summary (scaled by a plain copy's counts), read at run time.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_8b_q2_hbm_traffic.txt")
 METRIC = "decode tok/s @bs1, 8B Q2_0 2k ctx; Q1/Q2 GEMV HBM GB/s vs peak"
 
 
@@ -47,7 +46,27 @@ def step_bytes(cfg, seq_len: int) -> dict:
     small = row_bytes(cfg.head_type, d) + cfg.vocab * 4
     return {"weights": L * w_layer, "head": head, "kv": kv_read + kv_write, "other": norms + small,
             "total": L * w_layer + head + kv_read + kv_write + norms + small,
-            "gate_up": 2 * cfg.d_ffn * rb(d) + d * 4 * 2 + cfg.d_ffn + cfg.d_ffn // 32 * 8}
+            "gate_up": 2 * cfg.d_ffn * rb(d) + d * 4 * 2 + cfg.d_ffn + cfg.d_ffn // 32 * 8,
+            # attn_output and ffn_down: weights, packed activation in, y read + written
+            "out_proj": d * rb(nq) + nq + nq // 32 * 8 + d * 8,
+            "down": d * rb(cfg.d_ffn) + cfg.d_ffn + cfg.d_ffn // 32 * 8 + d * 8,
+            "in_proj": (nq + 2 * nkv) * rb(d) + d * 4 * 2 + (nq + 2 * nkv) * 4,
+            # one layer's attention: K and V rows read, the new row written
+            "attention": 2 * cfg.n_kv_heads * seq_len * row + 2 * cfg.n_kv_heads * row}
+
+
+def measured_traffic(kernel_prefix: str):
+    """HBM bytes per dispatch of a kernel from the committed counter summary
+    (the 'traffic MB' column), or None when the summary has no such row."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                if ln.startswith(kernel_prefix):
+                    cols = ln[len(kernel_prefix):].split()
+                    return int(float(cols[-3]) * 1e6)
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
 
 
 def cpu_baseline(model, cfg, seed, kv_seed, tok0, budget_s: float):
@@ -276,6 +295,13 @@ def main():
     print(f"[bench] stage ms (layer 0): {json.dumps(stage)}", file=sys.stderr, flush=True)
     gu_ms = stage["gate_up"]
     gu_gbs = b["gate_up"] / (gu_ms * 1e-3) / 1e9
+    # the kernel with the largest share of a step (rocprof ranks the
+    # packed-input GEMV first: it runs twice per layer, attn_output and ffn_down)
+    od_ms = stage["out_proj"] + stage["down"]
+    od_bytes = b["out_proj"] + b["down"]
+    od_gbs = od_bytes / (od_ms * 1e-3) / 1e9
+    od_traffic = measured_traffic("void k_gemv<2, 0, 1, 1>(GemvArgs)")
+    gu_traffic = measured_traffic("void k_gemv<2, 1, 2, 2>(GemvArgs)")
     step_gbs = b["total"] * tps / 1e9
     out = {
         "metric": METRIC,
@@ -296,10 +322,23 @@ def main():
                    "bytes_per_step": b["total"], "parallelism": "single GPU"},
         "step_hbm": {"achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(step_gbs / PEAK_HBM_GBS, 4)},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv<Q2,RMSNORM,SILU> (fused gate+up, layer 0)",
-                     "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
-                     "avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": b["gate_up"]},
+        "roofline": {"bound": "hbm",
+                     "kernel": "k_gemv<Q2,PACKED,ADD> (attn_output + ffn_down, layer 0; largest share of a step)",
+                     "achieved": round(od_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(od_gbs / PEAK_HBM_GBS, 4),
+                     "traffic": None if od_traffic is None else od_traffic,
+                     "traffic_note": "mean HBM bytes per dispatch of the two launches (rocprofv3 FETCH/WRITE, "
+                                     "profiles/decode_8b_q2_hbm_traffic.txt)",
+                     "avg_launch_ms": round(od_ms / 2, 5), "bytes_per_launch": od_bytes // 2},
+        "roofline_gate_up": {"bound": "hbm", "kernel": "k_gemv<Q2,RMSNORM,SILU> (fused gate+up, layer 0)",
+                             "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": gu_traffic,
+                             "avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": b["gate_up"]},
+        "roofline_attention": {"bound": "hbm", "kernel": "k_attn_split + k_attn_merge (layer 0)",
+                               "achieved": round(b["attention"] / (stage["mix"] * 1e-3) / 1e9, 1),
+                               "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                               "frac": round(b["attention"] / (stage["mix"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                               "avg_stage_ms": round(stage["mix"], 5)},
         "stage_ms": {k: round(v, 5) for k, v in stage.items()},
         "first_tokens": [int(t) for t in toks[:8]],
     }
