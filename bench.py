@@ -225,10 +225,26 @@ def hybrid_leg(ctx, n_prompt: int, K: int, W: int) -> dict:
     m.close()
     print(f"[bench] 9B hybrid: prefill {n_prompt} tokens {pf_ms:.1f} ms ({n_prompt / (pf_ms * 1e-3):.0f} tok/s), "
           f"decode {dec_ms:.4f} ms/step ({1000.0 / dec_ms:.1f} tok/s)", file=sys.stderr, flush=True)
+    # the same prompt through the chunked GDN recurrence (HH_GDN_CHUNKED=1):
+    # fp32-rounding parity with the sequential rule, which stays the default
+    os.environ["HH_GDN_CHUNKED"] = "1"
+    try:
+        mc = Model(ctx, cfg)
+    finally:
+        os.environ.pop("HH_GDN_CHUNKED", None)
+    mc.synthesize(2027)
+    mc.generate(prompt[:64], 2, repeat_pen=1.0)
+    mc.reset()
+    mc.generate(prompt, 2, repeat_pen=1.0)
+    pfc_ms = mc.last_prefill_ms()
+    mc.close()
+    print(f"[bench] 9B hybrid, chunked GDN prefill: {n_prompt} tokens {pfc_ms:.1f} ms", file=sys.stderr, flush=True)
     return {"model": "9B-shaped qwen35 hybrid Q2_0 (32 layers, full attention every 4th)",
             "prefill_tokens": n_prompt, "prefill_ms": round(pf_ms, 2),
             "prefill_tok_per_s": round(n_prompt / (pf_ms * 1e-3), 1),
             "decode_tok_per_s": round(1000.0 / dec_ms, 2), "decode_ms_per_step": round(dec_ms, 4),
+            "prefill_chunked_gdn_ms": round(pfc_ms, 2),
+            "prefill_chunked_gdn_tok_per_s": round(n_prompt / (pfc_ms * 1e-3), 1),
             "first_tokens": [int(t) for t in toks[:8]],
             "note": "prompt through the batched prefill (bit-identical to token-by-token decode), then decode "
                     "from the prefilled state; prefill time is the prompt phase of generate"}

@@ -14,7 +14,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = ["hh_gemv.hip", "hh_gemm.hip", "hh_ops.hip", "hh_gdn.hip", "hh_runtime.hip", "hh_gguf.cpp"]
+SOURCES = ["hh_gemv.hip", "hh_gemm.hip", "hh_ops.hip", "hh_gdn.hip", "hh_gdn_chunk.hip", "hh_runtime.hip", "hh_gguf.cpp"]
 LIB = os.path.join(HERE, "libhearth_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

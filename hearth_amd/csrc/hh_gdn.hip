@@ -405,7 +405,7 @@ int hh_gdn_launch(const GdnArgs& a, hipStream_t s) {
 // Batched prefill of one GDN layer over a.S tokens (the proj rows already hold
 // the in_proj outputs): prep per token, conv window advance, recurrence,
 // gated norm rows.
-int hh_gdn_rows_launch(const GdnArgs& a, hipStream_t s) {
+int hh_gdn_rows_launch(const GdnArgs& a, float* chunk_scratch, hipStream_t s) {
   const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
   if (conv_dim % 256 || a.hd != 128 || a.kernel > 8 || a.kernel < 2) return 1;
   if (a.d % 1024 || a.d > 8192 || a.S <= 0 || a.S > 65535) return 1;
@@ -414,8 +414,12 @@ int hh_gdn_rows_launch(const GdnArgs& a, hipStream_t s) {
   if (hipGetLastError() != hipSuccess) return 1;
   hipLaunchKernelGGL(k_gdn_conv_advance, dim3(n_conv_wg), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
-  hipLaunchKernelGGL(k_gdn_rec_rows, dim3(a.n_v * 4), dim3(256), 0, s, a);
-  if (hipGetLastError() != hipSuccess) return 1;
+  if (chunk_scratch) {   // chunked recurrence (hh_gdn_chunk.hip): fp32-rounding parity
+    if (hh_gdn_chunked_rec_launch(a, chunk_scratch, s)) return 1;
+  } else {
+    hipLaunchKernelGGL(k_gdn_rec_rows, dim3(a.n_v * 4), dim3(256), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return 1;
+  }
   hipLaunchKernelGGL(k_gdn_gated_rows, dim3((a.n_v + 3) / 4, a.S), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }

@@ -164,4 +164,8 @@ struct GdnArgs {
   float* y_rows;          // non-null: gated-norm rows as f32 [S][v_dim] instead of xq/xd
 };
 int hh_gdn_launch(const GdnArgs& a, hipStream_t s);
-int hh_gdn_rows_launch(const GdnArgs& a, hipStream_t s);
+// chunk_scratch != null: the recurrence in chunked form (hh_gdn_chunk.hip),
+// scratch of hh_gdn_chunk_scratch_bytes(n_v, S) bytes
+int hh_gdn_rows_launch(const GdnArgs& a, float* chunk_scratch, hipStream_t s);
+size_t hh_gdn_chunk_scratch_bytes(int n_v, int S);
+int hh_gdn_chunked_rec_launch(const GdnArgs& a, float* scratch, hipStream_t s);

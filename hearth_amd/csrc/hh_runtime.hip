@@ -176,6 +176,9 @@ struct hh_model {
   uint8_t* pf_buf = nullptr;
   size_t pf_cap = 0;
   int batched_prefill = 1;
+  // HH_GDN_CHUNKED=1: the batched prefill runs the GDN recurrence in chunked
+  // form (fp32-rounding parity with the sequential rule instead of bit parity)
+  int gdn_chunked = 0;
   // Hadamard fold: one device sign vector per folded width (+1 until set), and
   // the f32 hand-off of the matmul inputs that are rotated in the consumer's prologue
   float* had_signs = nullptr;
@@ -481,7 +484,8 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
                oPML = take((size_t)TA * c.n_kv_heads * n_chunks * G * 2 * 4),
                oGQK = take(hyb ? (size_t)S * 2 * kdim * 4 : 0), oGV = take(hyb ? (size_t)S * vdim * 4 : 0),
                oGAB = take(hyb ? (size_t)S * 2 * c.ssm_n_v_heads * 4 : 0), oGO = take(hyb ? (size_t)S * vdim * 4 : 0),
-               oRot = take(c.had_block > 0 ? (size_t)S * std::max(std::max(vdim, nq), F) * 4 : 0);
+               oRot = take(c.had_block > 0 ? (size_t)S * std::max(std::max(vdim, nq), F) * 4 : 0),
+               oChunk = take(hyb && m->gdn_chunked ? hh_gdn_chunk_scratch_bytes(c.ssm_n_v_heads, S) : 0);
   if (off > m->pf_cap) {
     if (m->pf_buf) HIP_TRY(hipFree(m->pf_buf));
     m->pf_buf = nullptr;
@@ -543,7 +547,7 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       ga.xq = Xq;
       ga.xd = Xd;
       ga.y_rows = Rot;
-      KTRY(hh_gdn_rows_launch(ga, s));
+      KTRY(hh_gdn_rows_launch(ga, m->gdn_chunked ? (float*)(B + oChunk) : nullptr, s));
       if (had)
         KTRY(hh_rot_q8_rows_launch(Rot, nullptr, 0.0f, vdim, S, signs_of(m, vdim), c.had_block, c.ssm_n_k_heads,
                                    c.ssm_n_v_heads / c.ssm_n_k_heads, Xq, Xd, s));
@@ -1065,6 +1069,8 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   {
     const char* e = getenv("HH_BATCHED_PREFILL");
     m->batched_prefill = (e && e[0] == '0') ? 0 : 1;
+    const char* g = getenv("HH_GDN_CHUNKED");
+    m->gdn_chunked = (g && g[0] == '1') ? 1 : 0;
   }
   HIP_TRY(hipDeviceSynchronize());
   int rc = capture(m);
@@ -1092,6 +1098,23 @@ int hh_model_destroy(hh_model* m) {
   if (m->pf_buf) hipFree(m->pf_buf);
   delete m;
   return HH_OK;
+}
+
+int hh_model_download_state(hh_model* m, int gdn_index, float* host, size_t n_floats) {
+  if (!m || !host) return fail(HH_ERR_INVALID, "null argument");
+  const hh_model_config& c = m->cfg;
+  const size_t per = (size_t)c.ssm_n_v_heads * c.ssm_head_dim * c.ssm_head_dim;
+  int gi = 0;
+  for (const Layer& L : m->layers) {
+    if (!L.gdn) continue;
+    if (gi++ != gdn_index) continue;
+    if (n_floats != per) return fail(HH_ERR_DIM, "state holds n_v * hd * hd floats");
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    HIP_TRY(hipMemcpy(host, L.gdn_state, per * sizeof(float), hipMemcpyDeviceToHost));
+    return HH_OK;
+  }
+  return fail(HH_ERR_RANGE, "no such Gated-DeltaNet layer");
 }
 
 int hh_model_set_hadamard_signs(hh_model* m, int width, const float* signs) {

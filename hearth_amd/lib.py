@@ -159,6 +159,7 @@ _EXPORTS = {
                                         C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_size_t)]),
     "hh_model_synthesize": (C.c_int, [C.c_void_p, C.c_uint64]),
     "hh_model_set_hadamard_signs": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p]),
+    "hh_model_download_state": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]),
     "hh_model_reset": (C.c_int, [C.c_void_p]),
     "hh_model_prefill_kv_synthetic": (C.c_int, [C.c_void_p, C.c_uint64, C.c_int]),
     "hh_model_set_cancel": (C.c_int, [C.c_void_p, C.c_int]),
@@ -436,6 +437,13 @@ class Model:
 
     def prefill_kv_synthetic(self, seed: int, n_pos: int) -> None:
         _check(self.lib.hh_model_prefill_kv_synthetic(self.h, seed, n_pos))
+
+    def download_state(self, gdn_index: int) -> np.ndarray:
+        """Recurrent state [n_v][hd][hd] of the gdn_index-th Gated-DeltaNet layer."""
+        c = self.cfg
+        out = np.empty((c.ssm_n_v_heads, c.ssm_head_dim, c.ssm_head_dim), np.float32)
+        _check(self.lib.hh_model_download_state(self.h, gdn_index, out.ctypes.data, out.size))
+        return out
 
     def set_hadamard_signs(self, width: int, signs: np.ndarray) -> None:
         """Sign vector of one Hadamard fold width (qwen35.rs:561-586, :843-845)."""

@@ -186,6 +186,10 @@ int hh_model_tensor_info(hh_model* m, int index, const char** name, int* ggml_ty
  * ignored.  Values must be +1 or -1. */
 int hh_model_set_hadamard_signs(hh_model* m, int width, const float* signs);
 
+/* Copy the recurrent state of the gdn_index-th Gated-DeltaNet layer to host:
+ * [n_v][hd][hd] f32 (GdnState::layer_slice, qwen35.rs:242-261). */
+int hh_model_download_state(hh_model* m, int gdn_index, float* host, size_t n_floats);
+
 /* Fill every tensor on the device from the seeded generator (synthetic weights). */
 int hh_model_synthesize(hh_model* m, uint64_t seed);
 /* Reset KV + recurrent state (fresh session). */

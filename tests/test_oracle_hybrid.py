@@ -150,3 +150,59 @@ def test_hybrid_device_order_tokens_vs_reference_order(oracle, seed):
     print(f"seed {seed}: arm spread {spread:.3g}, ambiguous steps {amb}, "
           f"AVX2-arm divergences {reference_run.avx_divergences}, divergences {div}", flush=True)
     assert len(div) <= amb
+
+
+def _delta_sequential(S, K, Q, V, g, beta):
+    """qwen35.rs:1371-1404 token by token in float64 (dot on the undecayed state)."""
+    S = S.copy()
+    out = []
+    for t in range(len(g)):
+        dot = S.T @ K[t]
+        S = S * np.exp(g[t]) + np.outer(K[t], beta[t] * (V[t] - dot))
+        out.append(S.T @ Q[t] / np.sqrt(S.shape[0]))
+    return S, np.array(out)
+
+
+def _delta_chunked(S, K, Q, V, g, beta, C):
+    """The chunked form the device's hh_gdn_chunk.hip evaluates (its header):
+    per chunk, G = cumsum g; (I + A) U = B with A[t][s] = beta_t e^{G_{t-1}-G_s} k_t.k_s;
+    o_t = e^{G_t} S^T q_t + sum_{s<=t} e^{G_t-G_s} (q_t.k_s) u_s; S' = e^{G_last} S + sum e^{G_last-G_s} k_s u_s^T."""
+    S = S.copy()
+    outs = []
+    hd = S.shape[0]
+    for c0 in range(0, len(g), C):
+        k, q, v, gg, b = K[c0:c0 + C], Q[c0:c0 + C], V[c0:c0 + C], g[c0:c0 + C], beta[c0:c0 + C]
+        n = len(gg)
+        G = np.cumsum(gg)
+        Gm1 = np.concatenate([[0.0], G[:-1]])
+        A = np.zeros((n, n))
+        for t in range(n):
+            for s in range(t):
+                A[t, s] = b[t] * np.exp(Gm1[t] - G[s]) * (k[t] @ k[s])
+        B = b[:, None] * (v - np.exp(Gm1)[:, None] * (k @ S))
+        U = np.linalg.solve(np.eye(n) + A, B)
+        M = np.tril(np.exp(G[:, None] - G[None, :]) * (q @ k.T))
+        outs.append((np.exp(G)[:, None] * (q @ S) + M @ U) / np.sqrt(hd))
+        S = np.exp(G[-1]) * S + (k * np.exp(G[-1] - G)[:, None]).T @ U
+    return S, np.concatenate(outs)
+
+
+@pytest.mark.parametrize("n_tok", [1, 63, 64, 150])
+def test_chunked_delta_rule_equals_sequential(n_tok):
+    """The chunked restatement of the delta rule (the algebra of the device's
+    optional chunked prefill) equals the token-by-token rule in float64, from a
+    nonzero state, across chunk boundaries and a ragged last chunk."""
+    rng = np.random.default_rng(n_tok)
+    hd = 32
+    unit = lambda x: x / np.linalg.norm(x, axis=1, keepdims=True)
+    K, Q = unit(rng.standard_normal((n_tok, hd))), unit(rng.standard_normal((n_tok, hd)))
+    V = rng.standard_normal((n_tok, hd))
+    g = -np.log1p(np.exp(rng.standard_normal(n_tok)))        # softplus(.) * (-1)
+    beta = 1 / (1 + np.exp(-rng.standard_normal(n_tok)))
+    S0 = rng.standard_normal((hd, hd)) * 0.1
+    Ss, Os = _delta_sequential(S0, K, Q, V, g, beta)
+    Sc, Oc = _delta_chunked(S0, K, Q, V, g, beta, 64)
+    assert np.abs(Sc - Ss).max() < 1e-10 and np.abs(Oc - Os).max() < 1e-10
+    # dropping the decay from the dot term (a plausible slip) is visible
+    Sb, _ = _delta_chunked(S0, K, Q, V, np.zeros_like(g), beta, 64)
+    assert n_tok == 1 or np.abs(Sb - Ss).max() > 1e-3
