@@ -24,34 +24,26 @@ namespace {
 
 HH_DEV float softplus_f(float x) { return x > 20.0f ? x : hx_log(1.0f + hx_exp(x)); }
 
-// ROWS = false: the decode step (one token; the conv window comes from
-// conv_state, which is advanced).  ROWS = true: token s = blockIdx.y of a
-// batched prefill; the window's earlier inputs come from the projection rows
-// of tokens s-1, s-2, ... and, before the first token, from conv_state, which
-// k_gdn_conv_advance moves on afterwards.
-template <bool ROWS>
-__global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
+// Token s = blockIdx.y of a batched prefill: conv + silu + L2 norm of every
+// channel, and g / beta per v-head.  The window's earlier inputs come from the
+// projection rows of tokens s-1, s-2, ... and, before the first token, from
+// conv buffer pos0 & 1, which k_gdn_conv_advance moves on afterwards.
+__global__ __launch_bounds__(256) void k_gdn_prep_rows(GdnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
   const int n_conv_wg = conv_dim / 256;
-  const int s = ROWS ? (int)blockIdx.y : 0;
+  const int s = blockIdx.y;
   __shared__ float red[16];
   if ((int)blockIdx.x < n_conv_wg) {
     const int ch = blockIdx.x * 256 + tid;
     const int K = a.kernel;
     float win[8];
-    float* cs = a.conv_state + (size_t)ch * (K - 1);
-    if constexpr (ROWS) {
-      for (int t = 0; t < K - 1; ++t) {
-        const int u = s - (K - 1) + t;   // token of window slot t
-        win[t] = u >= 0 ? a.proj[(size_t)u * a.row_in + ch] : cs[s + t];
-      }
-      win[K - 1] = a.proj[(size_t)s * a.row_in + ch];
-    } else {
-      for (int t = 0; t < K - 1; ++t) win[t] = cs[t];
-      win[K - 1] = a.proj[ch];
-      for (int t = 0; t < K - 1; ++t) cs[t] = win[t + 1];
+    const float* cs = a.conv_state + (size_t)(a.pos0 & 1) * conv_dim * (K - 1) + (size_t)ch * (K - 1);
+    for (int t = 0; t < K - 1; ++t) {
+      const int u = s - (K - 1) + t;   // token of window slot t
+      win[t] = u >= 0 ? a.proj[(size_t)u * a.row_in + ch] : cs[s + t];
     }
+    win[K - 1] = a.proj[(size_t)s * a.row_in + ch];
     const float* w = a.conv_w + (size_t)ch * K;
     float acc = 0.0f;
     for (int t = 0; t < K; ++t) acc += w[t] * win[t];
@@ -73,9 +65,9 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   // alpha/beta of v-head h = blockIdx.x - n_conv_wg (matvec_dense :1015-1025 on
   // rms_norm(hidden, attn_norm)).  Lane t holds the float4s at 4(t + 256j) +
   // 4096c (the block_sumsq_f4 slots) of hidden, attn_norm and both weight rows,
-  // all loaded at once.  Order: lane t sums its normalized products in (c, j,
-  // element) order, each wave adds its lanes by butterfly, then
-  // (W0 + W1) + (W2 + W3).
+  // all loaded at once.  Order (the input projection's, k_gemv's alpha/beta
+  // epilogue): slot t + 256j sums its products over c, then element, ascending;
+  // the 64 slots of each (wave, j) by butterfly into W[wave + 4j]; tree16(W).
   const int d = a.d;
   const int h = (int)blockIdx.x - n_conv_wg;
   const float* wa = a.w_alpha + (size_t)h * d;
@@ -113,11 +105,13 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
   }
   __syncthreads();
   const float inv = 1.0f / sqrtf(tree16(red) / (float)d + a.eps);
-  float sa = 0.0f, sb = 0.0f;
+  float sa[4], sb[4];
 #pragma unroll
-  for (int c = 0; c < NC; ++c)
+  for (int j = 0; j < 4; ++j) {
+    sa[j] = 0.0f;
+    sb[j] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int c = 0; c < NC; ++c) {
       if (4 * (tid + 256 * j) + 4096 * c >= d) continue;
       const float x[4] = {hx[j][c].x * inv * hw[j][c].x, hx[j][c].y * inv * hw[j][c].y,
                           hx[j][c].z * inv * hw[j][c].z, hx[j][c].w * inv * hw[j][c].w};
@@ -125,51 +119,93 @@ __global__ __launch_bounds__(256) void k_gdn_prep(GdnArgs a) {
       const float ub[4] = {vb[j][c].x, vb[j][c].y, vb[j][c].z, vb[j][c].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sa = sa + ua[i] * x[i];
-        sb = sb + ub[i] * x[i];
+        sa[j] = sa[j] + ua[i] * x[i];
+        sb[j] = sb[j] + ub[i] * x[i];
       }
     }
-  sa = wave_sum(sa);
-  sb = wave_sum(sb);
+  }
+  __shared__ float redb[16];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sa[j] = wave_sum(sa[j]);
+    sb[j] = wave_sum(sb[j]);
+  }
   __syncthreads();   // red reused
   if (lane == 0) {
-    red[wid] = sa;
-    red[4 + wid] = sb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      red[wid + 4 * j] = sa[j];
+      redb[wid + 4 * j] = sb[j];
+    }
   }
   __syncthreads();
   if (tid == 0) {
-    const float A = (red[0] + red[1]) + (red[2] + red[3]);
-    const float B = (red[4] + red[5]) + (red[6] + red[7]);
+    const float A = tree16(red);
+    const float B = tree16(redb);
     a.ab[(size_t)s * 2 * a.n_v + h] = softplus_f(A + a.dt_bias[h]) * a.ssm_a[h];
     a.ab[(size_t)s * 2 * a.n_v + a.n_v + h] = 1.0f / (1.0f + hx_exp(-B));
   }
 }
 
-// One 1024-lane workgroup per v-head h.  Lane = (column slice jb, row chunk
-// ic, column jj): column j = 32 jb + jj, rows 16 ic .. 16 ic + 15.  The
-// column dots sum the 8 row-chunk partials in chunk order.  The gated norm of
-// the head's 128 outputs then runs in wave 0 from LDS.
-__global__ __launch_bounds__(1024) void k_gdn_rec(GdnArgs a) {
-  const int tid = threadIdx.x;
+// The decode step of one GDN layer: one 1024-lane workgroup per v-head h.
+// Lanes 0..383 first run the causal conv + silu of the head's channels (the
+// q and k channels of its k-group, then its own v channels; window from conv
+// buffer pos & 1, the shifted window written to buffer (pos + 1) & 1 by the
+// channel's owner: k-group channels by head h < n_k, v channels by h) and the
+// L2 norms of q and k (two wave sums per 128-channel head, as k_gdn_prep_rows).
+// g and beta come from the input projection's raw alpha / beta dots.  Then
+// lane = (column slice jb, row chunk ic, column jj): column j = 32 jb + jj,
+// rows 16 ic .. 16 ic + 15.  The column dots sum the 8 row-chunk partials in
+// chunk order.  The gated norm of the head's 128 outputs runs in wave 0 from LDS.
+__global__ __launch_bounds__(1024) void k_gdn_step(GdnArgs a) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   constexpr int hd = 128;
   const int h = blockIdx.x;
   const int jj = tid & 31, ic = (tid >> 5) & 7, jb = tid >> 8;
   const int j = jb * 32 + jj;
   const int kg = h % a.n_k;
-  const int kdim = a.n_k * hd;
-  const float* qn = a.qk + (size_t)kg * hd;
-  const float* kn = a.qk + kdim + (size_t)kg * hd;
+  const int kdim = a.n_k * hd, conv_dim = 2 * kdim + a.n_v * hd, K = a.kernel;
   float* S = a.state + (size_t)h * hd * hd;
   __shared__ float part[4][8][33];
   __shared__ float kv_s[2][hd];
+  __shared__ float v_s[hd];
   __shared__ float o_s[hd];
+  __shared__ float red[4];
   float sreg[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) sreg[r] = S[(size_t)(ic * 16 + r) * hd + j];
-  const float vj = a.vconv[(size_t)h * hd + j];
-  const float decay = hx_exp(a.ab[h]);
-  const float b = a.ab[a.n_v + h];
-  if (tid < hd) { kv_s[0][tid] = kn[tid]; kv_s[1][tid] = qn[tid]; }
+  float y = 0.0f;
+  if (tid < 3 * hd) {   // conv + silu (qwen35.rs:1294-1303, :1820-1829)
+    const int ch = tid < hd ? kg * hd + tid : tid < 2 * hd ? kdim + kg * hd + (tid - hd) : 2 * kdim + h * hd + (tid - 2 * hd);
+    const int pos = a.st->pos;
+    const size_t buf = (size_t)conv_dim * (K - 1);
+    const float* cs = a.conv_state + (size_t)(pos & 1) * buf + (size_t)ch * (K - 1);
+    float* cd = a.conv_state + (size_t)((pos + 1) & 1) * buf + (size_t)ch * (K - 1);
+    float win[8];
+    for (int t = 0; t < K - 1; ++t) win[t] = cs[t];
+    win[K - 1] = a.proj[ch];
+    if (tid >= 2 * hd || h < a.n_k)
+      for (int t = 0; t < K - 1; ++t) cd[t] = win[t + 1];
+    const float* w = a.conv_w + (size_t)ch * K;
+    float acc = 0.0f;
+    for (int t = 0; t < K; ++t) acc += w[t] * win[t];
+    y = acc / (1.0f + hx_exp(-acc));
+    if (tid < 2 * hd) {
+      const float ss = wave_sum(y * y);
+      if (lane == 0) red[wid] = ss;
+    } else {
+      v_s[tid - 2 * hd] = y;
+    }
+  }
+  // g = softplus(alpha + dt_bias) * ssm_a, beta = sigmoid(b) (qwen35.rs:1359-1363)
+  const float decay = hx_exp(softplus_f(a.ab_raw[h] + a.dt_bias[h]) * a.ssm_a[h]);
+  const float b = 1.0f / (1.0f + hx_exp(-a.ab_raw[a.n_v + h]));
+  __syncthreads();
+  if (tid < 2 * hd) {   // L2 norm of the q (lanes 0..127) and k (128..255) heads
+    const int hw = wid & ~1;
+    const float inv = 1.0f / sqrtf((red[hw] + red[hw + 1]) + a.eps);
+    kv_s[tid < hd ? 1 : 0][tid & (hd - 1)] = y * inv;
+  }
   // wave 0 also fetches the gate and norm weight of its two elements
   float zg[2] = {0.0f, 0.0f}, nw[2] = {0.0f, 0.0f};
   if (tid < 64) {
@@ -179,6 +215,7 @@ __global__ __launch_bounds__(1024) void k_gdn_rec(GdnArgs a) {
     nw[1] = a.ssm_norm[64 + tid];
   }
   __syncthreads();
+  const float vj = v_s[j];
   float dp = 0.0f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) dp += sreg[r] * kv_s[0][ic * 16 + r];
@@ -207,7 +244,6 @@ __global__ __launch_bounds__(1024) void k_gdn_rec(GdnArgs a) {
   __syncthreads();
   if (tid >= 64) return;
   // gated RMSNorm + Q8_0 of the head's outputs (qwen35.rs:1425-1439)
-  const int lane = tid;
   const float v0 = o_s[lane], v1 = o_s[64 + lane];
   const float ss = wave_sum(v0 * v0 + v1 * v1);
   const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
@@ -242,18 +278,20 @@ __global__ __launch_bounds__(256) void k_gdn_conv_advance(GdnArgs a) {
   const int ch = blockIdx.x * 256 + threadIdx.x;
   if (ch >= conv_dim) return;
   const int K = a.kernel, S = a.S;
-  float* cs = a.conv_state + (size_t)ch * (K - 1);
+  const size_t buf = (size_t)conv_dim * (K - 1);
+  const float* cs = a.conv_state + (size_t)(a.pos0 & 1) * buf + (size_t)ch * (K - 1);
+  float* cd = a.conv_state + (size_t)((a.pos0 + S) & 1) * buf + (size_t)ch * (K - 1);
   float nw[7];
   for (int t = 0; t < K - 1; ++t) {
     const int u = S - (K - 1) + t;
     nw[t] = u >= 0 ? a.proj[(size_t)u * a.row_in + ch] : cs[S + t];
   }
-  for (int t = 0; t < K - 1; ++t) cs[t] = nw[t];
+  for (int t = 0; t < K - 1; ++t) cd[t] = nw[t];
 }
 
 // Batched prefill recurrence.  A head's state columns evolve independently,
 // so workgroup (h, jb) owns columns 32 jb .. 32 jb + 31 of head h, 8 per wave,
-// and runs k_gdn_rec's per-token arithmetic for tokens 0 .. S-1 in order with
+// and runs k_gdn_step's per-token arithmetic for tokens 0 .. S-1 in order with
 // the state in registers: lane (column jj, row chunk ic) of a wave keeps rows
 // 16 ic .. 16 ic + 15 of column j, its column's 8 chunks in 8 adjacent lanes.
 // The column dots add the 8 chunk partials in chunk order, exactly as the
@@ -355,7 +393,7 @@ __global__ __launch_bounds__(256) void k_gdn_rec_rows(GdnArgs a) {
   for (int r = 0; r < 16; ++r) St[(size_t)(ic * 16 + r) * hd + j] = sreg[r];
 }
 
-// Gated RMSNorm + Q8_0 of o_rows (k_gdn_rec's tail per token and head), into
+// Gated RMSNorm + Q8_0 of o_rows (k_gdn_step's tail per token and head), into
 // the GEMM's split activation layout xq[S][v_dim], xd[S][v_dim/32].
 // Workgroup (s, 4 heads), one wave per head.
 __global__ __launch_bounds__(256) void k_gdn_gated_rows(GdnArgs a) {
@@ -396,9 +434,9 @@ int hh_gdn_launch(const GdnArgs& a, hipStream_t s) {
   if (conv_dim % 256 || a.hd != 128 || a.kernel > 8) return 1;
   int n_conv_wg = conv_dim / 256;
   if (a.d % 1024 || a.d > 8192) return 1;
-  hipLaunchKernelGGL(k_gdn_prep<false>, dim3(n_conv_wg + a.n_v), dim3(256), 0, s, a);
-  if (hipGetLastError() != hipSuccess) return 1;
-  hipLaunchKernelGGL(k_gdn_rec, dim3(a.n_v), dim3(1024), 0, s, a);
+  if (!a.ab_raw || !a.st || a.n_v % a.n_k) return 1;
+  (void)n_conv_wg;
+  hipLaunchKernelGGL(k_gdn_step, dim3(a.n_v), dim3(1024), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
@@ -410,7 +448,7 @@ int hh_gdn_rows_launch(const GdnArgs& a, float* chunk_scratch, hipStream_t s) {
   if (conv_dim % 256 || a.hd != 128 || a.kernel > 8 || a.kernel < 2) return 1;
   if (a.d % 1024 || a.d > 8192 || a.S <= 0 || a.S > 65535) return 1;
   const int n_conv_wg = conv_dim / 256;
-  hipLaunchKernelGGL(k_gdn_prep<true>, dim3(n_conv_wg + a.n_v, a.S), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_gdn_prep_rows, dim3(n_conv_wg + a.n_v, a.S), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
   hipLaunchKernelGGL(k_gdn_conv_advance, dim3(n_conv_wg), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;

@@ -285,7 +285,10 @@ constexpr int PK_L = NT;
 // slots 64w .. 64w+63 reduce by butterfly into W_w, the total is tree16(W).
 constexpr int NORM_CH = 2;   // K <= 8192
 constexpr int NJ = 1024 / NORM_L;
-struct NormRegs { float4 x[NJ][NORM_CH], w[NJ][NORM_CH]; };
+struct NormRegs {
+  float4 x[NJ][NORM_CH], w[NJ][NORM_CH];
+  float* nbuf = nullptr;   // non-null: the f32 normed vector is also kept here (LDS)
+};
 
 HH_DEV void norm_issue(const GemvArgs& p, NormRegs& r) {
   const int tid = threadIdx.x;
@@ -340,6 +343,7 @@ HH_DEV void norm_finish(const GemvArgs& p, const NormRegs& r, int8_t* aq, float*
       const bool in = e < K;
       float vv[4] = {r.x[j][c].x * inv * r.w[j][c].x, r.x[j][c].y * inv * r.w[j][c].y,   // ops.rs:29 (x * inv) * w
                      r.x[j][c].z * inv * r.w[j][c].z, r.x[j][c].w * inv * r.w[j][c].w};
+      if (r.nbuf && in) *(float4*)(r.nbuf + e) = make_float4(vv[0], vv[1], vv[2], vv[3]);
       float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
       am = group_max<8>(am);
       const float sc = q8_scale(am), rc = q8_rcp(sc);
@@ -459,6 +463,7 @@ constexpr int ROT_C = 5;
 template <int FMT, bool NORM> struct RotStage {
   float4 x[ROT_C], w[ROT_C];
   float* buf;   // K floats of LDS, free once the activation is staged
+  float* nbuf = nullptr;   // non-null: the unrotated f32 vector is also kept here (LDS)
   HH_DEV void issue(const GemvArgs& p) {
     const int tid = threadIdx.x;
 #pragma unroll
@@ -493,6 +498,7 @@ template <int FMT, bool NORM> struct RotStage {
           v[0] = v[0] * inv * w[c].x; v[1] = v[1] * inv * w[c].y;   // ops.rs:29 (x * inv) * w
           v[2] = v[2] * inv * w[c].z; v[3] = v[3] * inv * w[c].w;
         }
+        if (nbuf) *(float4*)(nbuf + e) = make_float4(v[0], v[1], v[2], v[3]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d = perm ? grouped_pos(e + i, 128, p.perm_nk, p.perm_rep) : e + i;
@@ -533,10 +539,13 @@ template <int FMT, bool NORM> struct RotStage {
 };
 
 template <int FMT, int PRO> struct ActStage;
-template <int FMT> struct ActStage<FMT, PRO_NORMROT> : RotStage<FMT, true> {};
+template <int FMT> struct ActStage<FMT, PRO_NORMROT> : RotStage<FMT, true> {
+  HH_DEV const float* r_nbuf() const { return this->nbuf; }
+};
 template <int FMT> struct ActStage<FMT, PRO_F32ROT> : RotStage<FMT, false> {};
 template <int FMT> struct ActStage<FMT, PRO_RMSNORM> {
   NormRegs r;
+  HH_DEV const float* r_nbuf() const { return r.nbuf; }
   HH_DEV void issue(const GemvArgs& p) { norm_issue(p, r); }
   HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT>(p, r, aq, ds, red); }
   HH_DEV void part1(const GemvArgs& p, int8_t*, float*, float* red) { norm_partial(p, r, red); }
@@ -618,6 +627,11 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   // issuing weights; they take the last units of each batch (none at all when
   // the workgroup holds fewer than NT - NORM_L units).  Products are indexed by
   // unit, so the mapping does not change any sum.
+  // GDN input projection: this workgroup's alpha/beta row (qwen35.rs:1285-1291)
+  constexpr bool AB_OK = (PRO == PRO_RMSNORM || PRO == PRO_NORMROT) && EPI == EPI_STORE;
+  const bool ab = AB_OK && p.ab_out && (int)blockIdx.x < p.ab_rows;   // uniform
+  __shared__ float abred[16];
+  float4 abw[2];
   const int lt = PRO == PRO_RMSNORM ? ((tid + NORM_L) & (NT - 1)) : tid;
   const int NI = (U + NT - 1) / NT;
   const int NB = (NI + DEPTH - 1) / DEPTH;
@@ -628,6 +642,17 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     for (int d = 0; d < DEPTH; ++d) {
       int lu = min((b * DEPTH + d) * NT + lt, U - 1);
       load_unit<FMT>(wr[d], unit_addr(lu));
+    }
+    if constexpr (AB_OK) {   // behind the first batch: waited for in the epilogue only
+      if (ab && b == 0) {
+        const int row = blockIdx.x;
+        const float* wrow = row < p.ab_n ? p.ab_wa + (size_t)row * K : p.ab_wb + (size_t)(row - p.ab_n) * K;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int e = 4 * tid + 4096 * c;
+          abw[c] = e < K ? *(const float4*)(wrow + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
     }
   };
   auto comp_batch = [&](const uint32_t (&wr)[DEPTH][DW], int b) {
@@ -646,8 +671,17 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   };
 
   ActStage<FMT, PRO> act;
-  if constexpr (PRO == PRO_NORMROT || PRO == PRO_F32ROT)   // K floats after rowsum, 16-byte aligned
-    act.buf = (float*)(((uintptr_t)(rowsum + rows_total) + 15) & ~(uintptr_t)15);
+  float* lds_tail = (float*)(((uintptr_t)(rowsum + rows_total) + 15) & ~(uintptr_t)15);   // 16-byte aligned
+  if constexpr (PRO == PRO_NORMROT || PRO == PRO_F32ROT) {   // K floats after rowsum
+    act.buf = lds_tail;
+    lds_tail += K;
+  }
+  if constexpr (AB_OK) {
+    if (ab) {
+      if constexpr (PRO == PRO_RMSNORM) act.r.nbuf = lds_tail;
+      else act.nbuf = lds_tail;
+    }
+  }
   act.issue(p);                      // activation first (in-order retirement)
   if constexpr (NU > 0 && PRO == PRO_RMSNORM) {
     // Waves 0-3 stage the activation and raise `ready`; every wave computes as
@@ -711,6 +745,30 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     for (int r = tid; r < rows_total; r += NT) {
       if constexpr (EPI == EPI_STORE) p.y[r0 + r] = rowsum[r];
       else p.y[r0 + r] = p.y[r0 + r] + rowsum[r];
+    }
+    if constexpr (AB_OK) {
+      // alpha/beta dot (matvec_dense, qwen35.rs:1015-1025) in 1024 slots: slot t
+      // sums w * x over its float4s at 4t + 4096c (c, then element, ascending);
+      // each wave's 64 slots by butterfly; the 16 wave sums by tree16
+      if (ab) {
+        const float* nb = act.r_nbuf();
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int e = 4 * tid + 4096 * c;
+          if (e < K) {
+            const float4 x = *(const float4*)(nb + e);
+            acc = acc + abw[c].x * x.x;
+            acc = acc + abw[c].y * x.y;
+            acc = acc + abw[c].z * x.z;
+            acc = acc + abw[c].w * x.w;
+          }
+        }
+        acc = wave_sum(acc);
+        if ((tid & 63) == 0) abred[tid >> 6] = acc;
+        __syncthreads();
+        if (tid == 0) p.ab_out[blockIdx.x] = tree16(abred);
+      }
     }
   } else if constexpr (EPI == EPI_SILU) {
     // ops.rs:240-253 silu then mul_elem (mod.rs:758-763), then Q8_0 (q8_0.rs:20-51)
@@ -1073,6 +1131,12 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   }
   size_t lds = hh_gemv_lds(fmt, a.K, rows_total);
   if (rot) lds += (size_t)a.K * 4 + 16;   // the rotation buffer after rowsum
+  if (a.ab_out) {   // the normed vector kept for the alpha/beta rows
+    if (epi != EPI_STORE || (pro != PRO_RMSNORM && pro != PRO_NORMROT) || a.K > 8192 || a.ab_rows > n_wg ||
+        a.ab_rows != 2 * a.ab_n)
+      return 1;
+    lds += (size_t)a.K * 4 + (rot ? 0 : 16);
+  }
   const int ni = (rows_total * a.P + NT - 1) / NT;   // units per lane
   const int nu = ni <= 1 ? 1 : ni <= 2 ? 2 : ni <= 4 ? 4 : 0;
   int rc = 1;

@@ -36,6 +36,13 @@ struct GemvArgs {
   const float* signs;   // [K] +-1
   int had_block;
   int perm_nk, perm_rep;   // PRO_F32ROT: GDN grouped head order when perm_rep > 1 (head dim 128)
+  // qwen35 GDN input projection (PRO_RMSNORM / PRO_NORMROT, EPI_STORE): workgroup
+  // b < ab_rows also writes the f32 dot of the normed (unrotated) activation with
+  // row b of [ssm_alpha (ab_n rows); ssm_beta (ab_n rows)] into ab_out[b]
+  const float* ab_wa;
+  const float* ab_wb;
+  int ab_n, ab_rows;
+  float* ab_out;
 };
 
 // PRO_NORMROT: rms_norm(x, norm_w) then the fold, then Q8_0.
@@ -162,6 +169,11 @@ struct GdnArgs {
   int8_t* xq;             // [S][v_dim] gated-norm Q8_0 codes (GEMM split layout)
   float* xd;              // [S][v_dim/32] scales
   float* y_rows;          // non-null: gated-norm rows as f32 [S][v_dim] instead of xq/xd
+  // conv windows are double-buffered: [2][conv_dim][kernel-1]; the decode step
+  // at position p reads buffer p & 1 and writes buffer (p + 1) & 1
+  const StepState* st;    // decode: position source
+  int pos0;               // batched prefill: position of token 0
+  const float* ab_raw;    // decode: [2 n_v] raw alpha / beta dots (from the input projection)
 };
 int hh_gdn_launch(const GdnArgs& a, hipStream_t s);
 // chunk_scratch != null: the recurrence in chunked form (hh_gdn_chunk.hip),

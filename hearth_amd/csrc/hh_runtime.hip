@@ -328,6 +328,13 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
     g.eps = c.eps;
     g.y = m->proj;
     if (had) fold(g, d);
+    if (L.gdn) {   // the first 2 n_v workgroups also form the raw alpha / beta dots
+      g.ab_wa = L.ssm_alpha;
+      g.ab_wb = L.ssm_beta;
+      g.ab_n = c.ssm_n_v_heads;
+      g.ab_rows = 2 * c.ssm_n_v_heads;
+      g.ab_out = m->gdn_scratch;
+    }
     if (want(1, li)) KTRY(hh_gemv_launch(wf, pro_norm, HH_EPI_STORE, g, s));
     int k_out;
     if (L.gdn) {
@@ -353,9 +360,8 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
       ga.eps = c.eps;
       ga.act_out = m->act_mid;
       ga.act_fmt = wf;
-      ga.ab = m->gdn_scratch;
-      ga.qk = m->gdn_scratch + 256;
-      ga.vconv = ga.qk + 2 * kdim;
+      ga.ab_raw = m->gdn_scratch;
+      ga.st = m->state;
       if (had) ga.out_f32 = m->rot_f32;
       if (want(2, li)) KTRY(hh_gdn_launch(ga, s));
       k_out = vdim;
@@ -541,6 +547,7 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       ga.qk = (float*)(B + oGQK);
       ga.vconv = (float*)(B + oGV);
       ga.ab = (float*)(B + oGAB);
+      ga.pos0 = pos0;
       ga.S = S;
       ga.row_in = L.n_in;
       ga.o_rows = (float*)(B + oGO);
@@ -982,7 +989,10 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   }
   size_t rec_per = 0;
   if (c.arch == 1) {
-    rec_per = (size_t)c.ssm_n_v_heads * c.ssm_head_dim * c.ssm_head_dim + (size_t)conv_dim * (c.ssm_conv_kernel - 1);
+    // recurrent state, then the conv window in two buffers (the decode step at
+    // position p reads buffer p & 1 and writes buffer (p + 1) & 1)
+    rec_per = (size_t)c.ssm_n_v_heads * c.ssm_head_dim * c.ssm_head_dim +
+              2 * (size_t)conv_dim * (c.ssm_conv_kernel - 1);
     m->rec_bytes = sizeof(float) * rec_per * (size_t)n_gdn;
     e = hipMalloc(&m->rec, m->rec_bytes);
     if (e != hipSuccess) { m->rec = nullptr; return fail(HH_ERR_OOM, "recurrent state allocation failed"); }
@@ -1043,7 +1053,8 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   HIP_TRY(hipMemset(m->counters, 0, sizeof(int) * 256));
   HIP_TRY(hipMalloc(&m->attn_po, sizeof(float) * (size_t)c.n_kv_heads * m->attn_splits * G * hd));
   HIP_TRY(hipMalloc(&m->attn_pml, sizeof(float) * (size_t)c.n_kv_heads * m->attn_splits * G * 2));
-  HIP_TRY(hipMalloc(&m->gdn_scratch, sizeof(float) * (size_t)(256 + 2 * kdim + vdim + 64)));
+  // raw alpha / beta dots of the GDN input projection, [2 n_v]
+  HIP_TRY(hipMalloc(&m->gdn_scratch, sizeof(float) * (size_t)(2 * c.ssm_n_v_heads + 64)));
   if (c.had_block > 0) {
     size_t tot = 0;
     for (int w : {c.d_model, c.d_ffn, nq, vdim}) {

@@ -908,6 +908,13 @@ static float bfly64(const float* v) {
   return a[0];
 }
 
+static float tree16f(const float* w) {
+  /* 16-way pairwise tree: ((w0 + w1) + (w2 + w3)) + ..., then the four quads pairwise */
+  float a0 = (w[0] + w[1]) + (w[2] + w[3]), a1 = (w[4] + w[5]) + (w[6] + w[7]);
+  float a2 = (w[8] + w[9]) + (w[10] + w[11]), a3 = (w[12] + w[13]) + (w[14] + w[15]);
+  return (a0 + a1) + (a2 + a3);
+}
+
 static float dev_sumsq_block(const float* x, int64_t K) {
   /* 1024 slots: slot t sums the float4s at 4t + 4096c in c order; slots
    * 64w..64w+63 butterfly into W_w; the 16 W_w add as a pairwise tree. */
@@ -923,9 +930,7 @@ static float dev_sumsq_block(const float* x, int64_t K) {
     lanes[t] = ss;
   }
   for (int k = 0; k < 16; k++) w[k] = bfly64(lanes + 64 * k);
-  float a0 = (w[0] + w[1]) + (w[2] + w[3]), a1 = (w[4] + w[5]) + (w[6] + w[7]);
-  float a2 = (w[8] + w[9]) + (w[10] + w[11]), a3 = (w[12] + w[13]) + (w[14] + w[15]);
-  return (a0 + a1) + (a2 + a3);
+  return tree16f(w);
 }
 
 static void dev_rms_norm_block(const float* x, const float* w, float eps, int64_t K, float* out) {
@@ -1509,26 +1514,23 @@ static void gdn_layer(ho_model* m, int li, layer_t* ly) {
   for (int r = 0; r < nv; r++) {
     const float* wa = (const float*)ly->ssm_alpha->data + (size_t)r * d;
     const float* wb = (const float*)ly->ssm_beta->data + (size_t)r * d;
-    if (m->order) {   /* 256 lanes: lane t sums the float4s at 4(t+256j)+4096c in (c, j, element)
-                         order; each 64-lane wave by butterfly; (W0 + W1) + (W2 + W3) */
-      float la[256], lb[256], wa4[4], wb4[4];
-      for (int t = 0; t < 256; t++) {
+    if (m->order) {   /* the input projection's epilogue: 1024 slots, slot t sums the float4s
+                         at 4t + 4096c (c, then element, ascending); slots 64w..64w+63
+                         butterfly into W_w; the 16 W_w add as a pairwise tree */
+      float la[1024], lb[1024], wa16[16], wb16[16];
+      for (int t = 0; t < 1024; t++) {
         float a = 0.0f, b = 0.0f;
-        for (int cc = 0; 4096 * cc < d; cc++)
-          for (int jj = 0; jj < 4; jj++) {
-            int e0 = 4 * (t + 256 * jj) + 4096 * cc;
-            if (e0 >= d) continue;
-            for (int i = 0; i < 4; i++) {
-              a = a + wa[e0 + i] * m->normed[e0 + i];
-              b = b + wb[e0 + i] * m->normed[e0 + i];
-            }
+        for (int e0 = 4 * t; e0 < d; e0 += 4096)
+          for (int i = 0; i < 4; i++) {
+            a = a + wa[e0 + i] * m->normed[e0 + i];
+            b = b + wb[e0 + i] * m->normed[e0 + i];
           }
         la[t] = a;
         lb[t] = b;
       }
-      for (int w = 0; w < 4; w++) { wa4[w] = bfly64(la + 64 * w); wb4[w] = bfly64(lb + 64 * w); }
-      abuf[r] = (wa4[0] + wa4[1]) + (wa4[2] + wa4[3]);
-      bbuf[r] = (wb4[0] + wb4[1]) + (wb4[2] + wb4[3]);
+      for (int w = 0; w < 16; w++) { wa16[w] = bfly64(la + 64 * w); wb16[w] = bfly64(lb + 64 * w); }
+      abuf[r] = tree16f(wa16);
+      bbuf[r] = tree16f(wb16);
       continue;
     }
     float acc = 0.0f, accb = 0.0f;
