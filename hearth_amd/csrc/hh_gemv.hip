@@ -32,7 +32,6 @@ namespace {
 enum { PRO_PACKED = 0, PRO_RMSNORM = 1, PRO_STDQ8 = 2, PRO_NORMROT = 3, PRO_F32ROT = 4 };
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
 
-constexpr uint32_t M2 = 0x03030303u;
 constexpr uint32_t M1 = 0x01010101u;
 
 HH_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
@@ -43,6 +42,13 @@ HH_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4(
 // contraction): block_acc = (((0 + s0*d0) + s1*d1) + s2*d2) + s3*d3.  The row
 // sum then adds the products in block order, so a row equals the scalar
 // DotFn bit for bit.
+// Q2: the activation chunk of 16 elements is staged as four nibble words
+// [hi even | hi odd | lo even | lo odd]: a = 16 (a >> 4) + (a & 15) exactly, nibble n
+// of an even (odd) word belongs to element 2n (2n + 1).  The 16 codes of a weight
+// dword D (code m at bits 2m) then need only two masks: D & 0x33333333 holds the
+// even codes as nibbles, (D >> 2) & 0x33333333 the odd ones, and
+// sum code * a = 16 sdot8(codes, hi) + udot8(codes, lo).
+constexpr uint32_t M4 = 0x33333333u;
 HH_DEV void unit_q2(const uint32_t (&w)[17], const int8_t* aq, const float* ad, const int* as, float (&pr)[2]) {
 #pragma clang fp contract(off)
 #pragma unroll
@@ -63,16 +69,19 @@ HH_DEV void unit_q2(const uint32_t (&w)[17], const int8_t* aq, const float* ad, 
     for (int sub = 0; sub < 4; ++sub) {
       const i32x4* A = (const i32x4*)(aq + blk * 128 + sub * 32);
       i32x4 a0 = A[0], a1 = A[1];
-      uint32_t D0 = c[2 * sub], D1 = c[2 * sub + 1];
-      int s = 0;
-      s = sdot4(D0 & M2, a0.x, s);
-      s = sdot4((D0 >> 2) & M2, a0.y, s);
-      s = sdot4((D0 >> 4) & M2, a0.z, s);
-      s = sdot4((D0 >> 6) & M2, a0.w, s);
-      s = sdot4(D1 & M2, a1.x, s);
-      s = sdot4((D1 >> 2) & M2, a1.y, s);
-      s = sdot4((D1 >> 4) & M2, a1.z, s);
-      s = sdot4((D1 >> 6) & M2, a1.w, s);
+      const uint32_t D0 = c[2 * sub], D1 = c[2 * sub + 1];
+      const uint32_t e0 = D0 & M4, o0 = (D0 >> 2) & M4, e1 = D1 & M4, o1 = (D1 >> 2) & M4;
+      int hi = 0;
+      hi = __builtin_amdgcn_sdot8((int)e0, a0.x, hi, false);
+      hi = __builtin_amdgcn_sdot8((int)o0, a0.y, hi, false);
+      hi = __builtin_amdgcn_sdot8((int)e1, a1.x, hi, false);
+      hi = __builtin_amdgcn_sdot8((int)o1, a1.y, hi, false);
+      uint32_t lo = 0;
+      lo = __builtin_amdgcn_udot8(e0, (uint32_t)a0.z, lo, false);
+      lo = __builtin_amdgcn_udot8(o0, (uint32_t)a0.w, lo, false);
+      lo = __builtin_amdgcn_udot8(e1, (uint32_t)a1.z, lo, false);
+      lo = __builtin_amdgcn_udot8(o1, (uint32_t)a1.w, lo, false);
+      int s = hi * 16 + (int)lo;
       s -= as[blk * 4 + sub];                 // sum (code-1)*a = sum code*a - sum a
       bacc += (float)s * ad[blk * 4 + sub];   // block_acc += dot * a_scale
     }
@@ -263,6 +272,24 @@ template <int FMT> HH_DEV void put_ds(float* ds, int blk32, float d, int s) {
   ((int*)ds)[t * dss<FMT>() + SUBS + sub] = s;
 }
 
+// Stage the int8 activations of elements e .. e+3 (e % 4 == 0, bytes of w in
+// element order) into the workgroup's LDS copy.  Q2: byte q = (e % 16) / 4 of
+// each nibble word of the chunk (elements e, e+2 are the even pair, e+1, e+3
+// the odd pair); other formats: one byte per element at lds_qpos.
+template <int FMT> HH_DEV void put4(int8_t* aq, int e, uint32_t w) {
+  if constexpr (FMT == FMT_Q2) {
+    uint8_t* ch = (uint8_t*)aq + (e >> 8) * 272 + (e & 240);
+    const int q = (e & 15) >> 2;
+    ch[q] = (uint8_t)(((w >> 4) & 0x0Fu) | ((w >> 16) & 0xF0u));        // hi even
+    ch[4 + q] = (uint8_t)(((w >> 12) & 0x0Fu) | ((w >> 24) & 0xF0u));   // hi odd
+    ch[8 + q] = (uint8_t)((w & 0x0Fu) | ((w >> 12) & 0xF0u));           // lo even
+    ch[12 + q] = (uint8_t)(((w >> 8) & 0x0Fu) | ((w >> 20) & 0xF0u));   // lo odd
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)(w >> (8 * i));
+  }
+}
+
 // A GEMV workgroup is NT = 1024 lanes (16 waves, one workgroup per CU at
 // the decode shapes): the activation prologue is the same for every
 // workgroup, so the fewer workgroups share a CU, the less of it each CU
@@ -357,8 +384,7 @@ HH_DEV void norm_finish(const GemvArgs& p, const NormRegs& r, int8_t* aq, float*
       }
       qs = group_sum_i<8>(qs);
       if (in) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)(word >> (8 * i));
+        put4<FMT>(aq, e, word);
         if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
       }
     }
@@ -405,7 +431,17 @@ template <int FMT> HH_DEV void packed_store(const GemvArgs& p, const PackedRegs&
     int c = tid + PK_L * i;
     if (c < K / 16) {
       int e = c * 16;
-      *(i32x4*)(aq + (e / EL) * qstride<FMT>() + (e % EL)) = r.q[i];
+      i32x4 v = r.q[i];
+      if constexpr (FMT == FMT_Q2) {
+        // packed chunk: dword k holds elements k, k+4, k+8, k+12 (element 4i+k at byte
+        // 4k+i), so byte j of the even words pairs dwords 0 and 2, of the odd words 1 and 3
+        const uint32_t d0 = v.x, d1 = v.y, d2 = v.z, d3 = v.w, m = 0x0F0F0F0Fu;
+        v.x = (int)(((d0 >> 4) & m) | (d2 & ~m));
+        v.y = (int)(((d1 >> 4) & m) | (d3 & ~m));
+        v.z = (int)((d0 & m) | ((d2 << 4) & ~m));
+        v.w = (int)((d1 & m) | ((d3 << 4) & ~m));
+      }
+      *(i32x4*)(aq + (e / EL) * qstride<FMT>() + (e % EL)) = v;
     }
   }
 #pragma unroll
@@ -444,8 +480,7 @@ template <int FMT> HH_DEV void std_store(const GemvArgs& p, const StdRegs& r, in
     for (int i = 0; i < 4; ++i) qs += (int)(int8_t)((r.q[c] >> (8 * i)) & 0xffu);
     qs = group_sum_i<8>(qs);
     if (e < K) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)((r.q[c] >> (8 * i)) & 0xffu);
+      put4<FMT>(aq, e, r.q[c]);
       if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(r.d[c]), qs);
     }
   }
@@ -530,8 +565,7 @@ template <int FMT, bool NORM> struct RotStage {
       }
       qs = group_sum_i<8>(qs);
       if (in) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) aq[lds_qpos(FMT, e + i)] = (int8_t)(word >> (8 * i));
+        put4<FMT>(aq, e, word);
         if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
       }
     }

@@ -211,7 +211,7 @@ def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
     hybrids, the same conv windows and GDN states) as feeding the prompt one
     token at a time: the first generated token's logits and the next tokens are
     identical, and match the device-order oracle (at 300 tokens too: the
-oracle skips the LM head for prompt tokens).  hybrid-2 prefills fewer
+    oracle skips the LM head for prompt tokens).  hybrid-2 prefills fewer
     tokens than the conv window holds; the kvq8 cases write a Q8_0 cache
     (quantized on write as the decode step does)."""
     print(f"prefill {cfg.d_model} {cfg.n_layers} n={n_prompt}", flush=True)
