@@ -127,10 +127,13 @@ HH_DEV float hx_log(float x) {
   return fmaf(fe, 0.693145751953125f, fmaf(fe, 1.428606765330187e-06f, lm));
 }
 
-// Position of element e (within the vector) in the permuted int8 array.
-//   Q2: chunk of 16; element 4i+k -> k*4+i     (matches (D >> 2k) & 0x03030303)
-//   Q1: chunk of 32; element 8i+j -> j*4+i     (matches (D >> j)  & 0x01010101)
+// Position of element e (within the vector) in the permuted int8 array of a
+// packed activation (the hand-off between kernels):
+//   Q2: chunk of 16; element 4i+k -> k*4+i     (the bytes of (D >> 2k) & 0x03030303)
+//   Q1: chunk of 32; element 8i+j -> j*4+i     (the bytes of (D >> j)  & 0x01010101)
 //   PTQ1_0 and Q8_0: natural order (a PTQ1_0 slot covers consecutive elements)
+// The GEMV stages Q2 and Q1 chunks in LDS as nibble words instead (put4 and
+// packed_store in hh_gemv.hip); the grouping above makes that a few bit operations.
 HH_DEV int perm_pos(int fmt, int e) {
   if (fmt == FMT_Q2) { int r = e & 15; return (e & ~15) | ((r & 3) << 2) | (r >> 2); }
   if (fmt == FMT_Q1) { int r = e & 31; return (e & ~31) | ((r & 7) << 2) | (r >> 3); }

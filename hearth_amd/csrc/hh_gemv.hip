@@ -32,7 +32,6 @@ namespace {
 enum { PRO_PACKED = 0, PRO_RMSNORM = 1, PRO_STDQ8 = 2, PRO_NORMROT = 3, PRO_F32ROT = 4 };
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
 
-constexpr uint32_t M1 = 0x01010101u;
 
 HH_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
@@ -49,6 +48,7 @@ HH_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4(
 // even codes as nibbles, (D >> 2) & 0x33333333 the odd ones, and
 // sum code * a = 16 sdot8(codes, hi) + udot8(codes, lo).
 constexpr uint32_t M4 = 0x33333333u;
+constexpr uint32_t M8 = 0x11111111u;
 HH_DEV void unit_q2(const uint32_t (&w)[17], const int8_t* aq, const float* ad, const int* as, float (&pr)[2]) {
 #pragma clang fp contract(off)
 #pragma unroll
@@ -107,18 +107,23 @@ HH_DEV void unit_q1(const uint32_t (&w)[9], const int8_t* aq, const float* ad, c
     float bacc = 0.0f;
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
+      // activation chunk: hi words H0..H3, lo words L0..L3; nibble n of word k is
+      // element 4n + k, as bit 4n + k of (D >> k) & 0x11111111
       const i32x4* A = (const i32x4*)(aq + blk * 128 + sub * 32);
       i32x4 a0 = A[0], a1 = A[1];
-      uint32_t D = c[sub];
-      int s = 0;
-      s = sdot4(D & M1, a0.x, s);
-      s = sdot4((D >> 1) & M1, a0.y, s);
-      s = sdot4((D >> 2) & M1, a0.z, s);
-      s = sdot4((D >> 3) & M1, a0.w, s);
-      s = sdot4((D >> 4) & M1, a1.x, s);
-      s = sdot4((D >> 5) & M1, a1.y, s);
-      s = sdot4((D >> 6) & M1, a1.z, s);
-      s = sdot4((D >> 7) & M1, a1.w, s);
+      const uint32_t D = c[sub];
+      const uint32_t p0 = D & M8, p1 = (D >> 1) & M8, p2 = (D >> 2) & M8, p3 = (D >> 3) & M8;
+      int hi = 0;
+      hi = __builtin_amdgcn_sdot8((int)p0, a0.x, hi, false);
+      hi = __builtin_amdgcn_sdot8((int)p1, a0.y, hi, false);
+      hi = __builtin_amdgcn_sdot8((int)p2, a0.z, hi, false);
+      hi = __builtin_amdgcn_sdot8((int)p3, a0.w, hi, false);
+      uint32_t lo = 0;
+      lo = __builtin_amdgcn_udot8(p0, (uint32_t)a1.x, lo, false);
+      lo = __builtin_amdgcn_udot8(p1, (uint32_t)a1.y, lo, false);
+      lo = __builtin_amdgcn_udot8(p2, (uint32_t)a1.z, lo, false);
+      lo = __builtin_amdgcn_udot8(p3, (uint32_t)a1.w, lo, false);
+      int s = hi * 16 + (int)lo;
       s = 2 * s - as[blk * 4 + sub];          // sum (+-1)*a = 2*sum bit*a - sum a
       bacc += (float)s * ad[blk * 4 + sub];
     }
@@ -273,10 +278,26 @@ template <int FMT> HH_DEV void put_ds(float* ds, int blk32, float d, int s) {
 }
 
 // Stage the int8 activations of elements e .. e+3 (e % 4 == 0, bytes of w in
-// element order) into the workgroup's LDS copy.  Q2: byte q = (e % 16) / 4 of
-// each nibble word of the chunk (elements e, e+2 are the even pair, e+1, e+3
-// the odd pair); other formats: one byte per element at lds_qpos.
-template <int FMT> HH_DEV void put4(int8_t* aq, int e, uint32_t w) {
+// element order) into the workgroup's LDS copy; lanes with in == false write
+// nothing.  Q2: byte q = (e % 16) / 4 of each nibble word of the chunk
+// (elements e, e+2 are the even pair, e+1, e+3 the odd pair).  Q1: lanes t and
+// t ^ 1 hold elements e and e ^ 4 of one 32-element chunk (the whole wave
+// calls this); after a lane swap the lane of e % 8 == 0 writes byte (e % 32) / 8
+// of the four hi words, its partner that byte of the four lo words.  Other
+// formats: one byte per element at lds_qpos.
+template <int FMT> HH_DEV void put4(int8_t* aq, int e, uint32_t w, bool in) {
+  if constexpr (FMT == FMT_Q1) {
+    const uint32_t o = (uint32_t)bfly_xchg<1>((int)w);
+    if (!in) return;
+    const bool first = (e & 4) == 0;
+    const uint32_t a = first ? w : o, b = first ? o : w;   // elements 8B + k, 8B + 4 + k
+    uint8_t* ch = (uint8_t*)aq + (e >> 8) * 272 + (e & 224) + (first ? 0 : 16) + ((e & 31) >> 3);
+    const int sh = first ? 4 : 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ch[4 * k] = (uint8_t)(((a >> (8 * k + sh)) & 0x0Fu) | (((b >> (8 * k + sh)) & 0x0Fu) << 4));
+    return;
+  }
+  if (!in) return;
   if constexpr (FMT == FMT_Q2) {
     uint8_t* ch = (uint8_t*)aq + (e >> 8) * 272 + (e & 240);
     const int q = (e & 15) >> 2;
@@ -383,10 +404,8 @@ HH_DEV void norm_finish(const GemvArgs& p, const NormRegs& r, int8_t* aq, float*
         word |= ((uint32_t)q & 0xffu) << (8 * i);
       }
       qs = group_sum_i<8>(qs);
-      if (in) {
-        put4<FMT>(aq, e, word);
-        if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
-      }
+      put4<FMT>(aq, e, word, in);
+      if (in && (tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
     }
   }
 }
@@ -429,9 +448,27 @@ template <int FMT> HH_DEV void packed_store(const GemvArgs& p, const PackedRegs&
 #pragma unroll
   for (int i = 0; i < PK_Q; ++i) {
     int c = tid + PK_L * i;
+    i32x4 v = r.q[i];
+    if constexpr (FMT == FMT_Q1) {
+      // a 32-element chunk is the 16-byte pieces of lanes t (dwords 0-3) and t ^ 1
+      // (dwords 4-7); dword j holds elements j, j+8, j+16, j+24 (element 8i+j at byte
+      // 4j+i).  Hi word k pairs dwords k and 4+k: the even lane writes the hi words,
+      // the odd lane the lo words, each at its own 16 bytes.
+      const uint32_t o0 = bfly_xchg<1>(v.x), o1 = bfly_xchg<1>(v.y), o2 = bfly_xchg<1>(v.z), o3 = bfly_xchg<1>(v.w);
+      const bool first = (c & 1) == 0;
+      const uint32_t m = 0x0F0F0F0Fu;
+      const uint32_t lo_[4] = {first ? (uint32_t)v.x : o0, first ? (uint32_t)v.y : o1, first ? (uint32_t)v.z : o2,
+                               first ? (uint32_t)v.w : o3};
+      const uint32_t hi_[4] = {first ? o0 : (uint32_t)v.x, first ? o1 : (uint32_t)v.y, first ? o2 : (uint32_t)v.z,
+                               first ? o3 : (uint32_t)v.w};
+      uint32_t r4[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        r4[k] = first ? (((lo_[k] >> 4) & m) | (hi_[k] & ~m)) : ((lo_[k] & m) | ((hi_[k] << 4) & ~m));
+      v.x = (int)r4[0]; v.y = (int)r4[1]; v.z = (int)r4[2]; v.w = (int)r4[3];
+    }
     if (c < K / 16) {
       int e = c * 16;
-      i32x4 v = r.q[i];
       if constexpr (FMT == FMT_Q2) {
         // packed chunk: dword k holds elements k, k+4, k+8, k+12 (element 4i+k at byte
         // 4k+i), so byte j of the even words pairs dwords 0 and 2, of the odd words 1 and 3
@@ -479,10 +516,8 @@ template <int FMT> HH_DEV void std_store(const GemvArgs& p, const StdRegs& r, in
 #pragma unroll
     for (int i = 0; i < 4; ++i) qs += (int)(int8_t)((r.q[c] >> (8 * i)) & 0xffu);
     qs = group_sum_i<8>(qs);
-    if (e < K) {
-      put4<FMT>(aq, e, r.q[c]);
-      if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(r.d[c]), qs);
-    }
+    put4<FMT>(aq, e, r.q[c], e < K);
+    if (e < K && (tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(r.d[c]), qs);
   }
 }
 
@@ -564,10 +599,8 @@ template <int FMT, bool NORM> struct RotStage {
         word |= ((uint32_t)q & 0xffu) << (8 * i);
       }
       qs = group_sum_i<8>(qs);
-      if (in) {
-        put4<FMT>(aq, e, word);
-        if ((tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
-      }
+      put4<FMT>(aq, e, word, in);
+      if (in && (tid & 7) == 0) put_ds<FMT>(ds, e >> 5, h2f(f2h(sc)), qs);
     }
   }
 };
