@@ -4,6 +4,8 @@
 // argmax, and the seeded synthetic-data generators.
 #include "hh_kernels.h"
 
+#include <type_traits>
+
 namespace {
 
 // ---------------------------------------------------------------------------
@@ -164,21 +166,28 @@ HH_DEV float4 slice_norm(float4 x, float4 w, float eps) {
   return make_float4(x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w);
 }
 
-// sn/cs: sin/cos of the slice's rotation index (c4 mod half); lanes with
-// 4c >= rope_dim keep x.
+// The RoPE table row of a lane's slice (rotation index c4 mod half): cos, and
+// sin negated for the first half, so that both halves rotate as x cos + y sin'.
+// First half: x0 cos - x1 sin = x0 cos + x1 (-sin) (IEEE a - b = a + (-b));
+// second half: x0 sin + x1 cos = x1 cos + x0 sin (IEEE addition commutes); the
+// products are the same, so both equal ops.rs's form bit for bit.
+HH_DEV void rope_row(const float* rope, int pos, int max_seq, int rope_dim, int c4, float4& sn, float4& cs) {
+  const int half = rope_dim / 2, ib = c4 < half ? c4 : c4 - half;
+  const float* base = rope + (size_t)(pos % max_seq) * half * 2;
+  sn = *(const float4*)(base + ib);
+  cs = *(const float4*)(base + half + ib);
+  if (c4 < half) sn = make_float4(-sn.x, -sn.y, -sn.z, -sn.w);
+}
+
+// sn/cs from rope_row; lanes with 4c >= rope_dim keep x.
 HH_DEV float4 slice_rope(float4 x, float4 sn, float4 cs, int c4, int rope_dim) {
   const int half = rope_dim / 2, X = half / 4;
   float4 y;   // partner slice (all lanes exchange; the wave stays converged)
   y.x = __shfl_xor(x.x, X, 64); y.y = __shfl_xor(x.y, X, 64);
   y.z = __shfl_xor(x.z, X, 64); y.w = __shfl_xor(x.w, X, 64);
-  if (c4 < half) {          // x0 = x, x1 = partner: x0*cos - x1*sin
-    return make_float4(x.x * cs.x - y.x * sn.x, x.y * cs.y - y.y * sn.y,
-                       x.z * cs.z - y.z * sn.z, x.w * cs.w - y.w * sn.w);
-  } else if (c4 < rope_dim) {   // x0 = partner, x1 = x: x0*sin + x1*cos
-    return make_float4(y.x * sn.x + x.x * cs.x, y.y * sn.y + x.y * cs.y,
-                       y.z * sn.z + x.z * cs.z, y.w * sn.w + x.w * cs.w);
-  }
-  return x;
+  const float4 r = make_float4(x.x * cs.x + y.x * sn.x, x.y * cs.y + y.y * sn.y,
+                               x.z * cs.z + y.z * sn.z, x.w * cs.w + y.w * sn.w);
+  return c4 < rope_dim ? r : x;
 }
 
 // Butterfly sum of NV values held by each lane of an aligned LPR-lane group,
@@ -273,14 +282,16 @@ HH_DEV float4 kv_q8_store(float4 x, const KvQ8& kv, size_t row, int hd, int c, b
   return make_float4(out[0], out[1], out[2], out[3]);
 }
 
-template <int HD, int NTA, bool KV8>
+// GT: the GQA group size n_heads / n_kv when it is one of the instantiated
+// values (the per-head loops then have exact trip counts), 0 = read at run time.
+template <int HD, int NTA, bool KV8, int GT>
 __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   constexpr int LPR = HD / 4, RPI = NTA / LPR, C = 8192 / HD, NR = C / RPI, NW = NTA / 64;
   static_assert(NR * RPI == C && NR >= 1, "geometry");
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int s = blockIdx.x, kvh = blockIdx.y;
-  const int G = a.n_heads / a.n_kv;
+  const int G = GT > 0 ? GT : a.n_heads / a.n_kv;
   int seq, pos;
   bool prep;
   if (a.fixed_seq > 0) {
@@ -305,11 +316,11 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   // 1. the small loads first (vector loads return in issue order): this
   // lane's slice of every q head and of the new k/v, the norm weights and the
   // RoPE row
-  constexpr int GMAX = 8;
-  float4 q4[GMAX], kn4 = make_float4(0.f, 0.f, 0.f, 0.f), vn4 = kn4;
+  constexpr int GMAX = GT > 0 ? GT : 8;
+  float4 q4[(GMAX + 3) & ~3], kn4 = make_float4(0.f, 0.f, 0.f, 0.f), vn4 = kn4;
   float4 nq4 = kn4, nk4 = kn4, sn4 = kn4, cs4 = kn4;
 #pragma unroll
-  for (int h = 0; h < GMAX; ++h) {
+  for (int h = 0; h < ((GMAX + 3) & ~3); ++h) {
     q4[h] = kn4;
     if (h < G) {
       const int qh = kvh * G + h;
@@ -323,12 +334,7 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   if (prep) {
     if (a.q_norm) nq4 = *(const float4*)(a.q_norm + 4 * c);
     if (a.k_norm) nk4 = *(const float4*)(a.k_norm + 4 * c);
-    if (a.rope && 4 * c < a.rope_dim) {
-      const int half = a.rope_dim / 2, ib = (4 * c < half) ? 4 * c : 4 * c - half;
-      const float* base = a.rope + (size_t)(pos % a.max_seq) * half * 2;
-      sn4 = *(const float4*)(base + ib);
-      cs4 = *(const float4*)(base + half + ib);
-    }
+    if (a.rope && 4 * c < a.rope_dim) rope_row(a.rope, pos, a.max_seq, a.rope_dim, 4 * c, sn4, cs4);
   }
 
   // 2. this chunk's K/V
@@ -685,12 +691,7 @@ __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QK
   if (nw) x = slice_norm<LPR>(x, *(const float4*)(nw + 4 * c), eps);
   if (rope) {
     float4 sn = make_float4(0.f, 0.f, 0.f, 0.f), cs = sn;
-    if (4 * c < rope_dim) {
-      const int half = rope_dim / 2, ib = (4 * c < half) ? 4 * c : 4 * c - half;
-      const float* base = rope + (size_t)(pos % max_seq) * half * 2;
-      sn = *(const float4*)(base + ib);
-      cs = *(const float4*)(base + half + ib);
-    }
+    if (4 * c < rope_dim) rope_row(rope, pos, max_seq, rope_dim, 4 * c, sn, cs);
     x = slice_rope(x, sn, cs, 4 * c, rope_dim);
   }
   if (is_k) {
@@ -1193,13 +1194,27 @@ int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
   const size_t split_lds = 4 * ((size_t)G * a.chunk + 2 * G + 8 + (ATTN_NT / 64) * 4 * (size_t)a.hd);
   const size_t merge_lds = 4 * ((size_t)a.max_splits + 256 + 4);
   const dim3 g(a.max_splits, a.n_kv), b(ATTN_NT);
+  auto split = [&](auto hd_c, auto kv8_c) {
+    constexpr int HD = decltype(hd_c)::value;
+    constexpr bool KV8 = decltype(kv8_c)::value;
+    switch (G) {
+      case 1: hipLaunchKernelGGL((k_attn_split<HD, ATTN_NT, KV8, 1>), g, b, split_lds, s, a); break;
+      case 2: hipLaunchKernelGGL((k_attn_split<HD, ATTN_NT, KV8, 2>), g, b, split_lds, s, a); break;
+      case 4: hipLaunchKernelGGL((k_attn_split<HD, ATTN_NT, KV8, 4>), g, b, split_lds, s, a); break;
+      case 6: hipLaunchKernelGGL((k_attn_split<HD, ATTN_NT, KV8, 6>), g, b, split_lds, s, a); break;
+      case 8: hipLaunchKernelGGL((k_attn_split<HD, ATTN_NT, KV8, 8>), g, b, split_lds, s, a); break;
+      default: hipLaunchKernelGGL((k_attn_split<HD, ATTN_NT, KV8, 0>), g, b, split_lds, s, a); break;
+    }
+  };
+  using T128 = std::integral_constant<int, 128>;
+  using T256 = std::integral_constant<int, 256>;
   if (a.hd == 128) {
-    if (a.kv_q8) hipLaunchKernelGGL((k_attn_split<128, ATTN_NT, true>), g, b, split_lds, s, a);
-    else hipLaunchKernelGGL((k_attn_split<128, ATTN_NT, false>), g, b, split_lds, s, a);
+    if (a.kv_q8) split(T128{}, std::true_type{});
+    else split(T128{}, std::false_type{});
     hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_heads, 2), dim3(256), merge_lds, s, a);
   } else {
-    if (a.kv_q8) hipLaunchKernelGGL((k_attn_split<256, ATTN_NT, true>), g, b, split_lds, s, a);
-    else hipLaunchKernelGGL((k_attn_split<256, ATTN_NT, false>), g, b, split_lds, s, a);
+    if (a.kv_q8) split(T256{}, std::true_type{});
+    else split(T256{}, std::false_type{});
     hipLaunchKernelGGL(k_attn_merge<256>, dim3(a.n_heads, 4), dim3(256), merge_lds, s, a);
   }
   return ok();
