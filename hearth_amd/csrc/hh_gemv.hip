@@ -29,7 +29,7 @@
 
 namespace {
 
-enum { PRO_PACKED = 0, PRO_RMSNORM = 1, PRO_STDQ8 = 2, PRO_NORMROT = 3, PRO_F32ROT = 4 };
+enum { PRO_PACKED = 0, PRO_RMSNORM = 1, PRO_STDQ8 = 2, PRO_NORMROT = 3, PRO_F32ROT = 4, PRO_RMSNORM_ALL = 5 };
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
 
 
@@ -332,20 +332,21 @@ constexpr int PK_L = NT;
 // slot s sums its float4s in c order as ss + (((x0^2 + x1^2) + x2^2) + x3^2),
 // slots 64w .. 64w+63 reduce by butterfly into W_w, the total is tree16(W).
 constexpr int NORM_CH = 2;   // K <= 8192
-constexpr int NJ = 1024 / NORM_L;
-struct NormRegs {
+template <int NL> struct NormRegsT {
+  static constexpr int NJ = 1024 / NL;
   float4 x[NJ][NORM_CH], w[NJ][NORM_CH];
   float* nbuf = nullptr;   // non-null: the f32 normed vector is also kept here (LDS)
 };
 
-HH_DEV void norm_issue(const GemvArgs& p, NormRegs& r) {
+template <int NL> HH_DEV void norm_issue(const GemvArgs& p, NormRegsT<NL>& r) {
+  constexpr int NJ = NormRegsT<NL>::NJ;
   const int tid = threadIdx.x;
-  if (tid >= NORM_L) return;
+  if (tid >= NL) return;
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int c = 0; c < NORM_CH; ++c) {
-      const int e = (tid + NORM_L * j) * 4 + 4096 * c;
+      const int e = (tid + NL * j) * 4 + 4096 * c;
       if (e < p.K) {
         r.x[j][c] = *(const float4*)(p.x + e);
         r.w[j][c] = *(const float4*)(p.norm_w + e);
@@ -353,16 +354,17 @@ HH_DEV void norm_issue(const GemvArgs& p, NormRegs& r) {
     }
 }
 
-HH_DEV void norm_partial(const GemvArgs& p, const NormRegs& r, float* red) {
+template <int NL> HH_DEV void norm_partial(const GemvArgs& p, const NormRegsT<NL>& r, float* red) {
+  constexpr int NJ = NormRegsT<NL>::NJ;
   const int tid = threadIdx.x;
-  if (tid >= NORM_L) return;
+  if (tid >= NL) return;
   float ss[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     ss[j] = 0.0f;
 #pragma unroll
     for (int c = 0; c < NORM_CH; ++c)
-      if ((tid + NORM_L * j) * 4 + 4096 * c < p.K)
+      if ((tid + NL * j) * 4 + 4096 * c < p.K)
         ss[j] += r.x[j][c].x * r.x[j][c].x + r.x[j][c].y * r.x[j][c].y + r.x[j][c].z * r.x[j][c].z +
                  r.x[j][c].w * r.x[j][c].w;
   }
@@ -370,14 +372,15 @@ HH_DEV void norm_partial(const GemvArgs& p, const NormRegs& r, float* red) {
   for (int j = 0; j < NJ; ++j) ss[j] = wave_sum(ss[j]);
   if ((tid & 63) == 0) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) red[(tid >> 6) + (NORM_L / 64) * j] = ss[j];
+    for (int j = 0; j < NJ; ++j) red[(tid >> 6) + (NL / 64) * j] = ss[j];
   }
 }
 
-template <int FMT>
-HH_DEV void norm_finish(const GemvArgs& p, const NormRegs& r, int8_t* aq, float* ds, const float* red) {
+template <int FMT, int NL>
+HH_DEV void norm_finish(const GemvArgs& p, const NormRegsT<NL>& r, int8_t* aq, float* ds, const float* red) {
+  constexpr int NJ = NormRegsT<NL>::NJ;
   const int tid = threadIdx.x;
-  if (tid >= NORM_L) return;
+  if (tid >= NL) return;
   const int K = p.K;
   const float tot = tree16(red);
   const float inv = 1.0f / sqrtf(tot / (float)K + p.eps);   // ops.rs:22-23
@@ -386,8 +389,8 @@ HH_DEV void norm_finish(const GemvArgs& p, const NormRegs& r, int8_t* aq, float*
     if (c > 0 && 4096 * c >= K) break;   // uniform: whole chunk absent
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int e = (tid + NORM_L * j) * 4 + 4096 * c;
-      if (4096 * c + NORM_L * j * 4 >= K) break;   // uniform
+      const int e = (tid + NL * j) * 4 + 4096 * c;
+      if (4096 * c + NL * j * 4 >= K) break;   // uniform
       const bool in = e < K;
       float vv[4] = {r.x[j][c].x * inv * r.w[j][c].x, r.x[j][c].y * inv * r.w[j][c].y,   // ops.rs:29 (x * inv) * w
                      r.x[j][c].z * inv * r.w[j][c].z, r.x[j][c].w * inv * r.w[j][c].w};
@@ -410,11 +413,11 @@ HH_DEV void norm_finish(const GemvArgs& p, const NormRegs& r, int8_t* aq, float*
   }
 }
 
-template <int FMT>
-HH_DEV void norm_store(const GemvArgs& p, const NormRegs& r, int8_t* aq, float* ds, float* red) {
-  norm_partial(p, r, red);
+template <int FMT, int NL>
+HH_DEV void norm_store(const GemvArgs& p, const NormRegsT<NL>& r, int8_t* aq, float* ds, float* red) {
+  norm_partial<NL>(p, r, red);
   __syncthreads();
-  norm_finish<FMT>(p, r, aq, ds, red);
+  norm_finish<FMT, NL>(p, r, aq, ds, red);
 }
 
 // PRO_PACKED: packed activation [q K][d K/32][s K/32] from a producer kernel,
@@ -611,12 +614,21 @@ template <int FMT> struct ActStage<FMT, PRO_NORMROT> : RotStage<FMT, true> {
 };
 template <int FMT> struct ActStage<FMT, PRO_F32ROT> : RotStage<FMT, false> {};
 template <int FMT> struct ActStage<FMT, PRO_RMSNORM> {
-  NormRegs r;
+  NormRegsT<NORM_L> r;
   HH_DEV const float* r_nbuf() const { return r.nbuf; }
-  HH_DEV void issue(const GemvArgs& p) { norm_issue(p, r); }
-  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT>(p, r, aq, ds, red); }
-  HH_DEV void part1(const GemvArgs& p, int8_t*, float*, float* red) { norm_partial(p, r, red); }
-  HH_DEV void part2(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_finish<FMT>(p, r, aq, ds, red); }
+  HH_DEV void issue(const GemvArgs& p) { norm_issue<NORM_L>(p, r); }
+  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT, NORM_L>(p, r, aq, ds, red); }
+  HH_DEV void part1(const GemvArgs& p, int8_t*, float*, float* red) { norm_partial<NORM_L>(p, r, red); }
+  HH_DEV void part2(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_finish<FMT, NORM_L>(p, r, aq, ds, red); }
+};
+// PRO_RMSNORM_ALL: the same arithmetic in all NT lanes (lane t holds slot t),
+// staged like the packed prologue: its loads are issued before the weights
+// and the weights stream while every lane quantizes its four values.
+template <int FMT> struct ActStage<FMT, PRO_RMSNORM_ALL> {
+  NormRegsT<NT> r;
+  HH_DEV const float* r_nbuf() const { return r.nbuf; }
+  HH_DEV void issue(const GemvArgs& p) { norm_issue<NT>(p, r); }
+  HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT, NT>(p, r, aq, ds, red); }
 };
 template <int FMT> struct ActStage<FMT, PRO_PACKED> {
   PackedRegs r;
@@ -695,7 +707,7 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   // the workgroup holds fewer than NT - NORM_L units).  Products are indexed by
   // unit, so the mapping does not change any sum.
   // GDN input projection: this workgroup's alpha/beta row (qwen35.rs:1285-1291)
-  constexpr bool AB_OK = (PRO == PRO_RMSNORM || PRO == PRO_NORMROT) && EPI == EPI_STORE;
+  constexpr bool AB_OK = (PRO == PRO_RMSNORM || PRO == PRO_RMSNORM_ALL || PRO == PRO_NORMROT) && EPI == EPI_STORE;
   const bool ab = AB_OK && p.ab_out && (int)blockIdx.x < p.ab_rows;   // uniform
   __shared__ float abred[16];
   float4 abw[2];
@@ -745,7 +757,7 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   }
   if constexpr (AB_OK) {
     if (ab) {
-      if constexpr (PRO == PRO_RMSNORM) act.r.nbuf = lds_tail;
+      if constexpr (PRO == PRO_RMSNORM || PRO == PRO_RMSNORM_ALL) act.r.nbuf = lds_tail;
       else act.nbuf = lds_tail;
     }
   }
@@ -1126,6 +1138,11 @@ int launch_p(const GemvArgs& a, int pro, int epi, int nu, int n_wg, size_t lds, 
       if (epi == EPI_STORE) return launch_u<FMT, PRO_RMSNORM, EPI_STORE>(a, nu, n_wg, lds, s);
       if (epi == EPI_SILU) return launch_u<FMT, PRO_RMSNORM, EPI_SILU>(a, nu, n_wg, lds, s);
       return 1;
+    case PRO_RMSNORM_ALL:
+      if (a.K % 1024 != 0 || a.K > NORM_CH * 4096) return 1;
+      if (epi == EPI_STORE) return launch_u<FMT, PRO_RMSNORM_ALL, EPI_STORE>(a, nu, n_wg, lds, s);
+      if (epi == EPI_SILU) return launch_u<FMT, PRO_RMSNORM_ALL, EPI_SILU>(a, nu, n_wg, lds, s);
+      return 1;
     case PRO_NORMROT:
       if (epi == EPI_STORE) return launch_u<FMT, PRO_NORMROT, EPI_STORE>(a, nu, n_wg, lds, s);
       if (epi == EPI_SILU) return launch_u<FMT, PRO_NORMROT, EPI_SILU>(a, nu, n_wg, lds, s);
@@ -1199,10 +1216,19 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   size_t lds = hh_gemv_lds(fmt, a.K, rows_total);
   if (rot) lds += (size_t)a.K * 4 + 16;   // the rotation buffer after rowsum
   if (a.ab_out) {   // the normed vector kept for the alpha/beta rows
-    if (epi != EPI_STORE || (pro != PRO_RMSNORM && pro != PRO_NORMROT) || a.K > 8192 || a.ab_rows > n_wg ||
+    if (epi != EPI_STORE || (pro != PRO_RMSNORM && pro != PRO_RMSNORM_ALL && pro != PRO_NORMROT) || a.K > 8192 ||
+        a.ab_rows > n_wg ||
         a.ab_rows != 2 * a.ab_n)
       return 1;
     lds += (size_t)a.K * 4 + (rot ? 0 : 16);
+  }
+  if (pro == PRO_RMSNORM && epi == EPI_STORE) {
+    // A workgroup with at most 32 KB of weights runs the RMSNorm prologue in all
+    // lanes with its weights issued behind the activation (8B in_proj 7.13 ->
+    // 6.55 us); larger shares keep the 4-wave staging and the `ready` hand-off
+    // (9B GDN in_proj, 52 KB: 7.96 -> 8.33 us the other way).
+    const int ub = fmt == FMT_Q1 ? UnitT<FMT_Q1>::BYTES : fmt == FMT_PT ? UnitT<FMT_PT>::BYTES : UnitT<FMT_Q2>::BYTES;
+    if ((size_t)rows_total * a.P * ub <= 32768) pro = PRO_RMSNORM_ALL;
   }
   const int ni = (rows_total * a.P + NT - 1) / NT;   // units per lane
   const int nu = ni <= 1 ? 1 : ni <= 2 ? 2 : ni <= 4 ? 4 : 0;

@@ -48,6 +48,8 @@ struct GemvArgs {
 // PRO_NORMROT: rms_norm(x, norm_w) then the fold, then Q8_0.
 // PRO_F32ROT: an f32 vector x (optionally permuted to grouped head order), the fold, then Q8_0.
 // EPI_SILU with y != null writes silu(g) * u as f32 into y instead of packed Q8_0.
+// (hh_gemv_launch runs PRO_RMSNORM + EPI_STORE launches with small weight shares
+// through an all-lanes variant of the same prologue.)
 enum { HH_PRO_PACKED = 0, HH_PRO_RMSNORM = 1, HH_PRO_STDQ8 = 2, HH_PRO_NORMROT = 3, HH_PRO_F32ROT = 4 };
 enum { HH_EPI_STORE = 0, HH_EPI_ADD = 1, HH_EPI_SILU = 2, HH_EPI_LOGITS = 3 };
 
