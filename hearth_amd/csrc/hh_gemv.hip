@@ -158,64 +158,79 @@ HH_DEV void unit_q8(const uint32_t (&w)[17], const int8_t* aq, const float* ad, 
 // PTQ1_0 (ptq1_0.rs:1-13): a block is qs[24] at 5 trits per byte (bytes 0..15
 // give elements 16n + m, bytes 16..23 elements 80 + 8n + (m-16)), qh[2] at 4
 // trits per byte (elements 120 + 2n + h), then the f16 scale.  Trit n of byte b
-// is ((b*3^n mod 256)*3) >> 8, walked as p <- b; q = 3p; trit = q >> 8;
-// p <- q mod 256, on two 16-bit lanes at once (v_pk_mul_lo_u16).
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-struct PtLanes {
-  u16x2 lo, hi;   // bytes 0,2 and 1,3 of a qs dword
-  HH_DEV explicit PtLanes(uint32_t q)
-      : lo(__builtin_bit_cast(u16x2, q & 0x00ff00ffu)), hi(__builtin_bit_cast(u16x2, (q >> 8) & 0x00ff00ffu)) {}
-  // the next slot's four trits (0..2) as bytes, in the dword's byte order
-  HH_DEV uint32_t next() {
-    const u16x2 three = {3, 3};
-    const u16x2 ql = lo * three, qh = hi * three;
-    const uint32_t tl = __builtin_bit_cast(uint32_t, (u16x2)(ql >> (u16x2){8, 8}));
-    const uint32_t th = __builtin_bit_cast(uint32_t, (u16x2)(qh >> (u16x2){8, 8}));
-    lo = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, ql) & 0x00ff00ffu);
-    hi = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, qh) & 0x00ff00ffu);
-    return tl | (th << 8);
-  }
-};
+// is ((b*3^n mod 256)*3) >> 8.  Every workgroup tabulates the 256 byte values
+// once in LDS (pt_lut: trits 0..3 as int8 (trit - 1) in .x, trit 4 in .y's low
+// byte); a qs dword then takes four table reads and a 4x4 byte transpose
+// (v_perm) to give, per trit index n, the four bytes' (trit - 1) values in
+// element order, ready for v_dot4 against the activations.
+__shared__ uint2 pt_lut[256];
 
-// One PTQ1_0 block (dwords w[0..6]) against its 128 activations: the
-// sub-block int dots sum(trit * a) - sum(a) = sum((trit - 1) * a), then the
-// scalar kernel's fp32 combine (ptq1_0.rs:587-599), as unit_q2.
-HH_DEV float block_pt(const uint32_t* w, const int8_t* aq, const float* ad, const int* as) {
+HH_DEV uint2 pt_lut_entry(uint32_t b) {
+  uint32_t p = b, t[5];
+#pragma unroll
+  for (int n = 0; n < 5; ++n) {
+    const uint32_t q = 3u * p;
+    t[n] = q >> 8;
+    p = q & 0xffu;
+  }
+  uint32_t x = 0;
+#pragma unroll
+  for (int n = 0; n < 4; ++n) x |= ((t[n] - 1u) & 0xffu) << (8 * n);
+  return make_uint2(x, (t[4] - 1u) & 0xffu);
+}
+
+// The five slots of a qs dword: out[n] = byte n of each of the four bytes'
+// table entries (byte m of out[n] from byte m of the dword).
+HH_DEV void pt_slots(uint32_t q, uint32_t (&out)[5]) {
+  const uint2 L0 = pt_lut[q & 0xffu], L1 = pt_lut[(q >> 8) & 0xffu], L2 = pt_lut[(q >> 16) & 0xffu],
+              L3 = pt_lut[q >> 24];
+  // perm(a, b, sel): selector 0..3 picks b's bytes, 4..7 a's
+  const uint32_t p01l = __builtin_amdgcn_perm(L1.x, L0.x, 0x05010400u);   // [L0.b0, L1.b0, L0.b1, L1.b1]
+  const uint32_t p01h = __builtin_amdgcn_perm(L1.x, L0.x, 0x07030602u);   // [L0.b2, L1.b2, L0.b3, L1.b3]
+  const uint32_t p23l = __builtin_amdgcn_perm(L3.x, L2.x, 0x05010400u);
+  const uint32_t p23h = __builtin_amdgcn_perm(L3.x, L2.x, 0x07030602u);
+  out[0] = __builtin_amdgcn_perm(p23l, p01l, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(p23l, p01l, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(p23h, p01h, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(p23h, p01h, 0x07060302u);
+  const uint32_t y01 = __builtin_amdgcn_perm(L1.y, L0.y, 0x0c0c0400u);   // [L0.y0, L1.y0, 0, 0]
+  const uint32_t y23 = __builtin_amdgcn_perm(L3.y, L2.y, 0x04000c0cu);   // [0, 0, L2.y0, L3.y0]
+  out[4] = y01 | y23;
+}
+
+// One PTQ1_0 block (dwords w[0..6]) against its 128 activations: per
+// sub-block the int dot sum((trit - 1) * a), then the scalar kernel's fp32
+// combine (ptq1_0.rs:587-599), as unit_q2.
+HH_DEV float block_pt(const uint32_t* w, const int8_t* aq, const float* ad, const int* /*as*/) {
 #pragma clang fp contract(off)
   const int* A = (const int*)aq;   // 32 activation dwords of the block
   int s[4] = {0, 0, 0, 0};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {   // stage A: slot n -> elements 16n + 4j .. +3
-    PtLanes L(w[j]);
+    uint32_t sl[5];
+    pt_slots(w[j], sl);
 #pragma unroll
-    for (int n = 0; n < 5; ++n) s[n >> 1] = sdot4(L.next(), (uint32_t)A[4 * n + j], s[n >> 1]);
+    for (int n = 0; n < 5; ++n) s[n >> 1] = sdot4(sl[n], (uint32_t)A[4 * n + j], s[n >> 1]);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {   // stage B: slot n -> elements 80 + 8n + 4j .. +3
-    PtLanes L(w[4 + j]);
+    uint32_t sl[5];
+    pt_slots(w[4 + j], sl);
 #pragma unroll
     for (int n = 0; n < 5; ++n) {
       const int sub = n < 2 ? 2 : 3;
-      s[sub] = sdot4(L.next(), (uint32_t)A[20 + 2 * n + j], s[sub]);
+      s[sub] = sdot4(sl[n], (uint32_t)A[20 + 2 * n + j], s[sub]);
     }
   }
-  {   // qh: bytes 24, 25 in the 16-bit lanes; elements 120 + 2n + h
+  {   // qh: bytes 24, 25 -> elements 120 + 2n + h
     const uint32_t W = w[6];
-    u16x2 p = __builtin_bit_cast(u16x2, (W & 0xffu) | ((W << 8) & 0x00ff0000u));
-    const u16x2 three = {3, 3};
-    uint32_t t[4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const u16x2 q = p * three;
-      t[n] = __builtin_bit_cast(uint32_t, (u16x2)(q >> (u16x2){8, 8}));
-      p = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, q) & 0x00ff00ffu);
-    }
-    s[3] = sdot4(__builtin_amdgcn_perm(t[1], t[0], 0x06040200u), (uint32_t)A[30], s[3]);
-    s[3] = sdot4(__builtin_amdgcn_perm(t[3], t[2], 0x06040200u), (uint32_t)A[31], s[3]);
+    const uint32_t Q0 = pt_lut[W & 0xffu].x, Q1 = pt_lut[(W >> 8) & 0xffu].x;
+    s[3] = sdot4(__builtin_amdgcn_perm(Q1, Q0, 0x05010400u), (uint32_t)A[30], s[3]);   // n = 0, 1
+    s[3] = sdot4(__builtin_amdgcn_perm(Q1, Q0, 0x07030602u), (uint32_t)A[31], s[3]);   // n = 2, 3
   }
   float bacc = 0.0f;
 #pragma unroll
-  for (int sub = 0; sub < 4; ++sub) bacc += (float)(s[sub] - as[sub]) * ad[sub];
+  for (int sub = 0; sub < 4; ++sub) bacc += (float)s[sub] * ad[sub];
   return bacc * h2f(w[6] >> 16);
 }
 
@@ -762,6 +777,9 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     }
   }
   act.issue(p);                      // activation first (in-order retirement)
+  if constexpr (FMT == FMT_PT) {     // read only after the prologue's barrier
+    if (tid < 256) pt_lut[tid] = pt_lut_entry(tid);
+  }
   if constexpr (NU > 0 && PRO == PRO_RMSNORM) {
     // Waves 0-3 stage the activation and raise `ready`; every wave computes as
     // soon as `ready` is complete and its own weights have arrived.  No barrier
