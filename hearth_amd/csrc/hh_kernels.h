@@ -144,14 +144,14 @@ int hh_kv_synth_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq, f
 // qwen35 GDN step (hh_gdn.hip)
 struct GdnArgs {
   const float* proj;      // [conv_dim] qkv projection (q | k | v), then [v_dim] z gate
-  const float* hidden;    // layer input; alpha/beta read rms_norm(hidden, attn_norm)
+  const float* hidden;    // prefill: layer input rows; alpha/beta read rms_norm(hidden, attn_norm)
   const float* attn_norm;
-  const float* w_alpha;   // [n_v][d] f32
+  const float* w_alpha;   // [n_v][d] f32 (prefill; decode forms the dots in the input projection)
   const float* w_beta;    // [n_v][d] f32
   const float* dt_bias;   // [n_v]
   const float* ssm_a;     // [n_v]
   const float* conv_w;    // [conv_dim][kernel]
-  float* conv_state;      // [conv_dim][kernel-1]
+  float* conv_state;      // [2][conv_dim][kernel-1] (see st / pos0 below)
   const float* ssm_norm;  // [hd]
   float* state;           // [n_v][hd][hd]
   int d, n_k, n_v, hd, kernel;
@@ -159,9 +159,10 @@ struct GdnArgs {
   uint8_t* act_out;       // packed activation of the gated-norm output (K = v_dim)
   int act_fmt;
   float* out_f32;         // non-null: the gated-norm output as f32 [v_dim] instead (folded models)
-  float* ab;              // scratch [2*n_v]
-  float* qk;              // scratch [2*k_dim] conv+silu+l2norm q,k
-  float* vconv;           // scratch [v_dim]
+  // batched prefill scratch rows (k_gdn_prep_rows -> recurrence): per token
+  float* ab;              // [S][2*n_v] g, beta
+  float* qk;              // [S][2*k_dim] conv+silu+l2norm q,k
+  float* vconv;           // [S][v_dim] conv+silu v
   const float* z;         // [v_dim] gate projection
   // batched prefill (hh_gdn_rows_launch): qk, vconv, ab, hidden are per-token
   // rows [S][...]; proj rows are row_in floats apart
