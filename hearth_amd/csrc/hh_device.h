@@ -280,6 +280,39 @@ template <int NTH> HH_DEV void lds_wht(float* x, int K, int blk) {
   __syncthreads();
 }
 
+// mod.rs:483-504: element i of the dequantized token_embd row of token tok.
+HH_DEV float embed_value(int type, const uint8_t* __restrict__ table, int d, int tok, int i) {
+  if (type == 8) {
+    const uint8_t* blk = table + (size_t)tok * (d / 32) * 34 + (size_t)(i / 32) * 34;
+    return h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) * (float)(int8_t)blk[2 + (i % 32)];
+  } else if (type == 42 || type == 142) {
+    const uint8_t* blk = table + (size_t)tok * (d / 128) * 34 + (size_t)(i / 128) * 34;
+    int e = i % 128;
+    int code = (blk[2 + e / 4] >> (2 * (e % 4))) & 3;
+    return (float)(code - 1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  }
+  const uint8_t* blk = table + (size_t)tok * (d / 128) * 18 + (size_t)(i / 128) * 18;
+  int e = i % 128;
+  int bit = (blk[2 + e / 8] >> (e % 8)) & 1;
+  return (float)(bit ? 1 : -1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+}
+
+// A latent (Hadamard-folded) embedding row gets R^-1 = H D after the lookup
+// (qwen35.rs:1054-1066, hadamard_unrotate :98-110): the WHT per had_block chunk,
+// then the sign pass.  buf: d floats of LDS.
+// NTH: the workgroup's lane count (all lanes call this; the latent path has barriers).
+template <int NTH>
+HH_DEV void embed_row(int type, const uint8_t* __restrict__ table, int d, int tok, float* __restrict__ out,
+                      const float* __restrict__ signs, int had_block, float* buf) {
+  if (had_block <= 0) {
+    for (int i = threadIdx.x; i < d; i += NTH) out[i] = embed_value(type, table, d, tok, i);
+    return;
+  }
+  for (int i = threadIdx.x; i < d; i += NTH) buf[i] = embed_value(type, table, d, tok, i);
+  lds_wht<NTH>(buf, d, had_block);
+  for (int i = threadIdx.x; i < d; i += NTH) out[i] = buf[i] * signs[i];
+}
+
 // Slot of element e of a GDN head-major vector in the grouped order the
 // ssm_out fold was computed in (qwen35.rs:1452-1478): head h = r * nk + kg
 // moves to head slot kg * rep + r.

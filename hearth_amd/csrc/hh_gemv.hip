@@ -946,25 +946,38 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
 // record the token, count it into the penalty history, move to the next
 // position.  For a prompt token other than the last the head computed
 // nothing and the state advances to the next prompt token.
+// The next step's embedding (mod.rs:483-504), written here so that the next
+// decode step needs no embedding kernel: all lanes, once the token is known.
+HH_DEV void head_final_embed(const GemvArgs& p, int tok, float* ebuf) {
+  if (!p.emb_out) return;   // uniform
+  embed_row<1024>(p.emb_type, p.emb_table, p.emb_d, tok, p.emb_out, p.emb_signs, p.emb_had, ebuf);
+}
+
 __global__ __launch_bounds__(1024) void k_head_final(GemvArgs p, int n_part) {
+  extern __shared__ __align__(16) float ebuf[];   // emb_d floats for a latent table
   __shared__ float sv[1024];
   __shared__ int si[1024];
-  __shared__ int step0, prompt_only;
+  __shared__ int step0, prompt_only, next_tok, advanced;
   StepState* st = p.state;
   const int tid = threadIdx.x;
   const int rule = p.rule;
   if (tid == 0) {
     step0 = st->step;
     prompt_only = (st->step + 1 < st->n_prompt);
+    next_tok = st->token;
+    advanced = 0;
   }
   __syncthreads();
   const int s = step0;
   if (prompt_only) {
     if (tid == 0) {
-      st->token = (int)p.prompt[s + 1];
+      next_tok = (int)p.prompt[s + 1];
+      st->token = next_tok;
       st->pos = st->pos + 1;
       st->step = s + 1;
     }
+    __syncthreads();
+    head_final_embed(p, next_tok, ebuf);
     return;
   }
   float v1 = -INFINITY;
@@ -1000,8 +1013,12 @@ __global__ __launch_bounds__(1024) void k_head_final(GemvArgs p, int n_part) {
       st->token = tok;
       st->pos = st->pos + 1;
       st->step = s + 1;
+      next_tok = tok;
+      advanced = 1;
     }
   }
+  __syncthreads();
+  if (advanced) head_final_embed(p, next_tok, ebuf);   // uniform
 }
 
 
@@ -1219,7 +1236,7 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
       case FMT_Q8: rc = launch_head<FMT_Q8>(a, s, &n_wg); break;
     }
     if (rc) return rc;
-    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), 0, s, a, n_wg);
+    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), a.emb_out && a.emb_had > 0 ? (size_t)a.emb_d * 4 : 0, s, a, n_wg);
     return hipGetLastError() == hipSuccess ? 0 : 1;
   }
   if (epi == EPI_SILU) {
@@ -1258,7 +1275,7 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
     case FMT_Q8: rc = launch_p<FMT_Q8>(a, pro, epi, nu, n_wg, lds, s); break;
   }
   if (rc == 0 && epi == EPI_LOGITS) {
-    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), 0, s, a, n_wg);
+    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), a.emb_out && a.emb_had > 0 ? (size_t)a.emb_d * 4 : 0, s, a, n_wg);
     rc = hipGetLastError() == hipSuccess ? 0 : 1;
   }
   return rc;

@@ -43,6 +43,12 @@ struct GemvArgs {
   const float* ab_wb;
   int ab_n, ab_rows;
   float* ab_out;
+  // EPI_LOGITS: k_head_final also writes the embedding of the next step's token
+  // into emb_out (null: not), with R^-1 for a latent table (emb_had > 0)
+  const uint8_t* emb_table;
+  int emb_type, emb_d, emb_had;
+  const float* emb_signs;
+  float* emb_out;
 };
 
 // PRO_NORMROT: rms_norm(x, norm_w) then the fold, then Q8_0.

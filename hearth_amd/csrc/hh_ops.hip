@@ -100,43 +100,12 @@ __global__ void k_rope(float* x, int n_heads, int hd, int rope_dim, const float*
   xh[i + half] = x0 * s + x1 * c;
 }
 
-// mod.rs:483-504: element i of the dequantized token_embd row of token tok.
-HH_DEV float embed_value(int type, const uint8_t* __restrict__ table, int d, int tok, int i) {
-  if (type == 8) {
-    const uint8_t* blk = table + (size_t)tok * (d / 32) * 34 + (size_t)(i / 32) * 34;
-    return h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) * (float)(int8_t)blk[2 + (i % 32)];
-  } else if (type == 42 || type == 142) {
-    const uint8_t* blk = table + (size_t)tok * (d / 128) * 34 + (size_t)(i / 128) * 34;
-    int e = i % 128;
-    int code = (blk[2 + e / 4] >> (2 * (e % 4))) & 3;
-    return (float)(code - 1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-  }
-  const uint8_t* blk = table + (size_t)tok * (d / 128) * 18 + (size_t)(i / 128) * 18;
-  int e = i % 128;
-  int bit = (blk[2 + e / 8] >> (e % 8)) & 1;
-  return (float)(bit ? 1 : -1) * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-}
-
-// A latent (Hadamard-folded) embedding row gets R^-1 = H D after the lookup
-// (qwen35.rs:1054-1066, hadamard_unrotate :98-110): the WHT per had_block chunk,
-// then the sign pass.  buf: d floats of LDS.
-HH_DEV void embed_row(int type, const uint8_t* __restrict__ table, int d, int tok, float* __restrict__ out,
-                      const float* __restrict__ signs, int had_block, float* buf) {
-  if (had_block <= 0) {
-    for (int i = threadIdx.x; i < d; i += 256) out[i] = embed_value(type, table, d, tok, i);
-    return;
-  }
-  for (int i = threadIdx.x; i < d; i += 256) buf[i] = embed_value(type, table, d, tok, i);
-  lds_wht<256>(buf, d, had_block);
-  for (int i = threadIdx.x; i < d; i += 256) out[i] = buf[i] * signs[i];
-}
-
 // hidden = dequantize(token_embd row), token from the step state.
 __global__ __launch_bounds__(256) void k_embed(int type, const uint8_t* __restrict__ table, int d,
                                                const StepState* __restrict__ st, float* __restrict__ hidden,
                                                const float* __restrict__ signs, int had_block) {
   extern __shared__ __align__(16) float ebuf[];
-  embed_row(type, table, d, st->token, hidden, signs, had_block, ebuf);
+  embed_row<256>(type, table, d, st->token, hidden, signs, had_block, ebuf);
 }
 
 // ---------------------------------------------------------------------------
@@ -567,7 +536,7 @@ __global__ __launch_bounds__(256) void k_embed_rows(int type, const uint8_t* __r
                                                     const float* __restrict__ signs, int had_block) {
   extern __shared__ __align__(16) float ebuf[];
   const int s = blockIdx.x;
-  embed_row(type, table, d, (int)toks[s], H + (size_t)s * d, signs, had_block, ebuf);
+  embed_row<256>(type, table, d, (int)toks[s], H + (size_t)s * d, signs, had_block, ebuf);
 }
 
 // The fold of a matmul input row (qwen35.rs:914-941) then Q8_0 into the GEMM's

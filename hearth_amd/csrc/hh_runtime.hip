@@ -167,8 +167,10 @@ struct hh_model {
   // graph
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
-  hipGraph_t graph_n = nullptr;        // GRAPH_STEPS consecutive decode steps in one graph
+  hipGraph_t graph_n = nullptr;        // graph_steps consecutive decode steps in one graph
   hipGraphExec_t gexec_n = nullptr;
+  hipGraph_t graph_ne = nullptr;       // one decode step without k_embed (the previous step's
+  hipGraphExec_t gexec_ne = nullptr;   // k_head_final wrote the embedding)
   int graph_steps = 1;
   hipEvent_t ev0 = nullptr, ev1 = nullptr, ev2 = nullptr, evp = nullptr;
   double last_decode_ms = 0.0, last_prefill_ms = 0.0;
@@ -292,20 +294,26 @@ int capture(hh_model* m) {
   if (e != hipSuccess) return fail(HH_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
   m->graph = g;
   HIP_TRY(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
-  if (m->gexec_n) { hipGraphExecDestroy(m->gexec_n); m->gexec_n = nullptr; }
-  if (m->graph_n) { hipGraphDestroy(m->graph_n); m->graph_n = nullptr; }
-  if (m->graph_steps > 1) {   // the step advances its own state, so steps chain inside one graph
+  // continuation graphs: steps whose token the previous step's k_head_final
+  // already embedded (every decode step of hh_model_generate after the first);
+  // the step advances its own state, so several chain inside one graph
+  auto capture_steps = [&](int n, hipGraph_t* gp, hipGraphExec_t* ep) -> int {
+    if (*ep) { hipGraphExecDestroy(*ep); *ep = nullptr; }
+    if (*gp) { hipGraphDestroy(*gp); *gp = nullptr; }
     HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int rc2 = 0;
-    for (int i = 0; i < m->graph_steps && rc2 == 0; ++i) rc2 = enqueue_step(m, s);
+    for (int i = 0; i < n && rc2 == 0; ++i) rc2 = enqueue_step(m, s, -1, ~1u);
     hipGraph_t gn = nullptr;
     hipError_t e2 = hipStreamEndCapture(s, &gn);
     if (rc2 != 0) { if (gn) hipGraphDestroy(gn); return rc2; }
     if (e2 != hipSuccess) return fail(HH_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e2));
-    m->graph_n = gn;
-    HIP_TRY(hipGraphInstantiate(&m->gexec_n, gn, nullptr, nullptr, 0));
-  }
-  return HH_OK;
+    *gp = gn;
+    HIP_TRY(hipGraphInstantiate(ep, gn, nullptr, nullptr, 0));
+    return HH_OK;
+  };
+  int rc3 = capture_steps(1, &m->graph_ne, &m->gexec_ne);
+  if (rc3 == HH_OK) rc3 = capture_steps(m->graph_steps, &m->graph_n, &m->gexec_n);
+  return rc3;
 }
 
 GemvArgs gemv_base(const uint8_t* w, int n_rows, int K, int rows_per_wg) {
@@ -453,6 +461,14 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
   h.part_val = m->head_pv;
   h.part_idx = m->head_pi;
   h.counter = m->counters;
+  // the next step's embedding, written by k_head_final (steps replayed by
+  // hh_model_generate then skip k_embed)
+  h.emb_table = m->token_embd->d;
+  h.emb_type = c.head_type;
+  h.emb_d = d;
+  h.emb_had = latent ? c.had_block : 0;
+  h.emb_signs = latent ? signs_of(m, d) : nullptr;
+  h.emb_out = m->hidden;
   if (had) fold(h, d);
   if (want(6, -1)) KTRY(hh_gemv_launch(hh_fmt_of(c.head_type), pro_norm, HH_EPI_LOGITS, h, s));
   return HH_OK;
@@ -1118,6 +1134,8 @@ int hh_model_destroy(hh_model* m) {
   if (m->graph) hipGraphDestroy(m->graph);
   if (m->gexec_n) hipGraphExecDestroy(m->gexec_n);
   if (m->graph_n) hipGraphDestroy(m->graph_n);
+  if (m->gexec_ne) hipGraphExecDestroy(m->gexec_ne);
+  if (m->graph_ne) hipGraphDestroy(m->graph_ne);
   void* bufs[] = {m->arena, m->kv, m->rec, m->rope, m->hidden, m->proj, m->act_mid, m->act_ffn, m->logits,
                   m->head_pv, m->head_pi, m->counters, m->attn_po, m->attn_pml, m->gdn_scratch, m->counts,
                   m->prompt, m->out_tokens, m->state, m->had_signs, m->rot_f32};
@@ -1310,10 +1328,10 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
   HIP_TRY(hipEventRecord(m->ev0, s));
   // decode steps: forward each generated token (the last forward only when its logits are wanted)
   int steps = n_gen - 1 + (last_logits ? 1 : 0);
+  // the last prompt step's k_head_final embedded the first generated token
   int i = 0;
-  if (m->gexec_n)
-    for (; i + m->graph_steps <= steps; i += m->graph_steps) HIP_TRY(hipGraphLaunch(m->gexec_n, s));
-  for (; i < steps; ++i) HIP_TRY(hipGraphLaunch(m->gexec, s));
+  for (; i + m->graph_steps <= steps; i += m->graph_steps) HIP_TRY(hipGraphLaunch(m->gexec_n, s));
+  for (; i < steps; ++i) HIP_TRY(hipGraphLaunch(m->gexec_ne, s));
   HIP_TRY(hipEventRecord(m->ev1, s));
   if (n_gen > 0)
     HIP_TRY(hipMemcpyAsync(out_tokens, m->out_tokens, sizeof(uint32_t) * n_gen, hipMemcpyDeviceToHost, s));
