@@ -79,6 +79,27 @@ def test_generate_tokens_parity(ctx, oracle, cfg, pen):
     assert np.array_equal(lg, lw)
 
 
+@pytest.mark.parametrize("cfg", [TINY, TINY_HYB], ids=["dense", "hybrid"])
+def test_generate_lengths_across_graph_batches(ctx, oracle, cfg):
+    """hh_model_generate runs the first decode step with the embedding kernel,
+    then steps whose embedding the previous k_head_final wrote, eight per graph
+    launch and the rest one at a time: lengths on both sides of those
+    boundaries, back to back on one model, equal the oracle token for token."""
+    m, o = make(ctx, oracle, cfg, seed=19)
+    pen = 1.1 if cfg.arch == 0 else 1.0
+    for n_gen in (1, 2, 8, 9, 17):
+        prompt = [oracle.synth_token(19, n_gen * 7 + i, cfg.vocab) for i in range(3)]
+        m.reset()
+        o.reset()
+        toks, lg = m.generate(prompt, n_gen, repeat_pen=pen, want_logits=True)
+        tw, lw = o.generate(prompt, n_gen, repeat_pen=pen, want_logits=True)
+        assert list(toks) == list(tw), n_gen
+        assert np.array_equal(lg, lw), n_gen
+        m.reset()
+        t2 = m.generate(prompt, n_gen, repeat_pen=pen)[0]   # no last logits: one step fewer
+        assert list(t2) == list(tw), n_gen
+
+
 def test_8b_shaped_prefilled_kv(ctx, oracle):
     """Config 3 geometry (d 4096, 32/8 heads, ffn 12288, vocab 151936) with 2
     layers, KV pre-filled to 2048 positions of seeded N(0,1) fp16 values, then
