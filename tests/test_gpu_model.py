@@ -116,6 +116,30 @@ def test_8b_shaped_prefilled_kv(ctx, oracle):
     assert np.array_equal(lg, lw)
 
 
+def test_8b_full_depth_bit_exact(ctx, oracle):
+    """The benchmarked model itself: all 36 layers of the 8B Q2_0 geometry, KV
+    pre-filled to 2048, four greedy steps with the 1.1 penalty through
+    hh_model_generate (graph batches and the head's embedding hand-off
+    included): tokens and the last logits equal the device-order oracle, which
+    holds the same weights (downloaded from the device)."""
+    cfg = CONFIGS["8b-q2"].replace(max_seq=2112)
+    from hearth_amd import Model
+    m = Model(ctx, cfg)
+    m.synthesize(2026)
+    o = oracle.OracleModel(cfg, seed=None, threads=16, order=oracle.OracleModel.DEVICE)
+    for name, t, ne0, ne1, nb in m.tensors():
+        o.tensor(name)[:] = m.download(name, nb)
+    m.prefill_kv_synthetic(77, 2048)
+    o.prefill_kv_synthetic(77, 2048)
+    print("8b full depth: generating", flush=True)
+    toks, lg = m.generate([5], 4, start_pos=2048, repeat_pen=1.1, want_logits=True)
+    tw, lw = o.generate([5], 4, start_pos=2048, repeat_pen=1.1, want_logits=True)
+    assert list(toks) == list(tw)
+    assert np.array_equal(lg, lw)
+    o.close()
+    m.close()
+
+
 @pytest.mark.parametrize("cfg,kv_type", [(CONFIGS["8b-q2"].replace(n_layers=1, max_seq=8192), 0),
                                          (CONFIGS["8b-q2"].replace(n_layers=1, max_seq=8192), 8),
                                          (CONFIGS["9b-hybrid-q2"].replace(n_layers=4, max_seq=8192), 0)],
