@@ -140,6 +140,30 @@ def test_8b_full_depth_bit_exact(ctx, oracle):
     m.close()
 
 
+@pytest.mark.parametrize("name", ["9b-hybrid-q2", "27b-hybrid-pq2"])
+def test_hybrid_full_depth_bit_exact(ctx, oracle, name):
+    """The benchmarked hybrids at full depth (9B: 32 layers; 27B PQ2_0: 64
+    layers, d 5120, vocab 248320): a 12-token prompt through the batched
+    prefill (MFMA GEMMs, GDN rows kernels, gated attention), then four greedy
+    steps; tokens and the last logits equal the device-order oracle fed token
+    by token on the same (downloaded) weights."""
+    cfg = CONFIGS[name].replace(max_seq=64)
+    from hearth_amd import Model
+    m = Model(ctx, cfg)
+    m.synthesize(31)
+    o = oracle.OracleModel(cfg, seed=None, threads=16, order=oracle.OracleModel.DEVICE)
+    for tname, t, ne0, ne1, nb in m.tensors():
+        o.tensor(tname)[:] = m.download(tname, nb)
+    prompt = [oracle.synth_token(31, i, cfg.vocab) for i in range(12)]
+    print(f"{name} full depth: generating", flush=True)
+    toks, lg = m.generate(prompt, 4, want_logits=True)
+    tw, lw = o.generate(prompt, 4, want_logits=True)
+    assert list(toks) == list(tw)
+    assert np.array_equal(lg, lw)
+    o.close()
+    m.close()
+
+
 @pytest.mark.parametrize("cfg,kv_type", [(CONFIGS["8b-q2"].replace(n_layers=1, max_seq=8192), 0),
                                          (CONFIGS["8b-q2"].replace(n_layers=1, max_seq=8192), 8),
                                          (CONFIGS["9b-hybrid-q2"].replace(n_layers=4, max_seq=8192), 0)],
