@@ -49,6 +49,9 @@ def _pick(oracle, cfg, logits, past, pen):
 def reference_run(oracle, cfg, seed, prompt, n_gen, threads=4, pen=1.0, prefilled=0, kv_seed=None):
     """Reference-order greedy run: returns the full token sequence, per-step
     reference logits (scalar arm, penalized when pen != 1) and the arm spread.
+    Also leaves on the function the scalar arm's raw per-step logits
+    (`raw_logits`) and the AVX2 arm's relative deviation from them (`avx_rel`,
+    max |avx - scalar| / max |scalar|, same teacher-forced inputs).
     `prefilled` > 0 starts at that position over a synthetic KV cache."""
     ref = oracle.OracleModel(cfg, seed=seed, threads=threads, arm=0, order=oracle.OracleModel.REFERENCE)
     avx = oracle.OracleModel(cfg, seed=seed, threads=threads, arm=1, order=oracle.OracleModel.REFERENCE)
@@ -59,6 +62,7 @@ def reference_run(oracle, cfg, seed, prompt, n_gen, threads=4, pen=1.0, prefille
     past = [prompt[-1]]
     logits, spread = [], 0.0
     avx_div = 0
+    raw, avx_rel = [], []
     for i in range(len(prompt) + n_gen - 1):
         pos = prefilled + i
         need = i >= len(prompt) - 1
@@ -66,6 +70,8 @@ def reference_run(oracle, cfg, seed, prompt, n_gen, threads=4, pen=1.0, prefille
         if need:
             la = avx.forward(seq[i], pos)
             spread = max(spread, float(np.abs(lr.astype(np.float64) - la).max()))
+            raw.append(np.array(lr, dtype=np.float32))
+            avx_rel.append(float(np.abs(la.astype(np.float64) - lr).max() / np.abs(lr).max()))
             logits.append(_penalized(oracle, lr, past, pen))
             tok = _pick(oracle, cfg, lr, past, pen)
             avx_div += int(_pick(oracle, cfg, la, past, pen) != tok)
@@ -76,6 +82,8 @@ def reference_run(oracle, cfg, seed, prompt, n_gen, threads=4, pen=1.0, prefille
     ref.close()
     avx.close()
     reference_run.avx_divergences = avx_div
+    reference_run.raw_logits = raw
+    reference_run.avx_rel = avx_rel
     return seq, logits, spread
 
 
