@@ -135,27 +135,29 @@ HH_DEV float4 slice_norm(float4 x, float4 w, float eps) {
   return make_float4(x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w);
 }
 
-// The RoPE table row of a lane's slice (rotation index c4 mod half): cos, and
-// sin negated for the first half, so that both halves rotate as x cos + y sin'.
-// First half: x0 cos - x1 sin = x0 cos + x1 (-sin) (IEEE a - b = a + (-b));
-// second half: x0 sin + x1 cos = x1 cos + x0 sin (IEEE addition commutes); the
-// products are the same, so both equal ops.rs's form bit for bit.
-HH_DEV void rope_row(const float* rope, int pos, int max_seq, int rope_dim, int c4, float4& sn, float4& cs) {
+// The RoPE table row of a lane's slice (rotation index c4 mod half): sin and
+// cos as stored.  slice_rope rotates the first half as x0 cos - x1 sin and the
+// second as x1 cos + x0 sin (= x0 sin + x1 cos: IEEE addition commutes), the
+// products and roundings of ops.rs's form, bit for bit.
+HH_DEV const float* rope_sin_ptr(const float* rope, int pos, int max_seq, int rope_dim, int c4) {
   const int half = rope_dim / 2, ib = c4 < half ? c4 : c4 - half;
-  const float* base = rope + (size_t)(pos % max_seq) * half * 2;
-  sn = *(const float4*)(base + ib);
-  cs = *(const float4*)(base + half + ib);
-  if (c4 < half) sn = make_float4(-sn.x, -sn.y, -sn.z, -sn.w);
+  return rope + (size_t)(pos % max_seq) * half * 2 + ib;   // cos at + half
 }
-
+HH_DEV void rope_row(const float* rope, int pos, int max_seq, int rope_dim, int c4, float4& sn, float4& cs) {
+  const float* ps = rope_sin_ptr(rope, pos, max_seq, rope_dim, c4);
+  sn = *(const float4*)ps;
+  cs = *(const float4*)(ps + rope_dim / 2);
+}
 // sn/cs from rope_row; lanes with 4c >= rope_dim keep x.
 HH_DEV float4 slice_rope(float4 x, float4 sn, float4 cs, int c4, int rope_dim) {
   const int half = rope_dim / 2, X = half / 4;
   float4 y;   // partner slice (all lanes exchange; the wave stays converged)
   y.x = __shfl_xor(x.x, X, 64); y.y = __shfl_xor(x.y, X, 64);
   y.z = __shfl_xor(x.z, X, 64); y.w = __shfl_xor(x.w, X, 64);
-  const float4 r = make_float4(x.x * cs.x + y.x * sn.x, x.y * cs.y + y.y * sn.y,
-                               x.z * cs.z + y.z * sn.z, x.w * cs.w + y.w * sn.w);
+  const float4 r = c4 < half ? make_float4(x.x * cs.x - y.x * sn.x, x.y * cs.y - y.y * sn.y,
+                                           x.z * cs.z - y.z * sn.z, x.w * cs.w - y.w * sn.w)
+                              : make_float4(x.x * cs.x + y.x * sn.x, x.y * cs.y + y.y * sn.y,
+                                           x.z * cs.z + y.z * sn.z, x.w * cs.w + y.w * sn.w);
   return c4 < rope_dim ? r : x;
 }
 
@@ -208,6 +210,10 @@ template <int N> HH_DEV float pairwise_tree(float* t) {
   return t[0];
 }
 
+// Zeros that stand in for K/V rows a split workgroup does not hold, so that
+// its loads need no branch (never written).
+__device__ __align__(16) float attn_zero_row[4];
+
 // Q8_0 KV rows (KV8): the cache holds int8 values [n_kv][max_seq][hd] followed
 // by the f16 block scales [n_kv][max_seq][hd/32].  A lane's float4 slice of a
 // row is its 4 int8 times the block's f16 scale, exactly the f32 value
@@ -217,6 +223,13 @@ struct KvQ8 {
   uint16_t* d;
   HH_DEV KvQ8(float* cache, int n_kv, int max_seq, int hd)
       : q((int8_t*)cache), d((uint16_t*)((int8_t*)cache + (size_t)n_kv * max_seq * hd)) {}
+  // the slice of row `row`, or zeros read from attn_zero_row when !held
+  HH_DEV float4 load_or_zero(size_t row, int hd, int c, bool held) const {
+    const uint32_t v = *(held ? (const uint32_t*)(q + row * hd + 4 * c) : (const uint32_t*)attn_zero_row);
+    const float s = h2f(*(held ? d + row * (hd / 32) + (c >> 3) : (const uint16_t*)attn_zero_row));
+    return make_float4((float)(int8_t)(v & 0xff) * s, (float)(int8_t)((v >> 8) & 0xff) * s,
+                       (float)(int8_t)((v >> 16) & 0xff) * s, (float)(int8_t)(v >> 24) * s);
+  }
   HH_DEV float4 load(size_t row, int hd, int c) const {   // row = kvh*max_seq + p, lane slice c
     const uint32_t v = *(const uint32_t*)(q + row * hd + 4 * c);
     const float s = h2f(d[row * (hd / 32) + (c >> 3)]);
@@ -284,43 +297,47 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
 
   // 1. the small loads first (vector loads return in issue order): this
   // lane's slice of every q head and of the new k/v, the norm weights and the
-  // RoPE row
+  // RoPE row.  Like the K/V loads below they are unconditional (absent ones
+  // read the zero row), so no wait on them can land before the K/V issue.
   constexpr int GMAX = GT > 0 ? GT : 8;
-  float4 q4[(GMAX + 3) & ~3], kn4 = make_float4(0.f, 0.f, 0.f, 0.f), vn4 = kn4;
-  float4 nq4 = kn4, nk4 = kn4, sn4 = kn4, cs4 = kn4;
+  const float* z = attn_zero_row;
+  float4 q4[(GMAX + 3) & ~3];
 #pragma unroll
   for (int h = 0; h < ((GMAX + 3) & ~3); ++h) {
-    q4[h] = kn4;
+    q4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (h < G) {
       const int qh = kvh * G + h;
       q4[h] = *(const float4*)(a.qkv + (a.gated ? (size_t)qh * 2 * HD : (size_t)qh * HD) + 4 * c);
     }
   }
-  if (has_new) {
-    kn4 = *(const float4*)(a.qkv + a.q_stride_heads + (size_t)kvh * HD + 4 * c);
-    vn4 = *(const float4*)(a.qkv + a.q_stride_heads + (size_t)a.n_kv * HD + (size_t)kvh * HD + 4 * c);
-  }
-  if (prep) {
-    if (a.q_norm) nq4 = *(const float4*)(a.q_norm + 4 * c);
-    if (a.k_norm) nk4 = *(const float4*)(a.k_norm + 4 * c);
-    if (a.rope && 4 * c < a.rope_dim) rope_row(a.rope, pos, a.max_seq, a.rope_dim, 4 * c, sn4, cs4);
-  }
+  const float* kv_new = a.qkv + a.q_stride_heads + (size_t)kvh * HD + 4 * c;
+  const float4 kn_raw = *(const float4*)(has_new ? kv_new : z);
+  const float4 vn_raw = *(const float4*)(has_new ? kv_new + (size_t)a.n_kv * HD : z);
+  const float4 nq4 = *(const float4*)(prep && a.q_norm ? a.q_norm + 4 * c : z);
+  const float4 nk4 = *(const float4*)(prep && a.k_norm ? a.k_norm + 4 * c : z);
+  const bool has_rope = prep && a.rope && 4 * c < a.rope_dim;
+  const float* ps = has_rope ? rope_sin_ptr(a.rope, pos, a.max_seq, a.rope_dim, 4 * c) : z;
+  const float4 sn4 = *(const float4*)ps;
+  const float4 cs4 = *(const float4*)(has_rope ? ps + a.rope_dim / 2 : z);
+  float4 kn4 = kn_raw, vn4 = vn_raw;
+  __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the K/V stream
 
-  // 2. this chunk's K/V
+  // 2. this chunk's K/V.  The loads are unconditional: a row the chunk does
+  // not hold (past the end, or the new position, filled in below) reads the
+  // zero row instead.  A load under a branch leaves the compiler no exact
+  // count of loads in flight, and its conservative wait would hold step 3's q
+  // prep until every K/V row had landed.
   float4 kr[NR], vr[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
     const int j = i * RPI + sub;
-    kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    vr[i] = kr[i];
-    if (j < np && p0 + j != pos) {
-      if constexpr (KV8) {
-        kr[i] = kq.load(row0 + p0 + j, HD, c);
-        vr[i] = vq.load(row0 + p0 + j, HD, c);
-      } else {
-        kr[i] = *(const float4*)(kg + (size_t)(p0 + j) * HD);
-        vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
-      }
+    const bool held = j < np && p0 + j != pos;
+    if constexpr (KV8) {
+      kr[i] = kq.load_or_zero(row0 + p0 + j, HD, c, held);
+      vr[i] = vq.load_or_zero(row0 + p0 + j, HD, c, held);
+    } else {
+      kr[i] = *(held ? (const float4*)(kg + (size_t)(p0 + j) * HD) : (const float4*)attn_zero_row);
+      vr[i] = *(held ? (const float4*)(vg + (size_t)(p0 + j) * HD) : (const float4*)attn_zero_row);
     }
   }
   // 3. q heads and the new k: per-head norm + rope on the lane's slice
@@ -465,18 +482,35 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   const size_t hb = (size_t)kvh * a.max_splits * G + h;
   const size_t tstride = (size_t)G * HD;
   const float* pb = a.part_o + hb * HD + d;
+  // Loads in the order their consumers need them, all issued before any
+  // wait: wave 0's (m, l) pairs of splits lane (its M/L pass), the gate (the
+  // last step, wave 0), then every wave's 16 partials.  The partial loads are
+  // unconditional (splits past the end re-read the last; the fma below skips
+  // them): under a branch, a load leaves the compiler no exact count of loads
+  // in flight, and its wait would cover every load issued before it.
+  float2 ml0 = make_float2(-INFINITY, 0.0f);
+  float g = 0.0f;
+  if (wid == 0) {
+    ml0 = *(const float2*)(a.part_ml + (hb + (size_t)min(lane, n_active - 1) * G) * 2);
+    if (a.gated) g = a.qkv[(size_t)qh * 2 * HD + HD + d];
+  }
   float pv[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int t = wid + 4 * i;
-    pv[i] = t < n_active ? pb[(size_t)t * tstride] : 0.0f;
+    const int t = min(wid + 4 * i, n_active - 1);
+    pv[i] = pb[(size_t)t * tstride];
   }
   if (wid == 0) {
-    float M = -INFINITY;
-    for (int t = lane; t < n_active; t += 64) M = fmaxf(M, a.part_ml[(hb + (size_t)t * G) * 2]);
+    float M = lane < n_active ? ml0.x : -INFINITY;
+    for (int t = lane + 64; t < n_active; t += 64) M = fmaxf(M, a.part_ml[(hb + (size_t)t * G) * 2]);
     M = wave_max(M);
     float L = 0.0f;
-    for (int t = lane; t < n_active; t += 64) {
+    if (lane < n_active) {
+      const float e = hx_exp(ml0.x - M);
+      wts[lane] = e;
+      L += e * ml0.y;
+    }
+    for (int t = lane + 64; t < n_active; t += 64) {
       float e = hx_exp(a.part_ml[(hb + (size_t)t * G) * 2] - M);
       wts[t] = e;
       L += e * a.part_ml[(hb + (size_t)t * G) * 2 + 1];
@@ -490,8 +524,8 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
     if (t0 > 0) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int t = t0 + wid + 4 * i;
-        pv[i] = t < n_active ? pb[(size_t)t * tstride] : 0.0f;
+        const int t = min(t0 + wid + 4 * i, n_active - 1);
+        pv[i] = pb[(size_t)t * tstride];
       }
     }
 #pragma unroll
@@ -505,10 +539,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   if (wid != 0) return;
   float o = (pw[lane] + pw[64 + lane]) + (pw[128 + lane] + pw[192 + lane]);
   o = o * (1.0f / *sL);
-  if (a.gated) {   // qwen35.rs:1627-1629 attn_out /= 1 + exp(-gate)
-    float g = a.qkv[(size_t)qh * 2 * HD + HD + d];
-    o = o / (1.0f + hx_exp(-g));
-  }
+  if (a.gated) o = o / (1.0f + hx_exp(-g));   // qwen35.rs:1627-1629 attn_out /= 1 + exp(-gate)
   if (a.out_f32) a.out_f32[(size_t)qh * HD + d] = o;
   if (a.act_out) {
     float am = group_max<32>(fabsf(o));
