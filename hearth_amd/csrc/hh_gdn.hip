@@ -157,38 +157,68 @@ __global__ __launch_bounds__(256) void k_gdn_prep_rows(GdnArgs a) {
 // lane = (column slice jb, row chunk ic, column jj): column j = 32 jb + jj,
 // rows 16 ic .. 16 ic + 15.  The column dots sum the 8 row-chunk partials in
 // chunk order.  The gated norm of the head's 128 outputs runs in wave 0 from LDS.
+template <int KT>   // the conv kernel length, or 0: read at run time (<= 8)
 __global__ __launch_bounds__(1024) void k_gdn_step(GdnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   constexpr int hd = 128;
+  constexpr int KM = KT > 0 ? KT : 8;
   const int h = blockIdx.x;
   const int jj = tid & 31, ic = (tid >> 5) & 7, jb = tid >> 8;
   const int j = jb * 32 + jj;
   const int kg = h % a.n_k;
-  const int kdim = a.n_k * hd, conv_dim = 2 * kdim + a.n_v * hd, K = a.kernel;
+  const int kdim = a.n_k * hd, conv_dim = 2 * kdim + a.n_v * hd, K = KT > 0 ? KT : a.kernel;
   float* S = a.state + (size_t)h * hd * hd;
   __shared__ float part[4][8][33];
   __shared__ float kv_s[2][hd];
   __shared__ float v_s[hd];
   __shared__ float o_s[hd];
   __shared__ float red[4];
+  // 1. the small loads first, unconditional (lanes 384.. read channel 0's
+  // window; the tail's gate and norm weight are read by every wave): vector
+  // loads return in issue order, and a load under a branch leaves the
+  // compiler no exact count of loads in flight, so either would make the
+  // conv chain wait for the state stream below.
+  const bool conv_lane = tid < 3 * hd;
+  const int ct = conv_lane ? tid : 0;
+  const int ch = ct < hd ? kg * hd + ct : ct < 2 * hd ? kdim + kg * hd + (ct - hd) : 2 * kdim + h * hd + (ct - 2 * hd);
+  const int pos = a.st->pos;
+  const size_t buf = (size_t)conv_dim * (K - 1);
+  const float* cs = a.conv_state + (size_t)(pos & 1) * buf + (size_t)ch * (K - 1);
+  const float* w = a.conv_w + (size_t)ch * K;
+  float win[KM], wc[KM];
+#pragma unroll
+  for (int t = 0; t < KM; ++t) {
+    win[t] = 0.0f;
+    wc[t] = 0.0f;
+    if (t < K - 1) win[t] = cs[t];
+  }
+  const float xin = a.proj[ch];
+#pragma unroll
+  for (int t = 0; t < KM; ++t)
+    if (t < K) wc[t] = w[t];
+  const float zg[2] = {a.z[(size_t)h * hd + lane], a.z[(size_t)h * hd + 64 + lane]};
+  const float nw[2] = {a.ssm_norm[lane], a.ssm_norm[64 + lane]};
+  const float alpha = a.ab_raw[h], braw = a.ab_raw[a.n_v + h], dtb = a.dt_bias[h], sa = a.ssm_a[h];
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. the head's state, column j, rows 16 ic .. 16 ic + 15
   float sreg[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) sreg[r] = S[(size_t)(ic * 16 + r) * hd + j];
   float y = 0.0f;
-  if (tid < 3 * hd) {   // conv + silu (qwen35.rs:1294-1303, :1820-1829)
-    const int ch = tid < hd ? kg * hd + tid : tid < 2 * hd ? kdim + kg * hd + (tid - hd) : 2 * kdim + h * hd + (tid - 2 * hd);
-    const int pos = a.st->pos;
-    const size_t buf = (size_t)conv_dim * (K - 1);
-    const float* cs = a.conv_state + (size_t)(pos & 1) * buf + (size_t)ch * (K - 1);
-    float* cd = a.conv_state + (size_t)((pos + 1) & 1) * buf + (size_t)ch * (K - 1);
-    float win[8];
-    for (int t = 0; t < K - 1; ++t) win[t] = cs[t];
-    win[K - 1] = a.proj[ch];
-    if (tid >= 2 * hd || h < a.n_k)
-      for (int t = 0; t < K - 1; ++t) cd[t] = win[t + 1];
-    const float* w = a.conv_w + (size_t)ch * K;
+  if (conv_lane) {   // conv + silu (qwen35.rs:1294-1303, :1820-1829)
+#pragma unroll
+    for (int t = 0; t < KM; ++t)
+      if (t == K - 1) win[t] = xin;
+    if (tid >= 2 * hd || h < a.n_k) {
+      float* cd = a.conv_state + (size_t)((pos + 1) & 1) * buf + (size_t)ch * (K - 1);
+#pragma unroll
+      for (int t = 0; t < KM - 1; ++t)
+        if (t < K - 1) cd[t] = win[t + 1];
+    }
     float acc = 0.0f;
-    for (int t = 0; t < K; ++t) acc += w[t] * win[t];
+#pragma unroll
+    for (int t = 0; t < KM; ++t)
+      if (t < K) acc += wc[t] * win[t];
     y = acc / (1.0f + hx_exp(-acc));
     if (tid < 2 * hd) {
       const float ss = wave_sum(y * y);
@@ -198,21 +228,13 @@ __global__ __launch_bounds__(1024) void k_gdn_step(GdnArgs a) {
     }
   }
   // g = softplus(alpha + dt_bias) * ssm_a, beta = sigmoid(b) (qwen35.rs:1359-1363)
-  const float decay = hx_exp(softplus_f(a.ab_raw[h] + a.dt_bias[h]) * a.ssm_a[h]);
-  const float b = 1.0f / (1.0f + hx_exp(-a.ab_raw[a.n_v + h]));
+  const float decay = hx_exp(softplus_f(alpha + dtb) * sa);
+  const float b = 1.0f / (1.0f + hx_exp(-braw));
   __syncthreads();
   if (tid < 2 * hd) {   // L2 norm of the q (lanes 0..127) and k (128..255) heads
     const int hw = wid & ~1;
     const float inv = 1.0f / sqrtf((red[hw] + red[hw + 1]) + a.eps);
     kv_s[tid < hd ? 1 : 0][tid & (hd - 1)] = y * inv;
-  }
-  // wave 0 also fetches the gate and norm weight of its two elements
-  float zg[2] = {0.0f, 0.0f}, nw[2] = {0.0f, 0.0f};
-  if (tid < 64) {
-    zg[0] = a.z[(size_t)h * hd + tid];
-    zg[1] = a.z[(size_t)h * hd + 64 + tid];
-    nw[0] = a.ssm_norm[tid];
-    nw[1] = a.ssm_norm[64 + tid];
   }
   __syncthreads();
   const float vj = v_s[j];
@@ -436,7 +458,8 @@ int hh_gdn_launch(const GdnArgs& a, hipStream_t s) {
   if (a.d % 1024 || a.d > 8192) return 1;
   if (!a.ab_raw || !a.st || a.n_v % a.n_k) return 1;
   (void)n_conv_wg;
-  hipLaunchKernelGGL(k_gdn_step, dim3(a.n_v), dim3(1024), 0, s, a);
+  if (a.kernel == 4) hipLaunchKernelGGL(k_gdn_step<4>, dim3(a.n_v), dim3(1024), 0, s, a);
+  else hipLaunchKernelGGL(k_gdn_step<0>, dim3(a.n_v), dim3(1024), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
