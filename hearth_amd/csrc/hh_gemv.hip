@@ -777,6 +777,11 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     }
   }
   act.issue(p);                      // activation first (in-order retirement)
+  // the residual of this lane's row (EPI_ADD), read now rather than after the
+  // row sums, where its round trip would be the kernel's last step
+  // (unconditional: lanes past the rows re-read the last)
+  float yres = 0.0f;
+  if constexpr (EPI == EPI_ADD) yres = p.y[r0 + min(tid, rows_total - 1)];
   if constexpr (FMT == FMT_PT) {     // read only after the prologue's barrier
     if (tid < 256) pt_lut[tid] = pt_lut_entry(tid);
   }
@@ -841,7 +846,7 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
     for (int r = tid; r < rows_total; r += NT) {
       if constexpr (EPI == EPI_STORE) p.y[r0 + r] = rowsum[r];
-      else p.y[r0 + r] = p.y[r0 + r] + rowsum[r];
+      else p.y[r0 + r] = (r == tid ? yres : p.y[r0 + r]) + rowsum[r];
     }
     if constexpr (AB_OK) {
       // alpha/beta dot (matvec_dense, qwen35.rs:1015-1025) in 1024 slots: slot t
