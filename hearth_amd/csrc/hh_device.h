@@ -220,6 +220,11 @@ template <int W> HH_DEV int group_sum_i(int v) {
   return v;
 }
 HH_DEV float wave_sum(float v) { return group_sum<64>(v); }
+// lane i <- lane i + K within its 16-lane row (DPP row_shl); lanes whose
+// source falls outside the row get 0
+template <int K> HH_DEV float dpp_from_lane_plus(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 | K, 0xF, 0xF, false));
+}
 HH_DEV float wave_max(float v) { return group_max<64>(v); }
 
 // Pairwise tree over 16 values (the wave sums of a 1024-slot reduction).

@@ -322,19 +322,16 @@ __global__ __launch_bounds__(256) void k_gdn_conv_advance(GdnArgs a) {
 // staged per block of TB tokens: the next block's k/q, v, g and beta are
 // loaded into registers while the current block runs.
 constexpr int REC_TB = 8;
-template <int K> HH_DEV float from_lane_plus(float v) {   // lane i <- lane i + K (same 16-lane row)
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 | K, 0xF, 0xF, false));
-}
 HH_DEV float sum8_in_order(float p) {   // lanes 8g: ((((0 + p0) + p1) + ...) + p7) of lanes 8g .. 8g+7
   float s = 0.0f;
   s += p;
-  s += from_lane_plus<1>(p);
-  s += from_lane_plus<2>(p);
-  s += from_lane_plus<3>(p);
-  s += from_lane_plus<4>(p);
-  s += from_lane_plus<5>(p);
-  s += from_lane_plus<6>(p);
-  s += from_lane_plus<7>(p);
+  s += dpp_from_lane_plus<1>(p);
+  s += dpp_from_lane_plus<2>(p);
+  s += dpp_from_lane_plus<3>(p);
+  s += dpp_from_lane_plus<4>(p);
+  s += dpp_from_lane_plus<5>(p);
+  s += dpp_from_lane_plus<6>(p);
+  s += dpp_from_lane_plus<7>(p);
   return s;
 }
 HH_DEV float from_group_base8(float v) {   // every lane <- lane (lane & ~7)

@@ -332,10 +332,12 @@ template <int FMT> HH_DEV void put4(int8_t* aq, int e, uint32_t w, bool in) {
 // repeats, and 16 waves hide its instruction latencies.
 constexpr int NT = 1024;
 
-// The RMSNorm prologue runs in the first NORM_L lanes (waves 0-3) and its
-// sum of squares is complete before any wave issues a weight load: the
-// activation read then meets an idle memory system instead of queueing behind
-// the whole chip's weight stream (measured on the 8B gate+up: 13.3 -> 12.2 us).
+// The RMSNorm prologue runs in the first NORM_L lanes (waves 0-3).  When it
+// reduces the sum of squares itself, that sum is complete before any wave
+// issues a weight load: the activation read then meets an idle memory system
+// instead of queueing behind the whole chip's weight stream (measured on the
+// 8B gate+up: 13.3 -> 12.2 us).  When the producer handed over the sum's tree
+// nodes (GemvArgs::sq_in) nothing is reduced and the weights go out at once.
 // The packed prologue (a plain copy) is staged by every lane and overlaps the
 // weight loads.
 constexpr int NORM_L = 256;
@@ -350,6 +352,7 @@ constexpr int NORM_CH = 2;   // K <= 8192
 template <int NL> struct NormRegsT {
   static constexpr int NJ = 1024 / NL;
   float4 x[NJ][NORM_CH], w[NJ][NORM_CH];
+  float4 sq;               // p.sq_in: tree nodes 4l .. 4l + 3 (lane l of the wave)
   float* nbuf = nullptr;   // non-null: the f32 normed vector is also kept here (LDS)
 };
 
@@ -357,6 +360,7 @@ template <int NL> HH_DEV void norm_issue(const GemvArgs& p, NormRegsT<NL>& r) {
   constexpr int NJ = NormRegsT<NL>::NJ;
   const int tid = threadIdx.x;
   if (tid >= NL) return;
+  if (p.sq_in) r.sq = *(const float4*)(p.sq_in + 4 * min(tid & 63, (p.K >> 6) - 1));   // K / 16 nodes
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -391,13 +395,25 @@ template <int NL> HH_DEV void norm_partial(const GemvArgs& p, const NormRegsT<NL
   }
 }
 
+// The sum of squares from the producer's tree nodes, in this wave alone: lane
+// l adds nodes 4l .. 4l+3 pairwise, then the wave's butterfly.  Node b covers
+// slots 4b .. 4b+3, so lane l's value is the tree node over slots 16l .. 16l+15
+// and the butterfly completes the same pairwise tree over the 1024 slots that
+// wave_sum + tree16 form (K <= 4096: one float4 per slot; nodes past K / 16
+// are zero, as those slots are).
+template <int NL> HH_DEV float norm_total_sq(const GemvArgs& p, const NormRegsT<NL>& r) {
+  const bool has = 4 * (threadIdx.x & 63) < (p.K >> 4);
+  const float v = has ? (r.sq.x + r.sq.y) + (r.sq.z + r.sq.w) : 0.0f;
+  return wave_sum(v);
+}
+
 template <int FMT, int NL>
 HH_DEV void norm_finish(const GemvArgs& p, const NormRegsT<NL>& r, int8_t* aq, float* ds, const float* red) {
   constexpr int NJ = NormRegsT<NL>::NJ;
   const int tid = threadIdx.x;
   if (tid >= NL) return;
   const int K = p.K;
-  const float tot = tree16(red);
+  const float tot = p.sq_in ? norm_total_sq<NL>(p, r) : tree16(red);
   const float inv = 1.0f / sqrtf(tot / (float)K + p.eps);   // ops.rs:22-23
 #pragma unroll
   for (int c = 0; c < NORM_CH; ++c) {
@@ -430,8 +446,10 @@ HH_DEV void norm_finish(const GemvArgs& p, const NormRegsT<NL>& r, int8_t* aq, f
 
 template <int FMT, int NL>
 HH_DEV void norm_store(const GemvArgs& p, const NormRegsT<NL>& r, int8_t* aq, float* ds, float* red) {
-  norm_partial<NL>(p, r, red);
-  __syncthreads();
+  if (!p.sq_in) {   // uniform
+    norm_partial<NL>(p, r, red);
+    __syncthreads();
+  }
   norm_finish<FMT, NL>(p, r, aq, ds, red);
 }
 
@@ -633,7 +651,14 @@ template <int FMT> struct ActStage<FMT, PRO_RMSNORM> {
   HH_DEV const float* r_nbuf() const { return r.nbuf; }
   HH_DEV void issue(const GemvArgs& p) { norm_issue<NORM_L>(p, r); }
   HH_DEV void store(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_store<FMT, NORM_L>(p, r, aq, ds, red); }
-  HH_DEV void part1(const GemvArgs& p, int8_t*, float*, float* red) { norm_partial<NORM_L>(p, r, red); }
+  // Without p.sq_in: the lane's part of the sum of squares, which waits for its
+  // activation loads, so the kernel's barrier after it holds every weight load
+  // until the activation has landed.  With p.sq_in nothing waits here and the
+  // weights stream at once (8B gate+up 10.98 -> 10.24 us, 9B GDN in_proj 7.97
+  // -> 7.63 us against the in-kernel reduction).
+  HH_DEV void part1(const GemvArgs& p, int8_t*, float*, float* red) {
+    if (!p.sq_in) norm_partial<NORM_L>(p, r, red);
+  }
   HH_DEV void part2(const GemvArgs& p, int8_t* aq, float* ds, float* red) { norm_finish<FMT, NORM_L>(p, r, aq, ds, red); }
 };
 // PRO_RMSNORM_ALL: the same arithmetic in all NT lanes (lane t holds slot t),
@@ -847,6 +872,20 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     for (int r = tid; r < rows_total; r += NT) {
       if constexpr (EPI == EPI_STORE) p.y[r0 + r] = rowsum[r];
       else p.y[r0 + r] = (r == tid ? yres : p.y[r0 + r]) + rowsum[r];
+    }
+    if constexpr (EPI == EPI_ADD) {
+      if (p.sq_out) {   // uniform; the launcher checks rows_per_wg % 16 == 0
+        // the RMSNorm tree over the rows just written, whole wave active:
+        // s (lane 4t) = ((v0 + v1) + v2) + v3, node (lane 16k) = (s0 + s1) + (s2 + s3)
+        const float yv = tid < rows_total ? yres + rowsum[tid] : 0.0f;
+        const float v = yv * yv;
+        float t = v + dpp_from_lane_plus<1>(v);
+        t = t + dpp_from_lane_plus<2>(v);
+        t = t + dpp_from_lane_plus<3>(v);
+        const float h = t + dpp_from_lane_plus<4>(t);
+        const float node = h + dpp_from_lane_plus<8>(h);
+        if (tid < rows_total && (tid & 15) == 0) p.sq_out[(r0 + tid) >> 4] = node;
+      }
     }
     if constexpr (AB_OK) {
       // alpha/beta dot (matvec_dense, qwen35.rs:1015-1025) in 1024 slots: slot t
@@ -1221,6 +1260,8 @@ size_t hh_gemv_lds(int fmt, int K, int rows_total_per_wg) {
 int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   int el = hh_unit_el(fmt);
   if (a.K % el != 0) return 1;
+  if (a.sq_in && (pro != PRO_RMSNORM || a.K % 64 != 0 || a.K > 4096)) return 1;
+  if (a.sq_out && (epi != EPI_ADD || a.rows_per_wg % 16 != 0 || a.rows_per_wg > NT || a.n_rows % 16 != 0)) return 1;
   a.P = a.K / el;
   int n_wg, rows_total;
   const bool rot = pro == PRO_NORMROT || pro == PRO_F32ROT;

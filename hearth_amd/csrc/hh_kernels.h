@@ -49,6 +49,13 @@ struct GemvArgs {
   int emb_type, emb_d, emb_had;
   const float* emb_signs;
   float* emb_out;
+  // Sum-of-squares hand-off of the hidden state.  sq_out (EPI_ADD, rows per
+  // workgroup a multiple of 16): for every 16 rows 16b.. of y written, the
+  // node (s0 + s1) + (s2 + s3) of the RMSNorm tree, s_t = ((y0^2 + y1^2) +
+  // y2^2) + y3^2 over rows 16b + 4t ..  sq_in (PRO_RMSNORM, EPI_LOGITS head;
+  // K <= 4096): those nodes of x, so each wave finishes the sum by itself.
+  float* sq_out;
+  const float* sq_in;
 };
 
 // PRO_NORMROT: rms_norm(x, norm_w) then the fold, then Q8_0.

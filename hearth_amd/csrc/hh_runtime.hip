@@ -148,6 +148,7 @@ struct hh_model {
   float* rope = nullptr;
   // step buffers
   float* hidden = nullptr;
+  float* hidden_sq = nullptr;   // RMSNorm tree nodes of hidden, one per 16 elements (GemvArgs::sq_out)
   float* proj = nullptr;        // QKV / GDN projection output
   uint8_t* act_mid = nullptr;   // packed input of attn_output / ssm_out
   uint8_t* act_ffn = nullptr;   // packed input of ffn_down
@@ -340,6 +341,11 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
   const bool latent = had && (c.had_flags & HH_HAD_LATENT_EMBD);
   const int pro_norm = had ? HH_PRO_NORMROT : HH_PRO_RMSNORM;
   auto fold = [&](GemvArgs& g, int width) { g.signs = signs_of(m, width); g.had_block = c.had_block; };
+  // The residual-add GEMVs hand the RMSNorm sum-of-squares tree nodes of the
+  // hidden state to the next norm prologue (no workgroup barrier there) when
+  // their workgroups own whole 16-row groups; layer 0's input comes from the
+  // embedding and keeps the in-kernel reduction.
+  const bool sq = !had && d % 64 == 0 && d <= 4096 && m->rows_out % 16 == 0 && m->rows_down % 16 == 0;
   if (want(0, -1))
     KTRY(hh_embed_launch(c.head_type, m->token_embd->d, d, m->state, m->hidden, latent ? signs_of(m, d) : nullptr,
                          latent ? c.had_block : 0, s));
@@ -352,6 +358,7 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
     g.eps = c.eps;
     g.y = m->proj;
     if (had) fold(g, d);
+    if (sq && li > 0) g.sq_in = m->hidden_sq;
     if (L.gdn) {   // the first 2 n_v workgroups also form the raw alpha / beta dots
       g.ab_wa = L.ssm_alpha;
       g.ab_wb = L.ssm_beta;
@@ -424,6 +431,7 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
     GemvArgs o = gemv_base(L.w_out, d, k_out, m->rows_out);
     o.act = m->act_mid;
     o.y = m->hidden;
+    if (sq) o.sq_out = m->hidden_sq;
     if (had) {
       o.x = m->rot_f32;
       fold(o, k_out);
@@ -438,17 +446,20 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
     gu.act_out = m->act_ffn;
     gu.act_out_fmt = wf;
     gu.act_out_k = c.d_ffn;
+    if (sq) gu.sq_in = m->hidden_sq;
     if (had) { fold(gu, d); gu.y = m->rot_f32; }
     if (want(4, li)) KTRY(hh_gemv_launch(wf, pro_norm, HH_EPI_SILU, gu, s));
     GemvArgs dn = gemv_base(L.w_down, d, c.d_ffn, m->rows_down);
     dn.act = m->act_ffn;
     dn.y = m->hidden;
+    if (sq) dn.sq_out = m->hidden_sq;
     if (had) { dn.x = m->rot_f32; fold(dn, c.d_ffn); }
     if (want(5, li)) KTRY(hh_gemv_launch(wf, had ? HH_PRO_F32ROT : HH_PRO_PACKED, HH_EPI_ADD, dn, s));
   }
   GemvArgs h = gemv_base(m->output->d, c.vocab, d, m->rows_head);
   h.x = m->hidden;
   h.norm_w = (const float*)m->output_norm->d;
+  if (sq && c.n_layers > 0) h.sq_in = m->hidden_sq;
   h.eps = c.eps;
   h.y = m->logits;
   h.state = m->state;
@@ -1075,6 +1086,7 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   int head_wg = std::max(256, (c.vocab + m->rows_head - 1) / m->rows_head);
   m->max_out = c.max_seq + 8;
   HIP_TRY(hipMalloc(&m->hidden, sizeof(float) * c.d_model));
+  HIP_TRY(hipMalloc(&m->hidden_sq, sizeof(float) * (c.d_model / 16 + 4)));
   HIP_TRY(hipMalloc(&m->proj, sizeof(float) * wide));
   HIP_TRY(hipMalloc(&m->act_mid, hh_packed_bytes(std::max(nq, vdim)) + 64));
   HIP_TRY(hipMalloc(&m->act_ffn, hh_packed_bytes(c.d_ffn) + 64));
@@ -1136,7 +1148,7 @@ int hh_model_destroy(hh_model* m) {
   if (m->graph_n) hipGraphDestroy(m->graph_n);
   if (m->gexec_ne) hipGraphExecDestroy(m->gexec_ne);
   if (m->graph_ne) hipGraphDestroy(m->graph_ne);
-  void* bufs[] = {m->arena, m->kv, m->rec, m->rope, m->hidden, m->proj, m->act_mid, m->act_ffn, m->logits,
+  void* bufs[] = {m->arena, m->kv, m->rec, m->rope, m->hidden, m->hidden_sq, m->proj, m->act_mid, m->act_ffn, m->logits,
                   m->head_pv, m->head_pi, m->counters, m->attn_po, m->attn_pml, m->gdn_scratch, m->counts,
                   m->prompt, m->out_tokens, m->state, m->had_signs, m->rot_f32};
   for (void* p : bufs)
