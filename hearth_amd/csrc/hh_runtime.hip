@@ -1082,6 +1082,13 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
     m->rows_out = gemv_rows_for(c.d_model, std::max(nq, vdim) / el);
     m->rows_down = gemv_rows_for(c.d_model, c.d_ffn / el);
     m->rows_head = gemv_rows_for(c.vocab, c.d_model / hh_unit_el(hh_fmt_of(c.head_type)));
+    // whole 16-row groups per residual-add workgroup, so that it can hand the
+    // RMSNorm tree nodes of the hidden state on (GemvArgs::sq_out); 1.7B (d
+    // 2048: 8 -> 16 rows, 128 workgroups) 1045 -> 1054 tok/s
+    if (c.d_model % 64 == 0 && c.d_model <= 4096 && c.had_block == 0) {
+      m->rows_out = (m->rows_out + 15) / 16 * 16;
+      m->rows_down = (m->rows_down + 15) / 16 * 16;
+    }
   }
   int head_wg = std::max(256, (c.vocab + m->rows_head - 1) / m->rows_head);
   m->max_out = c.max_seq + 8;
