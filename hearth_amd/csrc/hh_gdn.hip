@@ -181,16 +181,21 @@ __global__ __launch_bounds__(1024) void k_gdn_step(GdnArgs a) {
   const bool conv_lane = tid < 3 * hd;
   const int ct = conv_lane ? tid : 0;
   const int ch = ct < hd ? kg * hd + ct : ct < 2 * hd ? kdim + kg * hd + (ct - hd) : 2 * kdim + h * hd + (ct - 2 * hd);
-  const int pos = a.st->pos;
+  // both conv buffers' windows: which one holds this step's is the step
+  // position's parity, a load of its own that the addresses then need not wait for
   const size_t buf = (size_t)conv_dim * (K - 1);
-  const float* cs = a.conv_state + (size_t)(pos & 1) * buf + (size_t)ch * (K - 1);
+  const float* cs0 = a.conv_state + (size_t)ch * (K - 1);
   const float* w = a.conv_w + (size_t)ch * K;
-  float win[KM], wc[KM];
+  float win0[KM], win1[KM], wc[KM];
 #pragma unroll
   for (int t = 0; t < KM; ++t) {
-    win[t] = 0.0f;
+    win0[t] = 0.0f;
+    win1[t] = 0.0f;
     wc[t] = 0.0f;
-    if (t < K - 1) win[t] = cs[t];
+    if (t < K - 1) {
+      win0[t] = cs0[t];
+      win1[t] = cs0[buf + t];
+    }
   }
   const float xin = a.proj[ch];
 #pragma unroll
@@ -205,10 +210,11 @@ __global__ __launch_bounds__(1024) void k_gdn_step(GdnArgs a) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) sreg[r] = S[(size_t)(ic * 16 + r) * hd + j];
   float y = 0.0f;
+  const int pos = a.st->pos;
   if (conv_lane) {   // conv + silu (qwen35.rs:1294-1303, :1820-1829)
+    float win[KM];
 #pragma unroll
-    for (int t = 0; t < KM; ++t)
-      if (t == K - 1) win[t] = xin;
+    for (int t = 0; t < KM; ++t) win[t] = (t == K - 1) ? xin : (pos & 1) ? win1[t] : win0[t];
     if (tid >= 2 * hd || h < a.n_k) {
       float* cd = a.conv_state + (size_t)((pos + 1) & 1) * buf + (size_t)ch * (K - 1);
 #pragma unroll
