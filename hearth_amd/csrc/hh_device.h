@@ -18,6 +18,7 @@
 //   d[K/32] f32 (the f16 scale widened), s[K/32] int32 (sum of q per block; lets
 //        the unsigned 2-bit codes stand in for code-1 and bits for +-1).
 #pragma once
+#include <cstddef>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -343,6 +344,13 @@ HH_DEV int32_t synth_int(uint64_t key, uint64_t idx) {
 }
 
 // Device-side step state: the token loop runs without host round trips.
+// The 8 ints of the step state, lane l holding int l & 7: one vector load.
+// Its fields are taken with readlane where used.  A scalar load of the state
+// would be waited for together with the kernel-argument loads that the first
+// vector loads' addresses need (scalar loads return out of order, so that wait
+// is lgkmcnt(0)), putting the state's round trip ahead of them.
+HH_DEV int state_lanes(const void* st) { return ((const int*)st)[threadIdx.x & 7]; }
+
 struct StepState {
   int pos;        // position of the token being fed
   int step;       // steps executed in this session
@@ -353,3 +361,6 @@ struct StepState {
   int cancel;     // host-set cancel flag
   float pen;      // repetition penalty for the dense greedy rule
 };
+static_assert(sizeof(StepState) == 32 && offsetof(StepState, step) == 4 && offsetof(StepState, n_prompt) == 12 &&
+                  offsetof(StepState, pen) == 28,
+              "state_lanes readers take ints 1, 3 and 7");

@@ -1080,8 +1080,6 @@ __global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
   constexpr int UB = UnitT<FMT>::BYTES;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const StepState* st = p.state;
-  if (st->step + 1 < st->n_prompt) return;   // k_head_final advances the prompt
   const int K = p.K, P = p.P, n = p.n_rows;
   const int nunits_act = K / UnitT<FMT>::EL;
   int8_t* aq = (int8_t*)smem;
@@ -1104,8 +1102,8 @@ __global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
     cnt = cnt_src[p.counts ? r : 0];
   };
   const int rule = p.rule;
-  const float pen = st->pen;
-  const bool do_pen = rule == 0 && !(fabsf(pen - 1.0f) < 1e-6f);
+  float pen = 1.0f;        // StepState::pen, taken once the first loads are out
+  bool do_pen = false;
   float bv = -INFINITY;
   int bi = (rule == 0) ? -1 : 0x7fffffff;
   auto row = [&](const uint32_t (&wr)[U][DW], int cnt, int r) {
@@ -1138,13 +1136,19 @@ __global__ __launch_bounds__(NT) void k_head(GemvArgs p) {
   uint32_t wa[U][DW], wb[U][DW];
   int ca, cb;
   load_row(wa, ca, gw);
+  // the step state, read behind the first row: the loop waits for that row anyway
+  const int sv = state_lanes(p.state);
   act.store(p, aq, ds, red);
   __syncthreads();
-  for (int r = gw; r < n; r += 2 * W) {
+  // StepState::step + 1 < n_prompt: k_head_final advances the prompt, no rows
+  const int n_eff = __builtin_amdgcn_readlane(sv, 1) + 1 < __builtin_amdgcn_readlane(sv, 3) ? 0 : n;
+  pen = __int_as_float(__builtin_amdgcn_readlane(sv, 7));
+  do_pen = rule == 0 && !(fabsf(pen - 1.0f) < 1e-6f);
+  for (int r = gw; r < n_eff; r += 2 * W) {
     load_row(wb, cb, r + W);
     row(wa, ca, r);
     load_row(wa, ca, r + 2 * W);
-    if (r + W < n) row(wb, cb, r + W);
+    if (r + W < n_eff) row(wb, cb, r + W);
   }
   if (lane == 0) { bvs[wv] = bv; bis[wv] = bi; }
   __syncthreads();
