@@ -848,6 +848,29 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     comp_batch(wa, b);
     if (b + 1 < NB) comp_batch(wb, b + 1);
   }
+  if constexpr (AB_OK) {
+    // alpha/beta dot (matvec_dense, qwen35.rs:1015-1025) in 1024 slots: slot t
+    // sums w * x over its float4s at 4t + 4096c (c, then element, ascending);
+    // each wave's 64 slots by butterfly into abred; tree16 of abred after the
+    // row sums.  Run here, its wave sums share the barrier below.
+    if (ab) {
+      const float* nb = act.r_nbuf();
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int e = 4 * tid + 4096 * c;
+        if (e < K) {
+          const float4 x = *(const float4*)(nb + e);
+          acc = acc + abw[c].x * x.x;
+          acc = acc + abw[c].y * x.y;
+          acc = acc + abw[c].z * x.z;
+          acc = acc + abw[c].w * x.w;
+        }
+      }
+      acc = wave_sum(acc);
+      if ((tid & 63) == 0) abred[tid >> 6] = acc;
+    }
+  }
   __syncthreads();
 
   // per-row sums over the block products in block order (the scalar loop);
@@ -888,28 +911,7 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
       }
     }
     if constexpr (AB_OK) {
-      // alpha/beta dot (matvec_dense, qwen35.rs:1015-1025) in 1024 slots: slot t
-      // sums w * x over its float4s at 4t + 4096c (c, then element, ascending);
-      // each wave's 64 slots by butterfly; the 16 wave sums by tree16
-      if (ab) {
-        const float* nb = act.r_nbuf();
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int e = 4 * tid + 4096 * c;
-          if (e < K) {
-            const float4 x = *(const float4*)(nb + e);
-            acc = acc + abw[c].x * x.x;
-            acc = acc + abw[c].y * x.y;
-            acc = acc + abw[c].z * x.z;
-            acc = acc + abw[c].w * x.w;
-          }
-        }
-        acc = wave_sum(acc);
-        if ((tid & 63) == 0) abred[tid >> 6] = acc;
-        __syncthreads();
-        if (tid == 0) p.ab_out[blockIdx.x] = tree16(abred);
-      }
+      if (ab && tid == 0) p.ab_out[blockIdx.x] = tree16(abred);   // wave sums written before the row sums
     }
   } else if constexpr (EPI == EPI_SILU) {
     // ops.rs:240-253 silu then mul_elem (mod.rs:758-763), then Q8_0 (q8_0.rs:20-51)
