@@ -332,15 +332,17 @@ template <int FMT> HH_DEV void put4(int8_t* aq, int e, uint32_t w, bool in) {
 // repeats, and 16 waves hide its instruction latencies.
 constexpr int NT = 1024;
 
-// The RMSNorm prologue runs in the first NORM_L lanes (waves 0-3).  When it
+// The RMSNorm prologue runs in the first NORM_L lanes (waves 0-7).  When it
 // reduces the sum of squares itself, that sum is complete before any wave
 // issues a weight load: the activation read then meets an idle memory system
 // instead of queueing behind the whole chip's weight stream (measured on the
 // 8B gate+up: 13.3 -> 12.2 us).  When the producer handed over the sum's tree
 // nodes (GemvArgs::sq_in) nothing is reduced and the weights go out at once.
-// The packed prologue (a plain copy) is staged by every lane and overlaps the
-// weight loads.
-constexpr int NORM_L = 256;
+// Eight staging waves rather than four: with the hand-off the quantization is
+// the prologue's critical path (9B GDN in_proj 7.65 -> 6.75 us, 8B gate+up
+// 10.3 -> 10.2 us).  The packed prologue (a plain copy) is staged by every
+// lane and overlaps the weight loads.
+constexpr int NORM_L = 512;
 constexpr int PK_L = NT;
 
 // PRO_RMSNORM: rms_norm(x, w) then Q8_0, in lanes t < NORM_L.  Slot s
@@ -811,8 +813,9 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     if (tid < 256) pt_lut[tid] = pt_lut_entry(tid);
   }
   if constexpr (NU > 0 && PRO == PRO_RMSNORM) {
-    // Waves 0-3 stage the activation and raise `ready`; every wave computes as
-    // soon as `ready` is complete and its own weights have arrived.  No barrier
+    // The NORM_L staging lanes stage the activation and raise `ready`; every
+    // wave computes as soon as `ready` is complete and its own weights have
+    // arrived.  No barrier
     // separates the weight loads from the dot products: a CU's weight stream
     // retires in issue order while the waves that issued first already compute.
     __shared__ int ready;
@@ -1312,7 +1315,7 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   if (pro == PRO_RMSNORM && epi == EPI_STORE) {
     // A workgroup with at most 32 KB of weights runs the RMSNorm prologue in all
     // lanes with its weights issued behind the activation (8B in_proj 7.13 ->
-    // 6.55 us); larger shares keep the 4-wave staging and the `ready` hand-off
+    // 6.55 us); larger shares keep the staging waves and the `ready` hand-off
     // (9B GDN in_proj, 52 KB: 7.96 -> 8.33 us the other way).
     const int ub = fmt == FMT_Q1 ? UnitT<FMT_Q1>::BYTES : fmt == FMT_PT ? UnitT<FMT_PT>::BYTES : UnitT<FMT_Q2>::BYTES;
     if ((size_t)rows_total * a.P * ub <= 32768) pro = PRO_RMSNORM_ALL;
