@@ -892,7 +892,9 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     for (; j < NPR; ++j) s += part[j * RS + r];
     rowsum[r] = s;
   }
-  __syncthreads();
+  // EPI_STORE / EPI_ADD read rowsum[r] in the lane that wrote it (and the
+  // alpha/beta wave sums were written before the barrier above): no barrier
+  if constexpr (EPI != EPI_STORE && EPI != EPI_ADD) __syncthreads();
 
   if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
     for (int r = tid; r < rows_total; r += NT) {
