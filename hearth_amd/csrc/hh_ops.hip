@@ -148,12 +148,31 @@ HH_DEV void rope_row(const float* rope, int pos, int max_seq, int rope_dim, int 
   sn = *(const float4*)ps;
   cs = *(const float4*)(ps + rope_dim / 2);
 }
+// The value of lane (l ^ O), O a power of two: DPP within a 16-lane row for
+// O <= 8 (quad_perm for 1 and 2, row_ror:8 for 8, row_shl:4 / row_shr:4 by the
+// lane's bit 2 for 4), an LDS permute beyond.  The whole wave must be active.
+template <int O> HH_DEV float xor_lane(float v) {
+  const int x = __float_as_int(v);
+  if constexpr (O == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  else if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  else if constexpr (O == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false);   // lane + 4
+    const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // lane - 4
+    return __int_as_float((threadIdx.x & 4) ? dn : up);
+  } else if constexpr (O == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+  else return __shfl_xor(v, O, 64);
+}
+
 // sn/cs from rope_row; lanes with 4c >= rope_dim keep x.
 HH_DEV float4 slice_rope(float4 x, float4 sn, float4 cs, int c4, int rope_dim) {
   const int half = rope_dim / 2, X = half / 4;
   float4 y;   // partner slice (all lanes exchange; the wave stays converged)
-  y.x = __shfl_xor(x.x, X, 64); y.y = __shfl_xor(x.y, X, 64);
-  y.z = __shfl_xor(x.z, X, 64); y.w = __shfl_xor(x.w, X, 64);
+  if (X == 8) {   // rope_dim 64 (uniform branch)
+    y.x = xor_lane<8>(x.x); y.y = xor_lane<8>(x.y); y.z = xor_lane<8>(x.z); y.w = xor_lane<8>(x.w);
+  } else {
+    y.x = __shfl_xor(x.x, X, 64); y.y = __shfl_xor(x.y, X, 64);
+    y.z = __shfl_xor(x.z, X, 64); y.w = __shfl_xor(x.w, X, 64);
+  }
   const float4 r = c4 < half ? make_float4(x.x * cs.x - y.x * sn.x, x.y * cs.y - y.y * sn.y,
                                            x.z * cs.z - y.z * sn.z, x.w * cs.w - y.w * sn.w)
                               : make_float4(x.x * cs.x + y.x * sn.x, x.y * cs.y + y.y * sn.y,
@@ -176,13 +195,17 @@ template <int N, int O> struct ReduceScatter {
       for (int k = 0; k < N / 2; ++k) {
         float send = up ? v[k] : v[k + N / 2];
         float keep = up ? v[k + N / 2] : v[k];
-        v[k] = keep + __shfl_xor(send, O, 64);
+        v[k] = keep + xor_lane<O>(send);
       }
       return ReduceScatter<N / 2, O / 2>::run(v, lane);
     } else {
       float x = v[0];
-#pragma unroll
-      for (int o = O; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+      if constexpr (O >= 32) x += xor_lane<32>(x);
+      if constexpr (O >= 16) x += xor_lane<16>(x);
+      if constexpr (O >= 8) x += xor_lane<8>(x);
+      if constexpr (O >= 4) x += xor_lane<4>(x);
+      if constexpr (O >= 2) x += xor_lane<2>(x);
+      if constexpr (O >= 1) x += xor_lane<1>(x);
       return x;
     }
   }
