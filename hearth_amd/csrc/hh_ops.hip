@@ -160,7 +160,31 @@ template <int O> HH_DEV float xor_lane(float v) {
     const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // lane - 4
     return __int_as_float((threadIdx.x & 4) ? dn : up);
   } else if constexpr (O == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
-  else return __shfl_xor(v, O, 64);
+  else if constexpr (O == 16) {   // v_permlane16_swap(x, x): {rows 0,0,2,2 of x; rows 1,1,3,3 of x}
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+  } else {                        // O == 32: v_permlane32_swap(x, x): {low half twice; high half twice}
+    static_assert(O == 32, "offset");
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
+
+// One reduce-scatter level at offset O in {16, 32}: lanes below the offset bit
+// keep lo and receive the partner's lo, lanes above keep hi and receive the
+// partner's hi, and every lane returns keep + received.  The VALU swaps
+// (v_permlane16/32_swap(lo, hi)) hand each lane exactly that pair, so the sum
+// of the two results is keep + received (IEEE addition commutes).
+template <int O> HH_DEV float swap_pair_sum(float lo, float hi) {
+  static_assert(O == 16 || O == 32, "offset");
+  const unsigned a = __float_as_uint(lo), b = __float_as_uint(hi);
+  if constexpr (O == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
 }
 
 // sn/cs from rope_row; lanes with 4c >= rope_dim keep x.
@@ -169,6 +193,8 @@ HH_DEV float4 slice_rope(float4 x, float4 sn, float4 cs, int c4, int rope_dim) {
   float4 y;   // partner slice (all lanes exchange; the wave stays converged)
   if (X == 8) {   // rope_dim 64 (uniform branch)
     y.x = xor_lane<8>(x.x); y.y = xor_lane<8>(x.y); y.z = xor_lane<8>(x.z); y.w = xor_lane<8>(x.w);
+  } else if (X == 16) {   // rope_dim 128
+    y.x = xor_lane<16>(x.x); y.y = xor_lane<16>(x.y); y.z = xor_lane<16>(x.z); y.w = xor_lane<16>(x.w);
   } else {
     y.x = __shfl_xor(x.x, X, 64); y.y = __shfl_xor(x.y, X, 64);
     y.z = __shfl_xor(x.z, X, 64); y.w = __shfl_xor(x.w, X, 64);
@@ -193,9 +219,13 @@ template <int N, int O> struct ReduceScatter {
       const bool up = (lane & O) != 0;
 #pragma unroll
       for (int k = 0; k < N / 2; ++k) {
-        float send = up ? v[k] : v[k + N / 2];
-        float keep = up ? v[k + N / 2] : v[k];
-        v[k] = keep + xor_lane<O>(send);
+        if constexpr (O >= 16) {
+          v[k] = swap_pair_sum<O>(v[k], v[k + N / 2]);
+        } else {
+          float send = up ? v[k] : v[k + N / 2];
+          float keep = up ? v[k + N / 2] : v[k];
+          v[k] = keep + xor_lane<O>(send);
+        }
       }
       return ReduceScatter<N / 2, O / 2>::run(v, lane);
     } else {
@@ -450,11 +480,7 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
       const bool up = (lane & 32) != 0;
       float xs[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        float send = up ? acc[k] : acc[k + 8];
-        float keep = up ? acc[k + 8] : acc[k];
-        xs[k] = keep + __shfl_xor(send, 32, 64);
-      }
+      for (int k = 0; k < 8; ++k) xs[k] = swap_pair_sum<32>(acc[k], acc[k + 8]);
       // values kk = k (+ 8 on the upper half) go to row wid*4 + kk/4, column
       // 4c + kk%4: two 16-byte writes per lane (scalar writes at a 4-dword
       // lane stride would conflict 4 ways)
@@ -857,11 +883,7 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
           const bool up = (lane & 32) != 0;
           float xs[8];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            float send = up ? acc[k] : acc[k + 8];
-            float keep = up ? acc[k + 8] : acc[k];
-            xs[k] = keep + __shfl_xor(send, 32, 64);
-          }
+          for (int k = 0; k < 8; ++k) xs[k] = swap_pair_sum<32>(acc[k], acc[k + 8]);
 #pragma unroll
           for (int g = 0; g < 2; ++g)   // two 16-byte writes per lane, as the decode split
             *(float4*)(redu + (wid * 4 + g + (up ? 2 : 0)) * HD + 4 * cc) =
