@@ -79,6 +79,25 @@ def test_generate_tokens_parity(ctx, oracle, cfg, pen):
     assert np.array_equal(lg, lw)
 
 
+@pytest.mark.parametrize("K", [2, 3, 6])
+def test_hybrid_conv_kernel_lengths(ctx, oracle, K):
+    """The GDN causal conv at lengths other than qwen35's 4 (the loader takes 2..8):
+    the decode step's generic form (conv length read at run time) and the batched
+    prefill's conv-window hand-off, with prompts longer and shorter than the
+    window, then 16 greedy tokens: equal to the device-order oracle token for
+    token and in the last logits."""
+    cfg = TINY_HYB.replace(ssm_conv_kernel=K)
+    m, o = make(ctx, oracle, cfg, seed=23)
+    for n_prompt in (12, 2):
+        prompt = [oracle.synth_token(23, 50 * n_prompt + i, cfg.vocab) for i in range(n_prompt)]
+        m.reset()
+        o.reset()
+        toks, lg = m.generate(prompt, 16, repeat_pen=1.0, want_logits=True)
+        tw, lw = o.generate(prompt, 16, repeat_pen=1.0, want_logits=True)
+        assert list(toks) == list(tw), n_prompt
+        assert np.array_equal(lg, lw), n_prompt
+
+
 @pytest.mark.parametrize("cfg", [TINY, TINY_HYB], ids=["dense", "hybrid"])
 def test_generate_lengths_across_graph_batches(ctx, oracle, cfg):
     """hh_model_generate runs the first decode step with the embedding kernel,
