@@ -147,6 +147,13 @@ struct hh_model {
   size_t rec_bytes = 0;
   float* rope = nullptr;
   // step buffers
+  // KV rows per kv head in the cache (>= max_seq): an odd multiple of 64, so
+  // that the per-head stride is no multiple of a large power of two.  Strides
+  // of 2^22 B and more (max_seq 8192, 32768) measured ~2% slower decode at 2k
+  // context than 8000 or 2300, the kv heads' rows meeting in the same memory
+  // channels.  The attention kernels take it as their max_seq (the KV stride;
+  // positions stay below the configured max_seq, so the RoPE rows are the same).
+  int kv_rows = 0;
   float* hidden = nullptr;
   float* hidden_sq = nullptr;   // RMSNorm tree nodes of hidden, one per 16 elements (GemvArgs::sq_out)
   float* proj = nullptr;        // QKV / GDN projection output
@@ -409,7 +416,7 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
       aa.k_norm = L.k_norm;
       aa.eps = c.eps;
       aa.rope = m->rope;
-      aa.max_seq = c.max_seq;
+      aa.max_seq = m->kv_rows;
       aa.k_cache = L.k_cache;
       aa.v_cache = L.v_cache;
       aa.state = m->state;
@@ -605,10 +612,10 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
     } else {
       const int gated = hyb && c.attn_out_gate;
       KTRY(hh_prefill_qk_launch(hd, QKV, L.n_in, c.n_heads, c.n_kv_heads, c.qk_norm ? L.q_norm : nullptr,
-                                c.qk_norm ? L.k_norm : nullptr, c.eps, m->rope, m->rope_dim, c.max_seq, pos0, S,
+                                c.qk_norm ? L.k_norm : nullptr, c.eps, m->rope, m->rope_dim, m->kv_rows, pos0, S,
                                 gated, kv8, L.k_cache, L.v_cache, QB, s));
       for (int t0 = 0; t0 < S; t0 += TA)
-        KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, c.max_seq, pos0, t0,
+        KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, m->kv_rows, pos0, t0,
                                     std::min(TA, S - t0), n_chunks, PO, PML, gated ? QKV : nullptr, L.n_in, kv8,
                                     Xq, Xd, Rot, s));
       if (had)
@@ -1023,7 +1030,9 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
   // Q8_0 rows (kvcache.rs:41-57): int8 [kv_head][max_seq][hd], then the f16
   // block scales [kv_head][max_seq][hd/32] (136 B per row at hd 128, as the
   // reference's 34-byte blocks)
-  size_t per = (size_t)c.n_kv_heads * c.max_seq * hd;
+  m->kv_rows = (c.max_seq + 63) / 64 * 64;
+  if ((m->kv_rows / 64) % 2 == 0) m->kv_rows += 64;
+  size_t per = (size_t)c.n_kv_heads * m->kv_rows * hd;
   const size_t cache_bytes = c.kv_type == HH_Q8_0 ? align256(per + per / 32 * 2) : per * sizeof(float);
   m->kv_bytes = cache_bytes * 2 * (size_t)n_attn;
   if (m->kv_bytes) {
@@ -1267,10 +1276,10 @@ int hh_model_prefill_kv_synthetic(hh_model* m, uint64_t seed, int n_pos) {
     if (L.gdn) continue;
     auto synth = m->cfg.kv_type == HH_Q8_0 ? hh_kv_synth_q8_launch : hh_kv_synth_launch;
     snprintf(b, sizeof b, "blk.%d.kv_k", i);
-    KTRY(synth(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->cfg.max_seq, cs, L.k_cache,
+    KTRY(synth(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->kv_rows, cs, L.k_cache,
                m->ctx->stream));
     snprintf(b, sizeof b, "blk.%d.kv_v", i);
-    KTRY(synth(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->cfg.max_seq, cs, L.v_cache,
+    KTRY(synth(name_key(seed, b), n_pos, m->cfg.n_kv_heads, m->cfg.head_dim, m->kv_rows, cs, L.v_cache,
                m->ctx->stream));
   }
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
