@@ -227,6 +227,23 @@ template <int K> HH_DEV float dpp_from_lane_plus(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 | K, 0xF, 0xF, false));
 }
 HH_DEV float wave_max(float v) { return group_max<64>(v); }
+// wave_max for values that hold no NaN (softmax scores, -inf allowed): a
+// plain v_max_f32 per level, where fmaxf (and the med3 form, which the
+// compiler folds back into it) also quiets both operands first.
+HH_DEV float vmax_nonan(float a, float b) {
+  float r;
+  asm("v_max_f32_e32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+HH_DEV float wave_max_nonan(float v) {
+  v = vmax_nonan(v, bfly_xchg<1>(v));
+  v = vmax_nonan(v, bfly_xchg<2>(v));
+  v = vmax_nonan(v, bfly_xchg<4>(v));
+  v = vmax_nonan(v, bfly_xchg<8>(v));
+  v = vmax_nonan(v, bfly_xchg<16>(v));
+  v = vmax_nonan(v, bfly_xchg<32>(v));
+  return v;
+}
 
 // Pairwise tree over 16 values (the wave sums of a 1024-slot reduction).
 HH_DEV float tree16(const float* v) {

@@ -156,9 +156,10 @@ template <int O> HH_DEV float xor_lane(float v) {
   if constexpr (O == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
   else if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
   else if constexpr (O == 4) {
-    const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false);   // lane + 4
-    const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // lane - 4
-    return __int_as_float((threadIdx.x & 4) ? dn : up);
+    // banks 0 and 2 of each row (lane bit 2 clear) read lane + 4, then banks
+    // 1 and 3 read lane - 4 over the first result
+    const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0x5, false);
+    return __int_as_float(__builtin_amdgcn_update_dpp(up, x, 0x114, 0xF, 0xA, false));
   } else if constexpr (O == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
   else if constexpr (O == 16) {   // v_permlane16_swap(x, x): {rows 0,0,2,2 of x; rows 1,1,3,3 of x}
     const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
@@ -212,7 +213,46 @@ HH_DEV float4 slice_rope(float4 x, float4 sn, float4 cs, int c4, int rope_dim) {
 // the all-lanes butterfly x_l + x_(l^O) at that level, so the result for
 // value k is the butterfly sum with offsets LPR/2, ..., 1.  On return lane l
 // holds value k = (l % LPR) >> log2(LPR / NV).
+// Lanes hand over their values in a lane-dependent register order: register
+// r of lane l holds value r ^ rs_perm<NV, LPR / 2>(l).  At each level below
+// offset 16 every lane then keeps registers [0, N/2) and sends [N/2, N): a
+// lane whose offset bit is set holds the upper half in the lower registers,
+// and its partner's upper registers hold that same half, so each kept sum is
+// the same pair of values, added in the same order, with no per-lane select.
+// (The permlane swaps of the offsets 16 and 32 pair registers r and r + N/2
+// across the lanes themselves.)
+template <int N, int O> HH_DEV int rs_perm(int lane) {
+  if constexpr (N > 1) return ((O < 16 && (lane & O)) ? N / 2 : 0) ^ rs_perm<N / 2, O / 2>(lane);
+  else return 0;
+}
 template <int N, int O> struct ReduceScatter {
+  static HH_DEV float run(float* v) {
+    if constexpr (N > 1) {
+      static_assert(O > 0, "more values than lanes");
+#pragma unroll
+      for (int k = 0; k < N / 2; ++k) {
+        if constexpr (O >= 16) v[k] = swap_pair_sum<O>(v[k], v[k + N / 2]);
+        else v[k] = v[k] + xor_lane<O>(v[k + N / 2]);
+      }
+      return ReduceScatter<N / 2, O / 2>::run(v);
+    } else {
+      float x = v[0];
+      if constexpr (O >= 32) x += xor_lane<32>(x);
+      if constexpr (O >= 16) x += xor_lane<16>(x);
+      if constexpr (O >= 8) x += xor_lane<8>(x);
+      if constexpr (O >= 4) x += xor_lane<4>(x);
+      if constexpr (O >= 2) x += xor_lane<2>(x);
+      if constexpr (O >= 1) x += xor_lane<1>(x);
+      return x;
+    }
+  }
+};
+
+// The same butterfly sum with values in the natural register order: lanes
+// whose offset bit is set keep the upper half, chosen per lane.  The decode
+// split uses it: its one pass is latency-bound, and the permuted order's
+// extra K addressing and q swaps cost more there than the selects.
+template <int N, int O> struct ReduceScatterSel {
   static HH_DEV float run(float* v, int lane) {
     if constexpr (N > 1) {
       static_assert(O > 0, "more values than lanes");
@@ -222,12 +262,12 @@ template <int N, int O> struct ReduceScatter {
         if constexpr (O >= 16) {
           v[k] = swap_pair_sum<O>(v[k], v[k + N / 2]);
         } else {
-          float send = up ? v[k] : v[k + N / 2];
-          float keep = up ? v[k + N / 2] : v[k];
+          const float send = up ? v[k] : v[k + N / 2];
+          const float keep = up ? v[k + N / 2] : v[k];
           v[k] = keep + xor_lane<O>(send);
         }
       }
-      return ReduceScatter<N / 2, O / 2>::run(v, lane);
+      return ReduceScatterSel<N / 2, O / 2>::run(v, lane);
     } else {
       float x = v[0];
       if constexpr (O >= 32) x += xor_lane<32>(x);
@@ -439,7 +479,7 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
         v[hh * NR + i] = p;
       }
     }
-    const float r = ReduceScatter<NV, LPR / 2>::run(v, lane);
+    const float r = ReduceScatterSel<NV, LPR / 2>::run(v, lane);
     const int k = (lane & (LPR - 1)) >> KSH;
     const int h = hg + k / NR, j = (k % NR) * RPI + sub;
     if (h < G && (lane & ((1 << KSH) - 1)) == 0) sc[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
@@ -448,7 +488,7 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   // 5. per-head softmax statistics over the chunk (C <= 64)
   for (int h = wid; h < G; h += NW) {
     float x = lane < C ? sc[h * C + lane] : -INFINITY;
-    float m = wave_max(x);
+    float m = wave_max_nonan(x);
     float e = (lane < np) ? hx_exp(x - m) : 0.0f;
     float l = wave_sum(e);
     if (lane < C) sc[h * C + lane] = e;
@@ -765,7 +805,7 @@ __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QK
 // order) once per token of the tile whose position reaches the chunk, NTOK
 // tokens per pass.  GMAX bounds the query heads per kv head (registers).
 // Partials: PO[((sl*n_kv + kvh)*n_chunks + c)*G + h][HD], PML likewise x2.
-template <int HD, int NTA, bool KV8, int GMAX, int NTOK>
+template <int HD, int NTA, bool KV8, int GMAX, int NTOK, int GT>
 __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restrict__ QB, const float* __restrict__ k_cache,
                                                             const float* __restrict__ v_cache, int n_heads, int n_kv,
                                                             int max_seq, int pos0, int S, int t0, int TT, int n_chunks,
@@ -773,7 +813,7 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
   constexpr int LPR = HD / 4, RPI = NTA / LPR, C = 8192 / HD, NR = C / RPI, NW = NTA / 64;
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int c = blockIdx.x, kvh = blockIdx.y, G = n_heads / n_kv;
+  const int c = blockIdx.x, kvh = blockIdx.y, G = GT > 0 ? GT : n_heads / n_kv;
   const int sl0 = blockIdx.z * TT, sl1 = min(sl0 + TT, S - t0);   // tile-launch-relative tokens
   const int p0 = c * C;
   const int np_max = min(C, pos0 + t0 + sl1 - p0);
@@ -785,25 +825,29 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
   const size_t hstride = (size_t)max_seq * HD;
   const float* kg = k_cache + (size_t)kvh * hstride + 4 * cc;
   const float* vg = v_cache + (size_t)kvh * hstride + 4 * cc;
+  // K rows and q heads in the reduce-scatter's register order
+  // (ReduceScatter): K register i holds row (i ^ pi) * RPI + sub, q register
+  // h of a group of four head (h ^ ph); V rows stay in order (the P.V chain
+  // runs over i).  The q rows arrive normalized and rotated, so no step here
+  // needs the lanes of a row on one head.
+  constexpr int NV = 4 * NR;
+  const int rsp = rs_perm<NV, LPR / 2>(lane), pi = rsp % NR, ph = rsp / NR;
   float4 kr[NR], vr[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
-    const int j = i * RPI + sub;
+    const int j = i * RPI + sub, jk = (i ^ pi) * RPI + sub;
     kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     vr[i] = kr[i];
-    if (j < np_max) {
-      if constexpr (KV8) {
-        const size_t r = (size_t)kvh * max_seq + p0 + j;
-        kr[i] = KvQ8(const_cast<float*>(k_cache), n_kv, max_seq, HD).load(r, HD, cc);
-        vr[i] = KvQ8(const_cast<float*>(v_cache), n_kv, max_seq, HD).load(r, HD, cc);
-      } else {
-        kr[i] = *(const float4*)(kg + (size_t)(p0 + j) * HD);
-        vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
-      }
+    if constexpr (KV8) {
+      const size_t r = (size_t)kvh * max_seq + p0;
+      if (jk < np_max) kr[i] = KvQ8(const_cast<float*>(k_cache), n_kv, max_seq, HD).load(r + jk, HD, cc);
+      if (j < np_max) vr[i] = KvQ8(const_cast<float*>(v_cache), n_kv, max_seq, HD).load(r + j, HD, cc);
+    } else {
+      if (jk < np_max) kr[i] = *(const float4*)(kg + (size_t)(p0 + jk) * HD);
+      if (j < np_max) vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
     }
   }
   const float inv_sqrt = 1.0f / sqrtf((float)HD);
-  constexpr int NV = 4 * NR;
   constexpr int KSH = (LPR == 64 ? 6 : 5) - (NV == 32 ? 5 : NV == 16 ? 4 : 3);
   // NTOK tokens per pass (each with the decode arithmetic of one token): their
   // softmax rows spread over all waves and they share the barriers.  Tokens
@@ -819,7 +863,11 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
 #pragma unroll
       for (int h = 0; h < GMAX; ++h) {
         q4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (h < G) q4[h] = *(const float4*)(QB + (size_t)s * n_heads * HD + (size_t)(kvh * G + h) * HD + 4 * cc);
+        if ((h & ~3) < G) {
+          const int hs = (h & ~3) | ((h & 3) ^ ph);
+          const float* qp = QB + (size_t)s * n_heads * HD + (size_t)(kvh * G + hs) * HD + 4 * cc;
+          q4[h] = *(const float4*)(hs < G ? qp : attn_zero_row);
+        }
       }
       float* scu = sc + u * G * C;
 #pragma unroll
@@ -838,7 +886,7 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
             v[hh * NR + i] = pp;
           }
         }
-        const float r = ReduceScatter<NV, LPR / 2>::run(v, lane);
+        const float r = ReduceScatter<NV, LPR / 2>::run(v);
         const int k = (lane & (LPR - 1)) >> KSH;
         const int h = hg + k / NR, j = (k % NR) * RPI + sub;
         if (h < G && (lane & ((1 << KSH) - 1)) == 0) scu[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
@@ -850,7 +898,7 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
       const int np = min(C, pos0 + t0 + sl + u + 1 - p0);
       float* row = sc + (u * G + h) * C;
       float x = lane < C ? row[lane] : -INFINITY;
-      float m = wave_max(x);
+      float m = wave_max_nonan(x);
       float e = (lane < np) ? hx_exp(x - m) : 0.0f;
       float l = wave_sum(e);
       if (lane < C) row[lane] = e;
@@ -1389,12 +1437,18 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
       4 * (NTOK * ((size_t)G * (8192 / hd) + 2 * G + (ATTN_NT / 64) * 4 * (size_t)hd) + 8);
   const size_t merge_lds = 4 * ((size_t)n_chunks + 256 + 4);
   dim3 g1(n_chunks, n_kv, (n + TT - 1) / TT), g2(n * n_heads, hd / 64);
-#define HH_PSPLIT(HDV, KV, GM)                                                                              \
-  hipLaunchKernelGGL((k_attn_prefill_split<HDV, ATTN_NT, KV, GM, HDV == 128 ? 4 : 1>), g1, dim3(ATTN_NT),      \
+#define HH_PSPLIT(HDV, KV, GM, GTV)                                                                          \
+  hipLaunchKernelGGL((k_attn_prefill_split<HDV, ATTN_NT, KV, GM, HDV == 128 ? 4 : 1, GTV>), g1, dim3(ATTN_NT), \
                      split_lds, s, QB, k_cache, v_cache, n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, \
                      PML)
-#define HH_PSPLIT_G(HDV, KV) \
-  do { if (G <= 4) HH_PSPLIT(HDV, KV, 4); else HH_PSPLIT(HDV, KV, 8); } while (0)
+  // group sizes 4 and 8 get exact trip counts (GT), others read G at run time
+#define HH_PSPLIT_G(HDV, KV)                                          \
+  do {                                                                \
+    if (G == 4) HH_PSPLIT(HDV, KV, 4, 4);                             \
+    else if (G < 4) HH_PSPLIT(HDV, KV, 4, 0);                         \
+    else if (G == 8) HH_PSPLIT(HDV, KV, 8, 8);                        \
+    else HH_PSPLIT(HDV, KV, 8, 0);                                    \
+  } while (0)
   if (hd == 128) {
     if (kv_q8) HH_PSPLIT_G(128, true); else HH_PSPLIT_G(128, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
