@@ -763,10 +763,14 @@ int hh_gemv_q8(hh_ctx* c, int type, const void* w, int64_t n_rows, int64_t n_col
   if (n_rows <= 0 || n_rows > (1ll << 30)) return fail(HH_ERR_DIM, "bad n_rows");
   int P = (int)n_cols / el;
   int rows = gemv_rows_for((int)n_rows, P);
-  // Where one workgroup per CU would stream more than 4 units per lane, use
-  // ~3/4 of a unit per lane and many more workgroups instead (151936 x 2048:
-  // Q1_0 19.5 -> 17.3 us, Q2_0 24.7 -> 19.9 us, PTQ1_0 32.1 -> 29.4 us).
-  if (rows * P > 4 * 1024) rows = std::max(1, 768 / P);
+  // Where one workgroup per CU would stream more than 4 units per lane, give
+  // every lane of a workgroup exactly one unit and launch many more
+  // workgroups instead (151936 x 2048 against one workgroup per CU: Q1_0
+  // 19.5 -> 14.1 us, Q2_0 24.7 -> 19.0 us; 1024 units per workgroup beat
+  // 768: Q1_0 15.6 -> 14.1 us, Q8_0 62.8 -> 58.4 us, and beat 384, 512, 896,
+  // 1192, 1536, 2048 and 2376, which leave lanes idle or take the
+  // multi-unit kernels).
+  if (rows * P > 4 * 1024) rows = std::max(1, 1024 / P);   // 1024 = lanes per GEMV workgroup
   GemvArgs a = gemv_base((const uint8_t*)w, (int)n_rows, (int)n_cols, rows);
   a.act = xq8;
   a.y = y;
