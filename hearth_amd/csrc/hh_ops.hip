@@ -305,7 +305,7 @@ template <int N> HH_DEV float pairwise_tree(float* t) {
 
 // Zeros that stand in for K/V rows a split workgroup does not hold, so that
 // its loads need no branch (never written).
-__device__ __align__(16) float attn_zero_row[4];
+__device__ __align__(32) float attn_zero_row[8];   // also a zero StepState stand-in (state_lanes)
 
 // Q8_0 KV rows (KV8): the cache holds int8 values [n_kv][max_seq][hd] followed
 // by the f16 block scales [n_kv][max_seq][hd/32].  A lane's float4 slice of a
@@ -566,8 +566,11 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   const int qh = blockIdx.x, d = blockIdx.y * 64 + lane;
   const int G = a.n_heads / a.n_kv, kvh = qh / G, h = qh % G;
   constexpr int C = (256 / (HD / 4)) * 8;
-  const int seq = a.fixed_seq > 0 ? a.fixed_seq : a.state->pos + 1;
-  const int n_active = (seq + C - 1) / C;
+  // The step position is a vector load among the others (a scalar load's
+  // wait would also cover the kernel arguments, putting its round trip ahead
+  // of every load below); the loads of the first 64 splits clamp to the grid,
+  // not to the active splits, so no address waits for it.
+  const int sv = state_lanes(a.state ? (const void*)a.state : (const void*)attn_zero_row);
   const size_t hb = (size_t)kvh * a.max_splits * G + h;
   const size_t tstride = (size_t)G * HD;
   const float* pb = a.part_o + hb * HD + d;
@@ -580,15 +583,17 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   float2 ml0 = make_float2(-INFINITY, 0.0f);
   float g = 0.0f;
   if (wid == 0) {
-    ml0 = *(const float2*)(a.part_ml + (hb + (size_t)min(lane, n_active - 1) * G) * 2);
+    ml0 = *(const float2*)(a.part_ml + (hb + (size_t)min(lane, a.max_splits - 1) * G) * 2);
     if (a.gated) g = a.qkv[(size_t)qh * 2 * HD + HD + d];
   }
   float pv[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int t = min(wid + 4 * i, n_active - 1);
+    const int t = min(wid + 4 * i, a.max_splits - 1);
     pv[i] = pb[(size_t)t * tstride];
   }
+  const int seq = a.fixed_seq > 0 ? a.fixed_seq : __builtin_amdgcn_readfirstlane(sv) + 1;
+  const int n_active = (seq + C - 1) / C;
   if (wid == 0) {
     float M = lane < n_active ? ml0.x : -INFINITY;
     for (int t = lane + 64; t < n_active; t += 64) M = fmaxf(M, a.part_ml[(hb + (size_t)t * G) * 2]);
