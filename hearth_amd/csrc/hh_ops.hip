@@ -972,82 +972,104 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
   }
 }
 
-// Prefill attention, merge pass: k_attn_merge's arithmetic for token t0 + sl
-// (blockIdx.x = sl * n_heads + qh), writing the Q8_0 row of attn_output's
+// Prefill attention, merge pass: k_attn_merge's arithmetic for token t0 + sl,
+// one wave per (token, query head): pair blockIdx.x * 4 + wave = sl * n_heads
+// + qh.  Lane l holds columns CPL*l .. CPL*l + CPL-1 (CPL = HD / 64) and runs
+// the four split chains of k_attn_merge's four waves itself (chain g: splits
+// t = g (mod 4), fma in increasing t), then ((P0 + P1) + (P2 + P3)) / L.  M and
+// L are k_attn_merge's wave-0 pass.  Writes the Q8_0 row of attn_output's
 // input in the GEMM's split layout.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restrict__ PO, const float* __restrict__ PML,
-                                                            int n_heads, int n_kv, int n_chunks, int pos0, int t0,
+                                                            int n_heads, int n_kv, int n_chunks, int pos0, int t0, int n,
                                                             const float* __restrict__ gate, int gate_row,
                                                             int8_t* __restrict__ yq, float* __restrict__ yd,
                                                             float* __restrict__ yf) {
+  constexpr int CPL = HD / 64, C = 8192 / HD;
   extern __shared__ __align__(16) float wm[];
-  float* wts = wm;                         // n_chunks
-  float* pw = wm + n_chunks;               // 4 x 64
-  float* sL = pw + 256;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int sl = blockIdx.x / n_heads, qh = blockIdx.x % n_heads, d = blockIdx.y * 64 + lane;
+  float* wts = wm + wid * n_chunks;        // this wave's split weights
+  const int pair = blockIdx.x * 4 + wid;
+  const bool live = pair < n * n_heads;    // uniform per wave
+  const int sl = live ? pair / n_heads : 0, qh = pair % n_heads;
   const int G = n_heads / n_kv, kvh = qh / G, h = qh % G;
-  constexpr int C = 8192 / HD;
   const int s = t0 + sl, seq = pos0 + s + 1;
-  const int n_active = (seq + C - 1) / C;
+  const int n_active = live ? (seq + C - 1) / C : 0;
   const size_t hb = (size_t)(sl * n_kv + kvh) * n_chunks * G + h;
   const size_t tstride = (size_t)G * HD;
-  const float* pb = PO + hb * HD + d;
-  float pv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int t = wid + 4 * i;
-    pv[i] = t < n_active ? pb[(size_t)t * tstride] : 0.0f;
+  const int d0 = CPL * lane;
+  const float* pb = PO + hb * HD + d0;
+  float M = -INFINITY;
+  for (int t = lane; t < n_active; t += 64) M = fmaxf(M, PML[(hb + (size_t)t * G) * 2]);
+  M = wave_max(M);
+  float L = 0.0f;
+  for (int t = lane; t < n_active; t += 64) {
+    float e = hx_exp(PML[(hb + (size_t)t * G) * 2] - M);
+    wts[t] = e;
+    L += e * PML[(hb + (size_t)t * G) * 2 + 1];
   }
-  if (wid == 0) {
-    float M = -INFINITY;
-    for (int t = lane; t < n_active; t += 64) M = fmaxf(M, PML[(hb + (size_t)t * G) * 2]);
-    M = wave_max(M);
-    float L = 0.0f;
-    for (int t = lane; t < n_active; t += 64) {
-      float e = hx_exp(PML[(hb + (size_t)t * G) * 2] - M);
-      wts[t] = e;
-      L += e * PML[(hb + (size_t)t * G) * 2 + 1];
-    }
-    L = wave_sum(L);
-    if (lane == 0) *sL = L;
-  }
+  L = wave_sum(L);
   __syncthreads();
-  float P = 0.0f;
-  for (int tt0 = 0; tt0 < n_active; tt0 += 64) {
-    if (tt0 > 0) {
+  float P[4][CPL];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int t = tt0 + wid + 4 * i;
-        pv[i] = t < n_active ? pb[(size_t)t * tstride] : 0.0f;
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) P[g][k] = 0.0f;
+  for (int tb = 0; tb < n_active; tb += 16) {
+    float pv[16][CPL];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float* src = pb + (size_t)min(tb + i, n_active - 1) * tstride;
+      if constexpr (CPL == 2) {
+        const float2 v = *(const float2*)src;
+        pv[i][0] = v.x; pv[i][1] = v.y;
+      } else {
+        const float4 v = *(const float4*)src;
+        pv[i][0] = v.x; pv[i][1] = v.y; pv[i][2] = v.z; pv[i][3] = v.w;
       }
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int t = tt0 + wid + 4 * i;
-      if (t < n_active) P = fmaf(wts[t], pv[i], P);
+      const int t = tb + i;
+      if (t < n_active) {
+        const float w = wts[t];
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) P[i & 3][k] = fmaf(w, pv[i][k], P[i & 3][k]);
+      }
     }
   }
-  pw[wid * 64 + lane] = P;
-  __syncthreads();
-  if (wid != 0) return;
-  float o = (pw[lane] + pw[64 + lane]) + (pw[128 + lane] + pw[192 + lane]);
-  o = o * (1.0f / *sL);
-  if (gate) {   // qwen35.rs:1627-1629, as k_attn_merge
-    const float g = gate[(size_t)s * gate_row + (size_t)qh * 2 * HD + HD + d];
-    o = o / (1.0f + hx_exp(-g));
+  if (!live) return;
+  const float rl = 1.0f / L;
+  float o[CPL], gv[CPL];
+  if (gate) {
+    const float* gp = gate + (size_t)s * gate_row + (size_t)qh * 2 * HD + HD + d0;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) gv[k] = gp[k];
+  }
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    o[k] = (P[0][k] + P[1][k]) + (P[2][k] + P[3][k]);
+    o[k] = o[k] * rl;
+    if (gate) o[k] = o[k] / (1.0f + hx_exp(-gv[k]));   // qwen35.rs:1627-1629, as k_attn_merge
   }
   if (yf) {   // folded model: rotated and quantized by k_rot_q8_rows
-    yf[(size_t)s * n_heads * HD + qh * HD + d] = o;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) yf[(size_t)s * n_heads * HD + qh * HD + d0 + k] = o[k];
     return;
   }
-  const float am = group_max<32>(fabsf(o));
-  const float scq = q8_scale(am);
-  const int q = q8_round_r(o, scq, q8_rcp(scq));
-  const int e = qh * HD + d, K = n_heads * HD;
-  yq[(size_t)s * K + e] = (int8_t)q;
-  if ((lane & 31) == 0) yd[(size_t)s * (K / 32) + (e >> 5)] = h2f(f2h(scq));
+  // one Q8_0 block = 32 columns = 32 / CPL lanes
+  float am = fabsf(o[0]);
+#pragma unroll
+  for (int k = 1; k < CPL; ++k) am = fmaxf(am, fabsf(o[k]));
+  am = group_max<32 / CPL>(am);
+  const float scq = q8_scale(am), rc = q8_rcp(scq);
+  const int e = qh * HD + d0, K = n_heads * HD;
+  uint32_t word = 0;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) word |= ((uint32_t)q8_round_r(o[k], scq, rc) & 0xffu) << (8 * k);
+  if constexpr (CPL == 2) *(uint16_t*)(yq + (size_t)s * K + e) = (uint16_t)word;
+  else *(uint32_t*)(yq + (size_t)s * K + e) = word;
+  if ((lane & (32 / CPL - 1)) == 0) yd[(size_t)s * (K / 32) + (e >> 5)] = h2f(f2h(scq));
 }
 
 // ---------------------------------------------------------------------------
@@ -1440,8 +1462,8 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
   if (G > 8 || n_kv * G != n_heads) return 1;
   const size_t split_lds =
       4 * (NTOK * ((size_t)G * (8192 / hd) + 2 * G + (ATTN_NT / 64) * 4 * (size_t)hd) + 8);
-  const size_t merge_lds = 4 * ((size_t)n_chunks + 256 + 4);
-  dim3 g1(n_chunks, n_kv, (n + TT - 1) / TT), g2(n * n_heads, hd / 64);
+  const size_t merge_lds = 4 * (4 * (size_t)n_chunks);
+  dim3 g1(n_chunks, n_kv, (n + TT - 1) / TT), g2((n * n_heads + 3) / 4);
 #define HH_PSPLIT(HDV, KV, GM, GTV)                                                                          \
   hipLaunchKernelGGL((k_attn_prefill_split<HDV, ATTN_NT, KV, GM, HDV == 128 ? 4 : 1, GTV>), g1, dim3(ATTN_NT), \
                      split_lds, s, QB, k_cache, v_cache, n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, \
@@ -1457,11 +1479,11 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
   if (hd == 128) {
     if (kv_q8) HH_PSPLIT_G(128, true); else HH_PSPLIT_G(128, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, gate, gate_row, yq, yd, yf);
+                       t0, n, gate, gate_row, yq, yd, yf);
   } else if (hd == 256) {
     if (kv_q8) HH_PSPLIT_G(256, true); else HH_PSPLIT_G(256, false);
     hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, gate, gate_row, yq, yd, yf);
+                       t0, n, gate, gate_row, yq, yd, yf);
   } else {
     return 1;
   }
