@@ -754,6 +754,41 @@ __global__ __launch_bounds__(256) void k_silu_q8_rows(const float* __restrict__ 
   }
 }
 
+// k_silu_q8_rows on float4 slices (F % 1024 == 0): lane l of pass p takes
+// elements 4(256p + l) .. +3, so a Q8_0 block is 8 lanes and its max a
+// group max over them (exact: max does not depend on the order); four passes'
+// loads are issued together.  Same per-element arithmetic.
+__global__ __launch_bounds__(256) void k_silu_q8_rows4(const float* __restrict__ GU, int F, int8_t* __restrict__ xq,
+                                                       float* __restrict__ xd, float* __restrict__ yf) {
+  const int s = blockIdx.x, tid = threadIdx.x;
+  const float* g = GU + (size_t)s * 2 * F;
+  const int np = F / 1024;
+#pragma unroll 4
+  for (int p = 0; p < np; ++p) {
+    const int i = 4 * (256 * p + tid);
+    const float4 gv4 = *(const float4*)(g + i), uv4 = *(const float4*)(g + F + i);
+    const float gv[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uv[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
+    float h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float sg = gv[k] / (1.0f + hx_exp(-gv[k]));
+      h[k] = sg * uv[k];
+    }
+    if (yf) {   // folded model: rotated and quantized by k_rot_q8_rows
+      *(float4*)(yf + (size_t)s * F + i) = make_float4(h[0], h[1], h[2], h[3]);
+      continue;
+    }
+    float am = fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3])));
+    am = group_max<8>(am);
+    const float sc = q8_scale(am), rc = q8_rcp(sc);
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) word |= ((uint32_t)q8_round_r(h[k], sc, rc) & 0xffu) << (8 * k);
+    *(uint32_t*)(xq + (size_t)s * F + i) = word;
+    if ((tid & 7) == 0) xd[(size_t)s * (F / 32) + (i >> 5)] = h2f(f2h(sc));
+  }
+}
+
 __global__ void k_add_rows(float* __restrict__ H, const float* __restrict__ T, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) H[i] = H[i] + T[i];   // mod.rs:718-720, :776-778
@@ -1422,7 +1457,8 @@ int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int
 
 int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, float* yf, hipStream_t s) {
   if (F % 256 != 0) return 1;
-  hipLaunchKernelGGL(k_silu_q8_rows, dim3(S), dim3(256), 0, s, GU, F, xq, xd, yf);
+  if (F % 1024 == 0) hipLaunchKernelGGL(k_silu_q8_rows4, dim3(S), dim3(256), 0, s, GU, F, xq, xd, yf);
+  else hipLaunchKernelGGL(k_silu_q8_rows, dim3(S), dim3(256), 0, s, GU, F, xq, xd, yf);
   return ok();
 }
 
