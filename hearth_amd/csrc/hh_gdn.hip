@@ -341,7 +341,10 @@ HH_DEV float sum8_in_order(float p) {   // lanes 8g: ((((0 + p0) + p1) + ...) + 
   return s;
 }
 HH_DEV float from_group_base8(float v) {   // every lane <- lane (lane & ~7)
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x0018));
+  // quad broadcast of lane 4q, then banks 1 and 3 of each row (lanes 4-7,
+  // 12-15) take lane - 4: two DPP moves, no LDS round trip
+  const int q = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x00, 0xF, 0xF, false);
+  return __int_as_float(__builtin_amdgcn_update_dpp(q, q, 0x114, 0xF, 0xA, false));
 }
 __global__ __launch_bounds__(256) void k_gdn_rec_rows(GdnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -390,23 +393,41 @@ __global__ __launch_bounds__(256) void k_gdn_rec_rows(GdnArgs a) {
     float ob[TB], dec[TB];
 #pragma unroll
     for (int t = 0; t < TB; ++t) dec[t] = hx_exp(cg[t]);
+    // token t's k and q slices sit in registers, token t + 1's are read from
+    // LDS while token t computes (the LDS round trip is off the state chain)
+    float kc[16], qc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      kc[r] = kvb[blk & 1][0][ic * 16 + r];
+      qc[r] = kvb[blk & 1][0][hd + ic * 16 + r];
+    }
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
       if (t >= nt) break;   // uniform
-      const float* kk = kvb[blk & 1][t] + ic * 16;
-      const float* qq = kk + hd;
+      float kn[16], qn[16];
+      if (t + 1 < TB) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          kn[r] = kvb[blk & 1][t + 1][ic * 16 + r];
+          qn[r] = kvb[blk & 1][t + 1][hd + ic * 16 + r];
+        }
+      }
       float dp = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp += sreg[r] * kk[r];
+      for (int r = 0; r < 16; ++r) dp += sreg[r] * kc[r];
       const float dot = from_group_base8(sum8_in_order(dp));
       const float bd = cb[t] * (cv[t] - dot);
       float op = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        sreg[r] = sreg[r] * dec[t] + kk[r] * bd;
-        op += sreg[r] * qq[r];
+        sreg[r] = sreg[r] * dec[t] + kc[r] * bd;
+        op += sreg[r] * qc[r];
       }
       ob[t] = sum8_in_order(op);
+      if (t + 1 < TB) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { kc[r] = kn[r]; qc[r] = qn[r]; }
+      }
     }
     if (ic == 0) {
 #pragma unroll
