@@ -191,6 +191,29 @@ template <int O> HH_DEV int bfly_xchg(int v) {
 }
 template <int O> HH_DEV float bfly_xchg(float v) { return __int_as_float(bfly_xchg<O>(__float_as_int(v))); }
 
+// The value of lane (l ^ O), O a power of two: DPP within a 16-lane row for
+// O <= 8 (quad_perm for 1 and 2, row_ror:8 for 8, row_shl:4 / row_shr:4 by the
+// lane's bit 2 for 4), an LDS permute beyond.  The whole wave must be active.
+template <int O> HH_DEV float xor_lane(float v) {
+  const int x = __float_as_int(v);
+  if constexpr (O == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  else if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  else if constexpr (O == 4) {
+    // banks 0 and 2 of each row (lane bit 2 clear) read lane + 4, then banks
+    // 1 and 3 read lane - 4 over the first result
+    const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0x5, false);
+    return __int_as_float(__builtin_amdgcn_update_dpp(up, x, 0x114, 0xF, 0xA, false));
+  } else if constexpr (O == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+  else if constexpr (O == 16) {   // v_permlane16_swap(x, x): {rows 0,0,2,2 of x; rows 1,1,3,3 of x}
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+  } else {                        // O == 32: v_permlane32_swap(x, x): {low half twice; high half twice}
+    static_assert(O == 32, "offset");
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
+
 // Reductions over aligned groups of W lanes (W power of two <= 64); every
 // lane of a group ends with the group's value.
 template <int W> HH_DEV float group_sum(float v) {

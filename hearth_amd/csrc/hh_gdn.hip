@@ -24,6 +24,34 @@ namespace {
 
 HH_DEV float softplus_f(float x) { return x > 20.0f ? x : hx_log(1.0f + hx_exp(x)); }
 
+// N wave sums at once, as a reduce-scatter with ascending offsets: at offset
+// O a lane keeps one half of its values (the upper half where its offset bit
+// is set) and adds the partner's copy; once one value is left the remaining
+// offsets are a plain butterfly.  Each value's additions pair the same lane
+// groups as wave_sum's, so lane l returns wave_sum of value
+// k = sum_i bit_i(l) * N / 2^(i+1) (N = 8: 4 b0 + 2 b1 + b2).
+template <int N, int O = 1> HH_DEV float rs_asc(float* v, int lane) {
+  if constexpr (N > 1) {
+    const bool up = (lane & O) != 0;
+#pragma unroll
+    for (int k = 0; k < N / 2; ++k) {
+      const float send = up ? v[k] : v[k + N / 2];
+      const float keep = up ? v[k + N / 2] : v[k];
+      v[k] = keep + xor_lane<O>(send);
+    }
+    return rs_asc<N / 2, 2 * O>(v, lane);
+  } else {
+    float x = v[0];
+    if constexpr (O <= 1) x += xor_lane<1>(x);
+    if constexpr (O <= 2) x += xor_lane<2>(x);
+    if constexpr (O <= 4) x += xor_lane<4>(x);
+    if constexpr (O <= 8) x += xor_lane<8>(x);
+    if constexpr (O <= 16) x += xor_lane<16>(x);
+    if constexpr (O <= 32) x += xor_lane<32>(x);
+    return x;
+  }
+}
+
 // Token s = blockIdx.y of a batched prefill: conv + silu + L2 norm of every
 // channel, and g / beta per v-head.  The window's earlier inputs come from the
 // projection rows of tokens s-1, s-2, ... and, before the first token, from
@@ -97,11 +125,9 @@ __global__ __launch_bounds__(256) void k_gdn_prep_rows(GdnArgs a) {
       if (4 * (tid + 256 * j) + 4096 * c < d)
         ss[j] += hx[j][c].x * hx[j][c].x + hx[j][c].y * hx[j][c].y + hx[j][c].z * hx[j][c].z + hx[j][c].w * hx[j][c].w;
   }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) ss[j] = wave_sum(ss[j]);
-  if (lane == 0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red[wid + 4 * j] = ss[j];
+  {   // the four wave sums at once: lane l < 4 holds value 2 b0 + b1
+    const float x = rs_asc<4>(ss, lane);
+    if (lane < 4) red[wid + 4 * (2 * (lane & 1) + ((lane >> 1) & 1))] = x;
   }
   __syncthreads();
   const float inv = 1.0f / sqrtf(tree16(red) / (float)d + a.eps);
@@ -125,18 +151,15 @@ __global__ __launch_bounds__(256) void k_gdn_prep_rows(GdnArgs a) {
     }
   }
   __shared__ float redb[16];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sa[j] = wave_sum(sa[j]);
-    sb[j] = wave_sum(sb[j]);
-  }
+  // the eight wave sums at once: lane l < 8 holds value 4 b0 + 2 b1 + b2
+  // (values 0-3 alpha j, 4-7 beta j)
+  float v8[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+  const float x8 = rs_asc<8>(v8, lane);
   __syncthreads();   // red reused
-  if (lane == 0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      red[wid + 4 * j] = sa[j];
-      redb[wid + 4 * j] = sb[j];
-    }
+  if (lane < 8) {
+    const int k = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);
+    if (k < 4) red[wid + 4 * k] = x8;
+    else redb[wid + 4 * (k - 4)] = x8;
   }
   __syncthreads();
   if (tid == 0) {
