@@ -165,8 +165,11 @@ __global__ __launch_bounds__(256) void k_gdn_prep_rows(GdnArgs a) {
   if (tid == 0) {
     const float A = tree16(red);
     const float B = tree16(redb);
-    a.ab[(size_t)s * 2 * a.n_v + h] = softplus_f(A + a.dt_bias[h]) * a.ssm_a[h];
+    const float gg = softplus_f(A + a.dt_bias[h]) * a.ssm_a[h];
+    a.ab[(size_t)s * 2 * a.n_v + h] = gg;
     a.ab[(size_t)s * 2 * a.n_v + a.n_v + h] = 1.0f / (1.0f + hx_exp(-B));
+    // the decay once per (token, head) rather than in each of the 512 recurrence lanes
+    a.dec_rows[(size_t)s * a.n_v + h] = hx_exp(gg);
   }
 }
 
@@ -392,7 +395,7 @@ __global__ __launch_bounds__(256) void k_gdn_rec_rows(GdnArgs a) {
       const size_t sl = (size_t)min(blk * TB + t, S - 1);   // unconditional loads
       nkq[t] = kq0[sl * 2 * kdim];
       nv[t] = v0[sl * vdim];
-      ng[t] = a.ab[sl * 2 * a.n_v + h];
+      ng[t] = a.dec_rows[sl * a.n_v + h];
       nb[t] = a.ab[sl * 2 * a.n_v + a.n_v + h];
     }
   };
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(256) void k_gdn_rec_rows(GdnArgs a) {
     const int nt = min(TB, S - blk * TB);
     float ob[TB], dec[TB];
 #pragma unroll
-    for (int t = 0; t < TB; ++t) dec[t] = hx_exp(cg[t]);
+    for (int t = 0; t < TB; ++t) dec[t] = cg[t];   // exp(g), from k_gdn_prep_rows
     // token t's k and q slices sit in registers, token t + 1's are read from
     // LDS while token t computes (the LDS round trip is off the state chain)
     float kc[16], qc[16];

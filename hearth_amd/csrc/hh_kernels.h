@@ -174,6 +174,7 @@ struct GdnArgs {
   float* out_f32;         // non-null: the gated-norm output as f32 [v_dim] instead (folded models)
   // batched prefill scratch rows (k_gdn_prep_rows -> recurrence): per token
   float* ab;              // [S][2*n_v] g, beta
+  float* dec_rows;        // [S][n_v] exp(g), the recurrence's decay (k_gdn_prep_rows -> k_gdn_rec_rows)
   float* qk;              // [S][2*k_dim] conv+silu+l2norm q,k
   float* vconv;           // [S][v_dim] conv+silu v
   const float* z;         // [v_dim] gate projection

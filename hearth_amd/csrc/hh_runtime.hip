@@ -539,7 +539,8 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
                oPO = take((size_t)TA * c.n_kv_heads * n_chunks * G * hd * 4),
                oPML = take((size_t)TA * c.n_kv_heads * n_chunks * G * 2 * 4),
                oGQK = take(hyb ? (size_t)S * 2 * kdim * 4 : 0), oGV = take(hyb ? (size_t)S * vdim * 4 : 0),
-               oGAB = take(hyb ? (size_t)S * 2 * c.ssm_n_v_heads * 4 : 0), oGO = take(hyb ? (size_t)S * vdim * 4 : 0),
+               oGAB = take(hyb ? (size_t)S * 2 * c.ssm_n_v_heads * 4 : 0),
+               oGDEC = take(hyb ? (size_t)S * c.ssm_n_v_heads * 4 : 0), oGO = take(hyb ? (size_t)S * vdim * 4 : 0),
                oRot = take(c.had_block > 0 ? (size_t)S * std::max(std::max(vdim, nq), F) * 4 : 0),
                oChunk = take(hyb && m->gdn_chunked ? hh_gdn_chunk_scratch_bytes(c.ssm_n_v_heads, S) : 0);
   if (off > m->pf_cap) {
@@ -597,6 +598,7 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       ga.qk = (float*)(B + oGQK);
       ga.vconv = (float*)(B + oGV);
       ga.ab = (float*)(B + oGAB);
+      ga.dec_rows = (float*)(B + oGDEC);
       ga.pos0 = pos0;
       ga.S = S;
       ga.row_in = L.n_in;
