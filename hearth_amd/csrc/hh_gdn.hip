@@ -53,118 +53,152 @@ template <int N, int O = 1> HH_DEV float rs_asc(float* v, int lane) {
 }
 
 // Token s = blockIdx.y of a batched prefill: conv + silu + L2 norm of every
-// channel, and g / beta per v-head.  The window's earlier inputs come from the
-// projection rows of tokens s-1, s-2, ... and, before the first token, from
-// conv buffer pos0 & 1, which k_gdn_conv_advance moves on afterwards.
+// channel (g / beta per v-head: k_gdn_ab_rows).  The window's earlier inputs
+// come from the projection rows of tokens s-1, s-2, ... and, before the first
+// token, from conv buffer pos0 & 1, which k_gdn_conv_advance moves on
+// afterwards.
 __global__ __launch_bounds__(256) void k_gdn_prep_rows(GdnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int kdim = a.n_k * a.hd, vdim = a.n_v * a.hd, conv_dim = 2 * kdim + vdim;
-  const int n_conv_wg = conv_dim / 256;
   const int s = blockIdx.y;
   __shared__ float red[16];
-  if ((int)blockIdx.x < n_conv_wg) {
-    const int ch = blockIdx.x * 256 + tid;
-    const int K = a.kernel;
-    float win[8];
-    const float* cs = a.conv_state + (size_t)(a.pos0 & 1) * conv_dim * (K - 1) + (size_t)ch * (K - 1);
-    for (int t = 0; t < K - 1; ++t) {
-      const int u = s - (K - 1) + t;   // token of window slot t
-      win[t] = u >= 0 ? a.proj[(size_t)u * a.row_in + ch] : cs[s + t];
-    }
-    win[K - 1] = a.proj[(size_t)s * a.row_in + ch];
-    const float* w = a.conv_w + (size_t)ch * K;
-    float acc = 0.0f;
-    for (int t = 0; t < K; ++t) acc += w[t] * win[t];
-    float y = acc / (1.0f + hx_exp(-acc));             // silu
-    if (ch < 2 * kdim) {
-      // L2 norm over the 128-channel head this lane belongs to (2 waves per head)
-      float ss = wave_sum(y * y);
-      if (lane == 0) red[wid] = ss;
-      __syncthreads();
-      int hw = wid & ~1;
-      float tot = red[hw] + red[hw + 1];
-      float inv = 1.0f / sqrtf(tot + a.eps);
-      a.qk[(size_t)s * 2 * kdim + ch] = y * inv;
-    } else {
-      a.vconv[(size_t)s * vdim + ch - 2 * kdim] = y;
-    }
-    return;
+  const int ch = blockIdx.x * 256 + tid;
+  const int K = a.kernel;
+  float win[8];
+  const float* cs = a.conv_state + (size_t)(a.pos0 & 1) * conv_dim * (K - 1) + (size_t)ch * (K - 1);
+  for (int t = 0; t < K - 1; ++t) {
+    const int u = s - (K - 1) + t;   // token of window slot t
+    win[t] = u >= 0 ? a.proj[(size_t)u * a.row_in + ch] : cs[s + t];
   }
-  // alpha/beta of v-head h = blockIdx.x - n_conv_wg (matvec_dense :1015-1025 on
-  // rms_norm(hidden, attn_norm)).  Lane t holds the float4s at 4(t + 256j) +
-  // 4096c (the block_sumsq_f4 slots) of hidden, attn_norm and both weight rows,
-  // all loaded at once.  Order (the input projection's, k_gemv's alpha/beta
-  // epilogue): slot t + 256j sums its products over c, then element, ascending;
-  // the 64 slots of each (wave, j) by butterfly into W[wave + 4j]; tree16(W).
-  const int d = a.d;
-  const int h = (int)blockIdx.x - n_conv_wg;
+  win[K - 1] = a.proj[(size_t)s * a.row_in + ch];
+  const float* w = a.conv_w + (size_t)ch * K;
+  float acc = 0.0f;
+  for (int t = 0; t < K; ++t) acc += w[t] * win[t];
+  float y = acc / (1.0f + hx_exp(-acc));             // silu
+  if (ch < 2 * kdim) {
+    // L2 norm over the 128-channel head this lane belongs to (2 waves per head)
+    float ss = wave_sum(y * y);
+    if (lane == 0) red[wid] = ss;
+    __syncthreads();
+    int hw = wid & ~1;
+    float tot = red[hw] + red[hw + 1];
+    float inv = 1.0f / sqrtf(tot + a.eps);
+    a.qk[(size_t)s * 2 * kdim + ch] = y * inv;
+  } else {
+    a.vconv[(size_t)s * vdim + ch - 2 * kdim] = y;
+  }
+}
+
+// rs_asc's value index of lane l: k = sum_i bit_i(l) * N / 2^(i+1)
+template <int N> HH_DEV int rs_asc_index(int lane) {
+  int k = 0;
+#pragma unroll
+  for (int i = 0, w = N / 2; w >= 1; ++i, w >>= 1) k += ((lane >> i) & 1) * w;
+  return k;
+}
+
+// alpha/beta of v-head h = blockIdx.x for tokens 4 blockIdx.y .. +3
+// (matvec_dense :1015-1025 on rms_norm(hidden, attn_norm)).  Lane t holds the
+// float4s at 4(t + 256j) + 4096c (the block_sumsq_f4 slots) of each token's
+// hidden row, attn_norm and both weight rows; the weight rows and attn_norm
+// are read once for the four tokens.  Order (the input projection's, k_gemv's
+// alpha/beta epilogue): slot t + 256j sums its products over c, then element,
+// ascending; the 64 slots of each (wave, j) by butterfly into W[wave + 4j];
+// tree16(W).  The butterflies of all four tokens run as one reduce-scatter
+// per phase (rs_asc: the same pairs as wave_sum's), so each phase has one
+// barrier.
+template <int NC>   // float4 columns per slot: d <= 4096 NC
+__global__ __launch_bounds__(256) void k_gdn_ab_rows(GdnArgs a) {
+  constexpr int TB = 4;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int h = blockIdx.x, s0 = blockIdx.y * TB, d = a.d, S = a.S;
   const float* wa = a.w_alpha + (size_t)h * d;
   const float* wb = a.w_beta + (size_t)h * d;
-  constexpr int NC = 2;   // d <= 8192
-  float4 hx[4][NC], hw[4][NC], va[4][NC], vb[4][NC];
+  __shared__ float red_s[TB][16], red_a[TB][16], red_b[TB][16];
+  float4 hx[TB][4][NC], hw[4][NC], va[4][NC], vb[4][NC];
+#pragma unroll
+  for (int u = 0; u < TB; ++u) {
+    const size_t su = (size_t)min(s0 + u, S - 1);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * (tid + 256 * j) + 4096 * c;
+        hx[u][j][c] = e < d ? *(const float4*)(a.hidden + su * d + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+  }
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = 4 * (tid + 256 * j) + 4096 * c;
-      hx[j][c] = hw[j][c] = va[j][c] = vb[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+      hw[j][c] = va[j][c] = vb[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (e < d) {
-        hx[j][c] = *(const float4*)(a.hidden + (size_t)s * d + e);
         hw[j][c] = *(const float4*)(a.attn_norm + e);
         va[j][c] = *(const float4*)(wa + e);
         vb[j][c] = *(const float4*)(wb + e);
       }
     }
-  // sum of squares in block_sumsq_f4's order
-  float ss[4];
+  // sums of squares in block_sumsq_f4's order, value u*4 + j
+  float ss[TB * 4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    ss[j] = 0.0f;
+  for (int u = 0; u < TB; ++u)
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-      if (4 * (tid + 256 * j) + 4096 * c < d)
-        ss[j] += hx[j][c].x * hx[j][c].x + hx[j][c].y * hx[j][c].y + hx[j][c].z * hx[j][c].z + hx[j][c].w * hx[j][c].w;
-  }
-  {   // the four wave sums at once: lane l < 4 holds value 2 b0 + b1
-    const float x = rs_asc<4>(ss, lane);
-    if (lane < 4) red[wid + 4 * (2 * (lane & 1) + ((lane >> 1) & 1))] = x;
-  }
-  __syncthreads();
-  const float inv = 1.0f / sqrtf(tree16(red) / (float)d + a.eps);
-  float sa[4], sb[4];
+    for (int j = 0; j < 4; ++j) {
+      float q = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sa[j] = 0.0f;
-    sb[j] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      if (4 * (tid + 256 * j) + 4096 * c >= d) continue;
-      const float x[4] = {hx[j][c].x * inv * hw[j][c].x, hx[j][c].y * inv * hw[j][c].y,
-                          hx[j][c].z * inv * hw[j][c].z, hx[j][c].w * inv * hw[j][c].w};
-      const float ua[4] = {va[j][c].x, va[j][c].y, va[j][c].z, va[j][c].w};
-      const float ub[4] = {vb[j][c].x, vb[j][c].y, vb[j][c].z, vb[j][c].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sa[j] = sa[j] + ua[i] * x[i];
-        sb[j] = sb[j] + ub[i] * x[i];
-      }
+      for (int c = 0; c < NC; ++c)
+        if (4 * (tid + 256 * j) + 4096 * c < d)
+          q += hx[u][j][c].x * hx[u][j][c].x + hx[u][j][c].y * hx[u][j][c].y + hx[u][j][c].z * hx[u][j][c].z +
+               hx[u][j][c].w * hx[u][j][c].w;
+      ss[u * 4 + j] = q;
+    }
+  {
+    const float x = rs_asc<TB * 4>(ss, lane);
+    if (lane < TB * 4) {
+      const int k = rs_asc_index<TB * 4>(lane);
+      red_s[k / 4][wid + 4 * (k % 4)] = x;
     }
   }
-  __shared__ float redb[16];
-  // the eight wave sums at once: lane l < 8 holds value 4 b0 + 2 b1 + b2
-  // (values 0-3 alpha j, 4-7 beta j)
-  float v8[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
-  const float x8 = rs_asc<8>(v8, lane);
-  __syncthreads();   // red reused
-  if (lane < 8) {
-    const int k = 4 * (lane & 1) + 2 * ((lane >> 1) & 1) + ((lane >> 2) & 1);
-    if (k < 4) red[wid + 4 * k] = x8;
-    else redb[wid + 4 * (k - 4)] = x8;
+  __syncthreads();
+  // alpha / beta slot sums, value u*8 + j (alpha) and u*8 + 4 + j (beta)
+  float v[TB * 8];
+#pragma unroll
+  for (int u = 0; u < TB; ++u) {
+    const float inv = 1.0f / sqrtf(tree16(red_s[u]) / (float)d + a.eps);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        if (4 * (tid + 256 * j) + 4096 * c >= d) continue;
+        const float x[4] = {hx[u][j][c].x * inv * hw[j][c].x, hx[u][j][c].y * inv * hw[j][c].y,
+                            hx[u][j][c].z * inv * hw[j][c].z, hx[u][j][c].w * inv * hw[j][c].w};
+        const float ua[4] = {va[j][c].x, va[j][c].y, va[j][c].z, va[j][c].w};
+        const float ub[4] = {vb[j][c].x, vb[j][c].y, vb[j][c].z, vb[j][c].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sa = sa + ua[i] * x[i];
+          sb = sb + ub[i] * x[i];
+        }
+      }
+      v[u * 8 + j] = sa;
+      v[u * 8 + 4 + j] = sb;
+    }
+  }
+  {
+    const float x = rs_asc<TB * 8>(v, lane);
+    if (lane < TB * 8) {
+      const int k = rs_asc_index<TB * 8>(lane), u = k / 8, r = k % 8;
+      if (r < 4) red_a[u][wid + 4 * r] = x;
+      else red_b[u][wid + 4 * (r - 4)] = x;
+    }
   }
   __syncthreads();
-  if (tid == 0) {
-    const float A = tree16(red);
-    const float B = tree16(redb);
+  if (tid < TB && s0 + tid < S) {
+    const int s = s0 + tid;
+    const float A = tree16(red_a[tid]);
+    const float B = tree16(red_b[tid]);
     const float gg = softplus_f(A + a.dt_bias[h]) * a.ssm_a[h];
     a.ab[(size_t)s * 2 * a.n_v + h] = gg;
     a.ab[(size_t)s * 2 * a.n_v + a.n_v + h] = 1.0f / (1.0f + hx_exp(-B));
@@ -521,7 +555,11 @@ int hh_gdn_rows_launch(const GdnArgs& a, float* chunk_scratch, hipStream_t s) {
   if (conv_dim % 256 || a.hd != 128 || a.kernel > 8 || a.kernel < 2) return 1;
   if (a.d % 1024 || a.d > 8192 || a.S <= 0 || a.S > 65535) return 1;
   const int n_conv_wg = conv_dim / 256;
-  hipLaunchKernelGGL(k_gdn_prep_rows, dim3(n_conv_wg + a.n_v, a.S), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_gdn_prep_rows, dim3(n_conv_wg, a.S), dim3(256), 0, s, a);
+  if (hipGetLastError() != hipSuccess) return 1;
+  const dim3 gab(a.n_v, (a.S + 3) / 4);
+  if (a.d <= 4096) hipLaunchKernelGGL(k_gdn_ab_rows<1>, gab, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(k_gdn_ab_rows<2>, gab, dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
   hipLaunchKernelGGL(k_gdn_conv_advance, dim3(n_conv_wg), dim3(256), 0, s, a);
   if (hipGetLastError() != hipSuccess) return 1;
