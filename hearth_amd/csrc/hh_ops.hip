@@ -961,16 +961,33 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
         }
       }
       __syncthreads();
-      for (int idx = tid; idx < nt * 4 * HD; idx += NTA) {
-        const int u = idx / (4 * HD), r4 = idx % (4 * HD);
-        const int h = hg + r4 / HD;
+      if constexpr (4 * HD == NTA) {
+        // lane tid owns value r4 = tid of every token u: its partial sits at
+        // a fixed offset from token u's block, one token stride apart
+        const int h = hg + tid / HD;
         if (h < G) {
-          const float* redu = red + u * NW * 4 * HD;
-          float t[NW];
+          const size_t tok = (size_t)n_kv * n_chunks * G * HD;
+          float* dst = PO + (((size_t)sl * n_kv + kvh) * n_chunks + c) * G * HD + (size_t)hg * HD + tid;
+          for (int u = 0; u < nt; ++u) {
+            const float* redu = red + u * NW * 4 * HD;
+            float t[NW];
 #pragma unroll
-          for (int w = 0; w < NW; ++w) t[w] = redu[w * 4 * HD + r4];
-          const size_t pbase = ((size_t)((sl + u) * n_kv + kvh) * n_chunks + c) * G;
-          PO[(pbase + h) * HD + (r4 % HD)] = pairwise_tree<NW>(t);
+            for (int w = 0; w < NW; ++w) t[w] = redu[w * 4 * HD + tid];
+            dst[u * tok] = pairwise_tree<NW>(t);
+          }
+        }
+      } else {
+        for (int idx = tid; idx < nt * 4 * HD; idx += NTA) {
+          const int u = idx / (4 * HD), r4 = idx % (4 * HD);
+          const int h = hg + r4 / HD;
+          if (h < G) {
+            const float* redu = red + u * NW * 4 * HD;
+            float t[NW];
+#pragma unroll
+            for (int w = 0; w < NW; ++w) t[w] = redu[w * 4 * HD + r4];
+            const size_t pbase = ((size_t)((sl + u) * n_kv + kvh) * n_chunks + c) * G;
+            PO[(pbase + h) * HD + (r4 % HD)] = pairwise_tree<NW>(t);
+          }
         }
       }
       __syncthreads();
