@@ -710,31 +710,11 @@ __global__ __launch_bounds__(256) void k_norm_q8_rows(const float* __restrict__ 
 }
 
 // silu(g) * u of the [gate; up] rows of token s, then Q8_0 into the split
-// layout: the SILU epilogue's arithmetic (ops.rs:240-253, q8_0.rs:20-51).
-__global__ __launch_bounds__(256) void k_silu_q8_rows(const float* __restrict__ GU, int F, int8_t* __restrict__ xq,
-                                                      float* __restrict__ xd, float* __restrict__ yf) {
-  const int s = blockIdx.x, tid = threadIdx.x;
-  const float* g = GU + (size_t)s * 2 * F;
-  for (int i = tid; i < F; i += 256) {   // F % 256 == 0: whole waves
-    const float gv = g[i];
-    const float sg = gv / (1.0f + hx_exp(-gv));
-    const float h = sg * g[F + i];
-    if (yf) {   // folded model: rotated and quantized by k_rot_q8_rows
-      yf[(size_t)s * F + i] = h;
-      continue;
-    }
-    const float am = group_max<32>(fabsf(h));
-    const float sc = q8_scale(am);
-    const int q = q8_round_r(h, sc, q8_rcp(sc));
-    xq[(size_t)s * F + i] = (int8_t)q;
-    if ((i & 31) == 0) xd[(size_t)s * (F / 32) + (i >> 5)] = h2f(f2h(sc));
-  }
-}
-
-// k_silu_q8_rows on float4 slices (F % 1024 == 0): lane l of pass p takes
-// elements 4(256p + l) .. +3, so a Q8_0 block is 8 lanes and its max a
-// group max over them (exact: max does not depend on the order); four passes'
-// loads are issued together.  Same per-element arithmetic.
+// layout: the SILU epilogue's arithmetic (ops.rs:240-253, q8_0.rs:20-51), on
+// float4 slices (F % 1024 == 0): lane l of pass p takes elements
+// 4(256p + l) .. +3, so a Q8_0 block is 8 lanes and its max a group max over
+// them (exact: max does not depend on the order); four passes' loads are
+// issued together.
 __global__ __launch_bounds__(256) void k_silu_q8_rows4(const float* __restrict__ GU, int F, int8_t* __restrict__ xq,
                                                        float* __restrict__ xd, float* __restrict__ yf) {
   const int s = blockIdx.x, tid = threadIdx.x;
@@ -1450,9 +1430,8 @@ int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int
 }
 
 int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, float* yf, hipStream_t s) {
-  if (F % 256 != 0) return 1;
-  if (F % 1024 == 0) hipLaunchKernelGGL(k_silu_q8_rows4, dim3(S), dim3(256), 0, s, GU, F, xq, xd, yf);
-  else hipLaunchKernelGGL(k_silu_q8_rows, dim3(S), dim3(256), 0, s, GU, F, xq, xd, yf);
+  if (F % 1024 != 0) return 1;   // models hold d_ffn to multiples of 1024
+  hipLaunchKernelGGL(k_silu_q8_rows4, dim3(S), dim3(256), 0, s, GU, F, xq, xd, yf);
   return ok();
 }
 
