@@ -118,6 +118,9 @@ int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int
 // yf != null: silu(g) * u rows as f32 [S][F] instead of Q8_0
 int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, float* yf, hipStream_t s);
 int hh_add_rows_launch(float* H, const float* T, int64_t n, hipStream_t s);
+// H += T, then hh_norm_q8_rows_launch's output from the new H, in one pass (K % 1024 == 0, K <= 8192)
+int hh_add_norm_q8_rows_launch(float* H, const float* T, const float* w, float eps, int K, int S, int8_t* xq,
+                               float* xd, hipStream_t s);
 int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_kv, const float* q_norm,
                          const float* k_norm, float eps, const float* rope, int rope_dim, int max_seq, int pos0, int S,
                          int gated, int kv_q8, float* k_cache, float* v_cache, float* QB, hipStream_t s);

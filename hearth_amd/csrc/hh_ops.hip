@@ -709,6 +709,68 @@ __global__ __launch_bounds__(256) void k_norm_q8_rows(const float* __restrict__ 
   }
 }
 
+// The residual add then k_norm_q8_rows of the same rows, one pass: H = H + T
+// (k_add_rows' add) is kept in registers, written back, and normalized from
+// there.  Lane tid holds elements (tid + 256 i) * 4, which are both
+// block_sumsq_f4's slots (slot j sums i = j, j + 4, ... in that order) and
+// k_norm_q8_rows' quantization slices, so every sum and rounding is theirs.
+__global__ __launch_bounds__(256) void k_add_norm_q8_rows(float* __restrict__ H, const float* __restrict__ T,
+                                                          const float* __restrict__ w, float eps, int K,
+                                                          int8_t* __restrict__ xq, float* __restrict__ xd) {
+  __shared__ float red16[16];
+  const int s = blockIdx.x, tid = threadIdx.x;
+  float* h = H + (size_t)s * K;
+  const float* t = T + (size_t)s * K;
+  const int NI = K / 1024;   // <= 8
+  float4 v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i < NI) {
+      const int e = (tid + 256 * i) * 4;
+      const float4 a = *(const float4*)(h + e), b = *(const float4*)(t + e);
+      v[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);   // mod.rs:718-720, :776-778
+      *(float4*)(h + e) = v[i];
+    }
+  }
+  float ss[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ss[j] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      if (j + 4 * c < NI) {
+        const float4 x = v[j + 4 * c];
+        ss[j] += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ss[j] = wave_sum(ss[j]);
+  if ((tid & 63) == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red16[(tid >> 6) + 4 * j] = ss[j];
+  }
+  __syncthreads();
+  const float tot = tree16(red16);
+  const float inv = 1.0f / sqrtf(tot / (float)K + eps);   // ops.rs:22-23
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i < NI) {
+      const int e = (tid + 256 * i) * 4;
+      const float4 xv = v[i], wv = *(const float4*)(w + e);
+      float vv[4] = {xv.x * inv * wv.x, xv.y * inv * wv.y, xv.z * inv * wv.z, xv.w * inv * wv.w};
+      float am = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+      am = group_max<8>(am);
+      const float sc = q8_scale(am), rc = q8_rcp(sc);
+      uint32_t word = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) word |= ((uint32_t)q8_round_r(vv[k], sc, rc) & 0xffu) << (8 * k);
+      *(uint32_t*)(xq + (size_t)s * K + e) = word;
+      if ((tid & 7) == 0) xd[(size_t)s * (K / 32) + (e >> 5)] = h2f(f2h(sc));
+    }
+  }
+}
+
 // silu(g) * u of the [gate; up] rows of token s, then Q8_0 into the split
 // layout: the SILU epilogue's arithmetic (ops.rs:240-253, q8_0.rs:20-51), on
 // float4 slices (F % 1024 == 0): lane l of pass p takes elements
@@ -1432,6 +1494,13 @@ int hh_norm_q8_rows_launch(const float* X, const float* w, float eps, int K, int
 int hh_silu_q8_rows_launch(const float* GU, int F, int S, int8_t* xq, float* xd, float* yf, hipStream_t s) {
   if (F % 1024 != 0) return 1;   // models hold d_ffn to multiples of 1024
   hipLaunchKernelGGL(k_silu_q8_rows4, dim3(S), dim3(256), 0, s, GU, F, xq, xd, yf);
+  return ok();
+}
+
+int hh_add_norm_q8_rows_launch(float* H, const float* T, const float* w, float eps, int K, int S, int8_t* xq,
+                               float* xd, hipStream_t s) {
+  if (K % 1024 != 0 || K > 8192) return 1;
+  hipLaunchKernelGGL(k_add_norm_q8_rows, dim3(S), dim3(256), 0, s, H, T, w, eps, K, xq, xd);
   return ok();
 }
 

@@ -573,7 +573,14 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
                             latent ? c.had_block : 0, s));
   for (int li = 0; li < c.n_layers; ++li) {
     Layer& L = m->layers[li];
-    KTRY(norm_rows(L.attn_norm));
+    // the previous layer's ffn_down residual add runs here, fused with this
+    // layer's input norm where no Hadamard rotation sits between them
+    if (li > 0 && !had) {
+      KTRY(hh_add_norm_q8_rows_launch(H, T, L.attn_norm, c.eps, d, S, Xq, Xd, s));
+    } else {
+      if (li > 0) KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
+      KTRY(norm_rows(L.attn_norm));
+    }
     KTRY(hh_gemm_launch(m->wfmt, L.w_in, L.n_in, d, Xq, Xd, S, QKV, s));
     int k_out;
     if (L.gdn) {
@@ -625,13 +632,18 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       k_out = nq;
     }
     KTRY(hh_gemm_launch(m->wfmt, L.w_out, d, k_out, Xq, Xd, S, T, s));
-    KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
-    KTRY(norm_rows(L.ffn_norm));
+    if (!had) {
+      KTRY(hh_add_norm_q8_rows_launch(H, T, L.ffn_norm, c.eps, d, S, Xq, Xd, s));
+    } else {
+      KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
+      KTRY(norm_rows(L.ffn_norm));
+    }
     KTRY(hh_gemm_launch(m->wfmt, L.w_gu, 2 * F, d, Xq, Xd, S, GU, s));
     KTRY(hh_silu_q8_rows_launch(GU, F, S, Xq, Xd, Rot, s));
     if (had) KTRY(hh_rot_q8_rows_launch(Rot, nullptr, 0.0f, F, S, signs_of(m, F), c.had_block, 0, 0, Xq, Xd, s));
     KTRY(hh_gemm_launch(m->wfmt, L.w_down, d, F, Xq, Xd, S, T, s));
-    KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
+    // the residual add: fused into the next layer's input norm, plain after the last
+    if (li + 1 == c.n_layers) KTRY(hh_add_rows_launch(H, T, (int64_t)S * d, s));
   }
   return HH_OK;
 }
