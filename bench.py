@@ -176,6 +176,22 @@ def _generate_leg(ctx, name: str, cfg, seed: int, n_prompt: int, n_gen: int, pen
             "repeat_pen": pen, "first_tokens": [int(t) for t in toks[:8]]}
 
 
+def single_leg(ctx, name: str) -> dict:
+    """One configs leg with the same workload as config_legs (for rocprofv3 runs)."""
+    from hearth_amd import CONFIGS
+    if name == "1.7b":
+        c0 = CONFIGS["1.7b-q1"]
+        return _generate_leg(ctx, "1.7B Q1_0", c0.replace(max_seq=max(c0.max_seq, 128)), 2025, 16, 50, 1.1)
+    if name == "9b":
+        c3 = CONFIGS["9b-hybrid-q2"]
+        return _generate_leg(ctx, "9B hybrid Q2_0", c3.replace(max_seq=max(c3.max_seq, 1024)), 2027, 512, 129, 1.0)
+    if name == "27b-decode":
+        return _generate_leg(ctx, "27B hybrid PQ2_0 (decode)", CONFIGS["27b-hybrid-pq2"].replace(max_seq=8192), 2028,
+                             64, 17, 1.0)
+    return _generate_leg(ctx, "27B hybrid PQ2_0", CONFIGS["27b-hybrid-pq2"].replace(max_seq=8192), 2028, 2048, 65,
+                         1.0)
+
+
 def config_legs(ctx) -> dict:
     """BASELINE configs[0], [1], [3], [4] on the device (seeded synthetic weights).
     The prompt phase includes the last prompt token's decode step."""
@@ -266,6 +282,10 @@ def main():
                     help="skip the BASELINE configs[0,1,3,4] legs (1.7B Q1_0, GEMV microbench, 9B and 27B hybrids)")
     ap.add_argument("--hybrid-only", action="store_true",
                     help="run only the 9B hybrid leg and print its JSON (profiling)")
+    ap.add_argument("--leg", choices=("1.7b", "9b", "27b", "27b-decode"), default=None,
+                    help="run only one configs leg (1.7B Q1_0 = configs[0], 9B hybrid = configs[3], "
+                         "27B hybrid = configs[4]; 27b-decode: the 27B at 8192 context with a 64-token "
+                         "prompt and 16 decode steps, for counter runs) and print its JSON (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs one GPU per process: bench.py measures --gpus 1 only; "
@@ -278,6 +298,9 @@ def main():
         import torch
         torch.cuda.init()
     from hearth_amd import Ctx, Model, CONFIGS
+    if args.leg:
+        print(json.dumps({args.leg: single_leg(Ctx(0), args.leg)}), flush=True)
+        return
     if args.hybrid_only:
         print(json.dumps({"hybrid": hybrid_leg(Ctx(0), 2048, args.steps, args.warmup)}), flush=True)
         return

@@ -192,6 +192,9 @@ struct hh_model {
   // HH_GDN_CHUNKED=1: the batched prefill runs the GDN recurrence in chunked
   // form (fp32-rounding parity with the sequential rule instead of bit parity)
   int gdn_chunked = 0;
+  // the chunked form needs every ssm_a < 0 (its decays exp(G_t - G_s) then stay
+  // <= 1): -1 unchecked since the last weight write, 0 some ssm_a >= 0, 1 all negative
+  int ssm_a_negative = -1;
   // Hadamard fold: one device sign vector per folded width (+1 until set), and
   // the f32 hand-off of the matmul inputs that are rotated in the consumer's prologue
   float* had_signs = nullptr;
@@ -508,9 +511,33 @@ int enqueue_step(hh_model* m, hipStream_t s, int only_layer, unsigned stages) {
 #ifndef PF_ATTN_BYTES
 #define PF_ATTN_BYTES ((size_t)2 << 30)
 #endif
+// Whether every GDN layer's ssm_a is negative (read back once per weight write).
+int ssm_a_all_negative(hh_model* m, bool* ok) {
+  if (m->ssm_a_negative < 0) {
+    std::vector<float> a(m->cfg.ssm_n_v_heads);
+    int neg = 1;
+    for (const Layer& L : m->layers) {
+      if (!L.ssm_a) continue;
+      HIP_TRY(hipMemcpy(a.data(), L.ssm_a, sizeof(float) * a.size(), hipMemcpyDeviceToHost));
+      for (float v : a)
+        if (!(v < 0.0f)) neg = 0;
+    }
+    m->ssm_a_negative = neg;
+  }
+  *ok = m->ssm_a_negative == 1;
+  return HH_OK;
+}
+
 int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
   const hh_model_config& c = m->cfg;
   hipStream_t s = m->ctx->stream;
+  // HH_GDN_CHUNKED applies only where every ssm_a < 0; otherwise the
+  // sequential recurrence runs (it stays finite for any ssm_a)
+  bool chunked = false;
+  if (m->gdn_chunked) {
+    const int rc = ssm_a_all_negative(m, &chunked);
+    if (rc != HH_OK) return rc;
+  }
   const int d = c.d_model, hd = c.head_dim, nq = c.n_heads * hd, F = c.d_ffn;
   // the chunks the prompt reaches (the partials' chunk stride, shared by the
   // split and merge passes), not every chunk of the cache
@@ -542,7 +569,7 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
                oGAB = take(hyb ? (size_t)S * 2 * c.ssm_n_v_heads * 4 : 0),
                oGDEC = take(hyb ? (size_t)S * c.ssm_n_v_heads * 4 : 0), oGO = take(hyb ? (size_t)S * vdim * 4 : 0),
                oRot = take(c.had_block > 0 ? (size_t)S * std::max(std::max(vdim, nq), F) * 4 : 0),
-               oChunk = take(hyb && m->gdn_chunked ? hh_gdn_chunk_scratch_bytes(c.ssm_n_v_heads, S) : 0);
+               oChunk = take(hyb && chunked ? hh_gdn_chunk_scratch_bytes(c.ssm_n_v_heads, S) : 0);
   if (off > m->pf_cap) {
     if (m->pf_buf) HIP_TRY(hipFree(m->pf_buf));
     m->pf_buf = nullptr;
@@ -613,7 +640,7 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       ga.xq = Xq;
       ga.xd = Xd;
       ga.y_rows = Rot;
-      KTRY(hh_gdn_rows_launch(ga, m->gdn_chunked ? (float*)(B + oChunk) : nullptr, s));
+      KTRY(hh_gdn_rows_launch(ga, chunked ? (float*)(B + oChunk) : nullptr, s));
       if (had)
         KTRY(hh_rot_q8_rows_launch(Rot, nullptr, 0.0f, vdim, S, signs_of(m, vdim), c.had_block, c.ssm_n_k_heads,
                                    c.ssm_n_v_heads / c.ssm_n_k_heads, Xq, Xd, s));
@@ -674,11 +701,20 @@ int hh_ctx_create(int device_ordinal, hh_ctx** out) {
   }
   hh_ctx* c = new hh_ctx();
   c->device = device_ordinal;
-  HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
-  HIP_TRY(hipMalloc(&c->part_val, 4096 * sizeof(float)));
-  HIP_TRY(hipMalloc(&c->part_idx, 4096 * sizeof(int)));
-  HIP_TRY(hipMalloc(&c->counter, 64 * sizeof(int)));
-  HIP_TRY(hipMemset(c->counter, 0, 64 * sizeof(int)));
+  // a failure past this point releases what was created through hh_ctx_destroy
+  const int rc = [&]() -> int {
+    HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    HIP_TRY(hipMalloc(&c->part_val, 4096 * sizeof(float)));
+    HIP_TRY(hipMalloc(&c->part_idx, 4096 * sizeof(int)));
+    HIP_TRY(hipMalloc(&c->counter, 64 * sizeof(int)));
+    HIP_TRY(hipMemset(c->counter, 0, 64 * sizeof(int)));
+    return HH_OK;
+  }();
+  if (rc != HH_OK) {
+    const std::string msg = hh_last_error();
+    hh_ctx_destroy(c);
+    return fail(rc, msg);
+  }
   *out = c;
   return HH_OK;
 }
@@ -686,7 +722,7 @@ int hh_ctx_create(int device_ordinal, hh_ctx** out) {
 int hh_ctx_destroy(hh_ctx* c) {
   if (!c) return HH_OK;
   hipSetDevice(c->device);
-  hipStreamSynchronize(c->stream);
+  if (c->stream) hipStreamSynchronize(c->stream);
   hipFree(c->part_val);
   hipFree(c->part_idx);
   hipFree(c->counter);
@@ -695,7 +731,7 @@ int hh_ctx_destroy(hh_ctx* c) {
   if (c->gemm_scratch) hipFree(c->gemm_scratch);
   for (hipEvent_t e : c->ev)
     if (e) hipEventDestroy(e);
-  hipStreamDestroy(c->stream);
+  if (c->stream) hipStreamDestroy(c->stream);
   delete c;
   return HH_OK;
 }
@@ -839,7 +875,7 @@ int hh_attention(hh_ctx* c, const float* q, const float* k, const float* v, int 
     return fail(HH_ERR_DIM, "unsupported attention geometry (head_dim 128 or 256)");
   if (seq_len <= 0 || seq_len > max_seq) return fail(HH_ERR_RANGE, "seq_len out of range");
   int G = n_heads / n_kv;
-  if (G > 16) return fail(HH_ERR_DIM, "too many query heads per kv head");
+  if (G > 8) return fail(HH_ERR_DIM, "more than 8 query heads per kv head (n_heads / n_kv_heads)");
   int chunk = 8192 / hd;
   int splits = (seq_len + chunk - 1) / chunk;
   // split partials live in a context scratch buffer grown on demand; the
@@ -885,7 +921,7 @@ int hh_attention_noalloc(hh_ctx* c, const float* q, const float* k, const float*
     return fail(HH_ERR_DIM, "unsupported attention geometry (head_dim 128 or 256)");
   if (seq_len <= 0 || seq_len > max_seq) return fail(HH_ERR_RANGE, "seq_len out of range");
   const int G = n_heads / n_kv;
-  if (G > 16) return fail(HH_ERR_DIM, "too many query heads per kv head");
+  if (G > 8) return fail(HH_ERR_DIM, "more than 8 query heads per kv head (n_heads / n_kv_heads)");
   const int chunk = 8192 / hd;
   const int splits = (seq_len + chunk - 1) / chunk;
   const size_t need = sizeof(float) * (size_t)n_kv * splits * G * (hd + 2);
@@ -952,6 +988,8 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
     return fail(HH_ERR_DIM, "d_model and d_ffn must be multiples of 1024");
   if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || (c.head_dim != 128 && c.head_dim != 256))
     return fail(HH_ERR_DIM, "unsupported attention geometry (head_dim 128 or 256)");
+  if (c.n_heads / c.n_kv_heads > 8)
+    return fail(HH_ERR_DIM, "more than 8 query heads per kv head (n_heads / n_kv_heads)");
   if ((c.n_heads * c.head_dim) % 256) return fail(HH_ERR_DIM, "n_heads*head_dim must be a multiple of 256");
   if (c.max_seq <= 0) return fail(HH_ERR_DIM, "max_seq must be positive");
   if (c.kv_type != HH_F32 && c.kv_type != HH_Q8_0) return fail(HH_ERR_DTYPE, "kv_type must be F32 or Q8_0");
@@ -1235,6 +1273,7 @@ int hh_model_upload_tensor(hh_model* m, const char* name, int type, int64_t ne0,
     return fail(HH_ERR_DIM, std::string("shape mismatch for ") + name);
   HIP_TRY(hipMemcpyAsync(t->d, host, nbytes, hipMemcpyHostToDevice, m->ctx->stream));
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  m->ssm_a_negative = -1;
   return HH_OK;
 }
 
@@ -1271,6 +1310,7 @@ int hh_model_synthesize(hh_model* m, uint64_t seed) {
                          m->ctx->stream));
   }
   HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  m->ssm_a_negative = -1;
   return HH_OK;
 }
 

@@ -154,7 +154,12 @@ float ho_log(float x) {
   return fmaf(fe, 0.693145751953125f, fmaf(fe, 1.428606765330187e-06f, lm));
 }
 
-static inline float rd_f16(const uint8_t* p) { return ho_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+/* ho_f16_to_f32 of every half, tabulated once (the dots read a scale per block) */
+static float f16tab[65536];
+__attribute__((constructor)) static void init_f16tab(void) {
+  for (uint32_t h = 0; h < 65536; h++) f16tab[h] = ho_f16_to_f32((uint16_t)h);
+}
+static inline float rd_f16(const uint8_t* p) { return f16tab[p[0] | (p[1] << 8)]; }
 
 /* ------------------------------------------------------------------------- */
 /* formats                                                                   */
@@ -339,26 +344,38 @@ static inline int32_t hsum_i32x8(__m256i v) {
   s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xB1));
   return _mm_cvtsi128_si32(s);
 }
-/* sum_i u[i] * a[i] - bias * sum_i a[i], u unsigned bytes (0..3) */
-static inline int32_t udot32(__m256i u, const int8_t* a, int bias) {
+/* The four exact sub-block dots of one 128-element block at once (the integer
+ * sums do not depend on the order): out[s] = sum (code - 1) * a over sub-block
+ * s, codes widened through the byte tables by a gather, the four 8-lane
+ * partial vectors reduced together by horizontal adds. */
+static inline void block_reduce4(const __m256i* v, int32_t* out) {
+  __m256i h01 = _mm256_hadd_epi32(v[0], v[1]);
+  __m256i h23 = _mm256_hadd_epi32(v[2], v[3]);
+  __m256i h = _mm256_hadd_epi32(h01, h23);
+  _mm_storeu_si128((__m128i*)out, _mm_add_epi32(_mm256_castsi256_si128(h), _mm256_extracti128_si256(h, 1)));
+}
+static inline __m256i sub_partial(__m256i u, const uint8_t* ab) {
   const __m256i ones8 = _mm256_set1_epi8(1), ones16 = _mm256_set1_epi16(1);
-  __m256i av = _mm256_loadu_si256((const __m256i*)a);
-  __m256i p = _mm256_madd_epi16(_mm256_maddubs_epi16(u, av), ones16);
-  __m256i s = _mm256_madd_epi16(_mm256_maddubs_epi16(ones8, av), ones16);
-  return hsum_i32x8(p) - bias * hsum_i32x8(s);
+  __m256i av = _mm256_loadu_si256((const __m256i*)(ab + 2));
+  return _mm256_sub_epi32(_mm256_madd_epi16(_mm256_maddubs_epi16(u, av), ones16),
+                          _mm256_madd_epi16(_mm256_maddubs_epi16(ones8, av), ones16));
 }
-/* sum (code - 1) * a over one 32-element sub-block (8 code bytes) */
-static inline int32_t sub_dot_q2(const uint8_t* q, const int8_t* a) {
-  __m256i u = _mm256_setr_epi32((int)q2lut[q[0]], (int)q2lut[q[1]], (int)q2lut[q[2]], (int)q2lut[q[3]],
-                                (int)q2lut[q[4]], (int)q2lut[q[5]], (int)q2lut[q[6]], (int)q2lut[q[7]]);
-  return udot32(u, a, 1);
+static inline void block_dots_q2(const uint8_t* qs, const uint8_t* ab, int32_t* out) {
+  __m256i v[4];
+  for (int sub = 0; sub < 4; sub++) {
+    __m256i idx = _mm256_cvtepu8_epi32(_mm_loadl_epi64((const __m128i*)(qs + 8 * sub)));
+    v[sub] = sub_partial(_mm256_i32gather_epi32((const int*)q2lut, idx, 4), ab + sub * 34);
+  }
+  block_reduce4(v, out);
 }
-/* sum (bit ? +1 : -1) * a = 2 * sum bit * a - sum a over one sub-block (4 bit bytes) */
-static inline int32_t sub_dot_q1(const uint8_t* q, const int8_t* a) {
-  __m256i u = _mm256_setr_epi64x((long long)q1lut[q[0]], (long long)q1lut[q[1]], (long long)q1lut[q[2]],
-                                 (long long)q1lut[q[3]]);
-  u = _mm256_add_epi8(u, u);
-  return udot32(u, a, 1);
+static inline void block_dots_q1(const uint8_t* bits, const uint8_t* ab, int32_t* out) {
+  __m256i v[4];
+  for (int sub = 0; sub < 4; sub++) {
+    __m128i idx = _mm_cvtepu8_epi32(_mm_cvtsi32_si128(*(const int*)(bits + 4 * sub)));
+    __m256i u = _mm256_i32gather_epi64((const long long*)q1lut, idx, 8);
+    v[sub] = sub_partial(_mm256_add_epi8(u, u), ab + sub * 34);
+  }
+  block_reduce4(v, out);
 }
 
 /* q2_0.rs:537-574 scalar Q2_0 x Q8_0. */
@@ -370,12 +387,11 @@ float ho_dot_q2_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n) {
     float w_scale = rd_f16(wb);
     const uint8_t* qs = wb + 2;
     float block_acc = 0.0f;
+    int32_t dots[4];
+    block_dots_q2(qs, a + b * 4 * 34, dots);   /* sum (code - 1) * a per sub-block, exact */
     for (int sub = 0; sub < 4; sub++) {
-      const uint8_t* ab = a + (b * 4 + sub) * 34;
-      float a_scale = rd_f16(ab);
-      const int8_t* av = (const int8_t*)(ab + 2);
-      int32_t dot = sub_dot_q2(qs + sub * 8, av);   /* sum (code - 1) * a, exact */
-      block_acc += (float)dot * a_scale;
+      float a_scale = rd_f16(a + (b * 4 + sub) * 34);
+      block_acc += (float)dots[sub] * a_scale;
     }
     sum += block_acc * w_scale;
   }
@@ -414,12 +430,11 @@ float ho_dot_q1_0_q8_0(const uint8_t* w, const uint8_t* a, int64_t n) {
     float w_scale = rd_f16(wb);
     const uint8_t* bits = wb + 2;
     float block_acc = 0.0f;
+    int32_t dots[4];
+    block_dots_q1(bits, a + b * 4 * 34, dots);   /* sum (bit ? 1 : -1) * a per sub-block, exact */
     for (int sub = 0; sub < 4; sub++) {
-      const uint8_t* ab = a + (b * 4 + sub) * 34;
-      float a_scale = rd_f16(ab);
-      const int8_t* av = (const int8_t*)(ab + 2);
-      int32_t dot = sub_dot_q1(bits + sub * 4, av);  /* sum (bit ? 1 : -1) * a, exact */
-      block_acc += (float)dot * a_scale;
+      float a_scale = rd_f16(a + (b * 4 + sub) * 34);
+      block_acc += (float)dots[sub] * a_scale;
     }
     sum += block_acc * w_scale;
   }
@@ -1108,6 +1123,13 @@ struct ho_model {
   int n_signs, sign_w[8];
   float* signs[8];
   float* rot;
+  /* Q8_0 activation trace (diagnostics, ho_model_q8_trace): mode 1 appends
+   * every matmul input's Q8_0 bytes to trace, mode 2 uses the recorded bytes
+   * in place of its own and counts the bytes that differ */
+  int trace_mode;
+  uint8_t* trace;
+  size_t trace_cap, trace_pos;
+  int64_t trace_diff, trace_acts_diff;
 };
 
 static tensor_t* add_tensor(ho_model* m, const char* name, int type, int64_t rows, int64_t cols,
@@ -1360,6 +1382,14 @@ void ho_model_set_threads(ho_model* m, int n_threads, int arm) {
 
 const float* ho_model_hidden(const ho_model* m) { return m->hidden; }
 
+/* Work buffers left by the last forward (the last layer's values), for
+ * diagnostics: 0 hidden, 1 normed, 2 q, 3 k, 4 v, 5 attn_out, 6 gate (after
+ * silu), 7 up, 8 tmp (last projection output), 9 big (silu(gate)*up). */
+const float* ho_model_buffer(const ho_model* m, int which) {
+  const float* b[10] = {m->hidden, m->normed, m->q, m->k, m->v, m->attn_out, m->gate, m->up, m->tmp, m->big};
+  return which >= 0 && which < 10 ? b[which] : NULL;
+}
+
 static const float* signs_for(const ho_model* m, int width) {
   for (int i = 0; i < m->n_signs; i++)
     if (m->sign_w[i] == width) return m->signs[i];
@@ -1387,9 +1417,45 @@ static const float* fold_input(ho_model* m, const float* x, int64_t n) {
   return m->rot;
 }
 
+/* quantize_act (q8_0.rs:20-51) of a matmul input into m->q8, with the trace */
+static void quant_act(ho_model* m, const float* x, int64_t n) {
+  ho_quantize_q8_0(x, n, m->q8);
+  const size_t nb = (size_t)(n / 32) * 34;
+  if (m->trace_mode == 0 || m->trace_pos + nb > m->trace_cap) return;
+  uint8_t* t = m->trace + m->trace_pos;
+  if (m->trace_mode == 1) {
+    memcpy(t, m->q8, nb);
+  } else {
+    int64_t d = 0;
+    for (size_t i = 0; i < nb; i++) d += t[i] != m->q8[i];
+    m->trace_diff += d;
+    m->trace_acts_diff += d > 0;
+    memcpy(m->q8, t, nb);
+  }
+  m->trace_pos += nb;
+}
+
+/* Diagnostics: mode 0 off; 1 record every matmul input's Q8_0 bytes into buf
+ * (cap bytes); 2 replay them: each matmul then reads the recorded bytes
+ * instead of its own quantization.  Resets the cursor and the counters. */
+void ho_model_q8_trace(ho_model* m, int mode, uint8_t* buf, size_t cap) {
+  m->trace_mode = mode;
+  m->trace = buf;
+  m->trace_cap = cap;
+  m->trace_pos = 0;
+  m->trace_diff = m->trace_acts_diff = 0;
+}
+
+/* bytes used so far; out[0] = replayed bytes that differed from the model's
+ * own quantization, out[1] = matmul inputs with at least one such byte */
+size_t ho_model_q8_trace_stats(const ho_model* m, int64_t* out) {
+  if (out) { out[0] = m->trace_diff; out[1] = m->trace_acts_diff; }
+  return m->trace_pos;
+}
+
 /* matmul.rs:50-378 for the quantized dtypes: quantize_act + par_dot_rows. */
 static void mm(ho_model* m, const tensor_t* w, const float* x, float* out) {
-  ho_quantize_q8_0(fold_input(m, x, w->cols), w->cols, m->q8);
+  quant_act(m, fold_input(m, x, w->cols), w->cols);
   ho_gemv(w->type, w->data, w->rows, w->cols, m->q8, out, m->n_threads, m->arm);
 }
 
@@ -1424,7 +1490,7 @@ static void dev_head_gemv(int type, const uint8_t* w, int64_t rows, int64_t K, c
 static void head_mm(ho_model* m, const float* x, float* logits) {
   if (!logits) return; /* a prompt token whose logits nobody reads */
   const tensor_t* w = m->output;
-  ho_quantize_q8_0(fold_input(m, x, w->cols), w->cols, m->q8);
+  quant_act(m, fold_input(m, x, w->cols), w->cols);
   if (m->order) dev_head_gemv(w->type, w->data, w->rows, w->cols, m->q8, logits, m->n_threads);
   else ho_gemv(w->type, w->data, w->rows, w->cols, m->q8, logits, m->n_threads, m->arm);
 }

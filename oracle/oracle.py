@@ -88,6 +88,9 @@ def load() -> C.CDLL:
         "ho_forward": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int, f32p]),
         "ho_generate": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int, C.c_int, C.c_float, u32p, f32p]),
         "ho_model_hidden": (C.c_void_p, [C.c_void_p]),
+        "ho_model_buffer": (C.c_void_p, [C.c_void_p, C.c_int]),
+        "ho_model_q8_trace": (None, [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]),
+        "ho_model_q8_trace_stats": (C.c_size_t, [C.c_void_p, C.c_void_p]),
         "ho_wht": (None, [f32p, C.c_int64]),
         "ho_hadamard_rotate": (None, [f32p, C.c_int64, C.c_void_p, C.c_int]),
         "ho_hadamard_unrotate": (None, [f32p, C.c_int64, C.c_void_p, C.c_int]),
@@ -212,6 +215,19 @@ class OracleModel:
         assert s.size == width
         assert self.lib.ho_model_set_signs(self.h, width, _p(s)) == 0
         self._signs = getattr(self, "_signs", []) + [s]
+
+    def q8_trace(self, mode: int, buf: Optional[np.ndarray] = None) -> None:
+        """Diagnostics: mode 1 records every matmul input's Q8_0 bytes into buf,
+        mode 2 replays them in place of the model's own quantization, 0 = off."""
+        self._trace = buf
+        self.lib.ho_model_q8_trace(self.h, mode, None if buf is None else buf.ctypes.data,
+                                   0 if buf is None else buf.nbytes)
+
+    def q8_trace_stats(self):
+        """(bytes used, replayed bytes that differed, matmul inputs with a differing byte)"""
+        st = np.zeros(2, dtype=np.int64)
+        n = self.lib.ho_model_q8_trace_stats(self.h, st.ctypes.data)
+        return int(n), int(st[0]), int(st[1])
 
     def set_order(self, order: int) -> None:
         self.lib.ho_model_set_order(self.h, order)

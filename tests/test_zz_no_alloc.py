@@ -41,3 +41,16 @@ def test_noalloc_attention_rejects_beyond_scratch(ctx):
     with pytest.raises(HHError) as e:   # 8 x 625 splits x 4 x 130 floats > 4 MiB
         ctx.attention_noalloc(q, kv, kv, nh, nkv, hd, ms, 40000, out)
     assert e.value.status == 7 and "4 MiB" in str(e.value)
+
+
+def test_attention_rejects_more_than_8_heads_per_kv_head(ctx):
+    """G = n_heads / n_kv above 8 is a dimension error from both entry points."""
+    from hearth_amd import HHError
+    nh, nkv, hd, ms = 16, 1, 128, 64
+    q = torch.zeros(nh * hd, dtype=torch.float32, device="cuda")
+    kv = torch.zeros(nkv * ms * hd, dtype=torch.float32, device="cuda")
+    out = torch.zeros(nh * hd, dtype=torch.float32, device="cuda")
+    for call in (ctx.attention, ctx.attention_noalloc):
+        with pytest.raises(HHError) as e:
+            call(q, kv, kv, nh, nkv, hd, ms, 10, out)
+        assert e.value.status == 3 and "8 query heads" in str(e.value)
