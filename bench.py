@@ -55,9 +55,34 @@ def step_bytes(cfg, seq_len: int) -> dict:
             "attention": 2 * cfg.n_kv_heads * seq_len * row + 2 * cfg.n_kv_heads * row}
 
 
+GEMV_SOURCE = os.path.join(ROOT, "hearth_amd", "csrc", "hh_gemv.hip")
+
+
+def gemv_source_hash() -> str:
+    import hashlib
+    with open(GEMV_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def traffic_is_current() -> bool:
+    """The counter summary records the hash of hh_gemv.hip it was measured on;
+    a summary of other GEMV code is stale."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                if ln.startswith("GEMV source (hh_gemv.hip) sha256:"):
+                    return ln.split(":", 1)[1].strip() == gemv_source_hash()
+    except OSError:
+        pass
+    return False
+
+
 def measured_traffic(kernel_prefix: str):
     """HBM bytes per dispatch of a kernel from the committed counter summary
-    (the 'traffic MB' column), or None when the summary has no such row."""
+    (the 'traffic MB' column); None when the summary has no such row or was
+    measured on another version of the GEMV source."""
+    if not traffic_is_current():
+        return None
     try:
         with open(TRAFFIC_FILE) as f:
             for ln in f:
@@ -367,7 +392,10 @@ def main():
                      "frac": round(od_gbs / PEAK_HBM_GBS, 4),
                      "traffic": None if od_traffic is None else od_traffic,
                      "traffic_note": "mean HBM bytes per dispatch of the two launches (rocprofv3 FETCH/WRITE, "
-                                     "profiles/decode_8b_q2_hbm_traffic.txt)",
+                                     "profiles/decode_8b_q2_hbm_traffic.txt, measured on hh_gemv.hip sha256 "
+                                     + gemv_source_hash() + ")" if od_traffic is not None else
+                                     "null: profiles/decode_8b_q2_hbm_traffic.txt was measured on another "
+                                     "version of hh_gemv.hip",
                      "avg_launch_ms": round(od_ms / 2, 5), "bytes_per_launch": od_bytes // 2},
         "roofline_gate_up": {"bound": "hbm", "kernel": "k_gemv<Q2,RMSNORM,SILU> (fused gate+up, layer 0)",
                              "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
