@@ -119,3 +119,32 @@ def test_chunked_generate_tokens(ctx, oracle):
             assert gap <= spread, f"step {i}: token {got} != {ts[i]}, gap {gap:.3g} > arm spread {spread:.3g}"
     print(f"chunked: tokens equal {same}/{n_gen}, worst logit rel err {worst:.2e}, "
           f"reference arm spread {spread:.3g}", flush=True)
+
+
+def test_chunked_falls_back_unless_every_ssm_a_is_negative(ctx, oracle):
+    """The chunked form needs every decay exponent <= 0 (ssm_a < 0); with one
+    ssm_a >= 0 uploaded, HH_GDN_CHUNKED=1 runs the sequential recurrence, so the
+    prefilled state equals the sequential path's bit for bit (and stays finite).
+    A later upload that makes every ssm_a negative again re-enables it."""
+    from hearth_amd import GGML_F32
+    cfg = CONFIGS["9b-hybrid-q2"].replace(n_layers=1, max_seq=256)
+    prompt = [oracle.synth_token(8, i, cfg.vocab) for i in range(130)]
+    states = []
+    for chunked in (False, True):
+        m = _model(ctx, cfg, 31, chunked)
+        a = m.download("blk.0.ssm_a", 4 * cfg.ssm_n_v_heads).view(np.float32).copy()
+        assert (a < 0).all()
+        bad = a.copy()
+        bad[3] = 0.25
+        m.upload("blk.0.ssm_a", GGML_F32, cfg.ssm_n_v_heads, 1, bad)
+        m.prefill(prompt, 0)
+        states.append(m.download_state(0))
+        if chunked:   # negative again: the chunked path runs (state differs in the last bits)
+            m.upload("blk.0.ssm_a", GGML_F32, cfg.ssm_n_v_heads, 1, a)
+            m.reset()
+            m.prefill(prompt, 0)
+            s_chk = m.download_state(0)
+        m.close()
+    assert np.isfinite(states[1]).all()
+    assert np.array_equal(states[0], states[1])
+    assert not np.array_equal(s_chk, states[1])
