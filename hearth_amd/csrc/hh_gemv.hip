@@ -76,14 +76,18 @@ HH_DEV void unit_q2(const uint32_t (&w)[17], const int8_t* aq, const float* ad, 
       hi = __builtin_amdgcn_sdot8((int)o0, a0.y, hi, false);
       hi = __builtin_amdgcn_sdot8((int)e1, a1.x, hi, false);
       hi = __builtin_amdgcn_sdot8((int)o1, a1.y, hi, false);
-      uint32_t lo = 0;
+      // the unsigned chain starts at -sum(a) (mod 2^32, exact once added to
+      // 16 hi): sum (code-1)*a = sum code*a - sum a
+      uint32_t lo = (uint32_t)(-as[blk * 4 + sub]);
       lo = __builtin_amdgcn_udot8(e0, (uint32_t)a0.z, lo, false);
       lo = __builtin_amdgcn_udot8(o0, (uint32_t)a0.w, lo, false);
       lo = __builtin_amdgcn_udot8(e1, (uint32_t)a1.z, lo, false);
       lo = __builtin_amdgcn_udot8(o1, (uint32_t)a1.w, lo, false);
-      int s = hi * 16 + (int)lo;
-      s -= as[blk * 4 + sub];                 // sum (code-1)*a = sum code*a - sum a
-      bacc += (float)s * ad[blk * 4 + sub];   // block_acc += dot * a_scale
+      const int s = hi * 16 + (int)lo;
+      // block_acc += dot * a_scale: |dot| < 2^13 and a_scale is an f16 value,
+      // so the product is exact in f32 and the fma rounds once, as the
+      // separate multiply and add do
+      bacc = fmaf((float)s, ad[blk * 4 + sub], bacc);
     }
     pr[blk] = bacc * dw;                      // sum += block_acc * w_scale
   }
@@ -125,7 +129,7 @@ HH_DEV void unit_q1(const uint32_t (&w)[9], const int8_t* aq, const float* ad, c
       lo = __builtin_amdgcn_udot8(p3, (uint32_t)a1.w, lo, false);
       int s = hi * 16 + (int)lo;
       s = 2 * s - as[blk * 4 + sub];          // sum (+-1)*a = 2*sum bit*a - sum a
-      bacc += (float)s * ad[blk * 4 + sub];
+      bacc = fmaf((float)s, ad[blk * 4 + sub], bacc);   // exact product (|s| < 2^12), one rounding
     }
     pr[blk] = bacc * dw;
   }
@@ -230,7 +234,7 @@ HH_DEV float block_pt(const uint32_t* w, const int8_t* aq, const float* ad, cons
   }
   float bacc = 0.0f;
 #pragma unroll
-  for (int sub = 0; sub < 4; ++sub) bacc += (float)s[sub] * ad[sub];
+  for (int sub = 0; sub < 4; ++sub) bacc = fmaf((float)s[sub], ad[sub], bacc);   // exact product, one rounding
   return bacc * h2f(w[6] >> 16);
 }
 
