@@ -153,6 +153,24 @@ def prefill_leg(m, cfg, n_tok: int) -> dict:
                     "kernels included); dense-model forward_batch, bit-identical to token-by-token decode"}
 
 
+def prefill_mfma_attention_leg(ctx, cfg, seed: int, n_tok: int) -> dict:
+    """The same 2048-token prefill with its attention on fp32 MFMA
+    (HH_PREFILL_ATTN=mfma, k_attn_prefill_mfma): fp32-rounding parity with the
+    default split/merge attention instead of bit parity with decode."""
+    from hearth_amd import Model
+    os.environ["HH_PREFILL_ATTN"] = "mfma"
+    try:
+        m = Model(ctx, cfg)
+    finally:
+        os.environ.pop("HH_PREFILL_ATTN", None)
+    m.synthesize(seed)
+    r = prefill_leg(m, cfg, n_tok)
+    m.close()
+    r["note"] = ("opt-in HH_PREFILL_ATTN=mfma: causal attention on fp32 MFMA (flash form, online softmax); "
+                 "within 1e-5 of float64 attention, logits within fp32-rounding/Q8_0-flip distance of the default")
+    return r
+
+
 def kv_q8_leg(ctx, cfg, seed, kv_seed, tok0, K, W) -> dict:
     """The same decode with the KV cache held as Q8_0 rows (KVStorage::Q8_0,
     kvcache.rs:41-57): 3.8x fewer KV bytes at 2k context.  Reported beside the
@@ -280,12 +298,30 @@ def hybrid_leg(ctx, n_prompt: int, K: int, W: int) -> dict:
     pfc_ms = mc.last_prefill_ms()
     mc.close()
     print(f"[bench] 9B hybrid, chunked GDN prefill: {n_prompt} tokens {pfc_ms:.1f} ms", file=sys.stderr, flush=True)
+    # both opt-in prefill forms: chunked GDN and the fp32-MFMA attention
+    os.environ["HH_GDN_CHUNKED"] = "1"
+    os.environ["HH_PREFILL_ATTN"] = "mfma"
+    try:
+        mf = Model(ctx, cfg)
+    finally:
+        os.environ.pop("HH_GDN_CHUNKED", None)
+        os.environ.pop("HH_PREFILL_ATTN", None)
+    mf.synthesize(2027)
+    mf.generate(prompt[:64], 2, repeat_pen=1.0)
+    mf.reset()
+    mf.generate(prompt, 2, repeat_pen=1.0)
+    pff_ms = mf.last_prefill_ms()
+    mf.close()
+    print(f"[bench] 9B hybrid, chunked GDN + MFMA attention prefill: {n_prompt} tokens {pff_ms:.1f} ms", file=sys.stderr,
+          flush=True)
     return {"model": "9B-shaped qwen35 hybrid Q2_0 (32 layers, full attention every 4th)",
             "prefill_tokens": n_prompt, "prefill_ms": round(pf_ms, 2),
             "prefill_tok_per_s": round(n_prompt / (pf_ms * 1e-3), 1),
             "decode_tok_per_s": round(1000.0 / dec_ms, 2), "decode_ms_per_step": round(dec_ms, 4),
             "prefill_chunked_gdn_ms": round(pfc_ms, 2),
             "prefill_chunked_gdn_tok_per_s": round(n_prompt / (pfc_ms * 1e-3), 1),
+            "prefill_chunked_gdn_mfma_attention_ms": round(pff_ms, 2),
+            "prefill_chunked_gdn_mfma_attention_tok_per_s": round(n_prompt / (pff_ms * 1e-3), 1),
             "first_tokens": [int(t) for t in toks[:8]],
             "note": "prompt through the batched prefill (bit-identical to token-by-token decode), then decode "
                     "from the prefilled state; prefill time is the prompt phase of generate"}
@@ -413,6 +449,7 @@ def main():
         out["kv_q8"] = kv_q8_leg(ctx, cfg, seed, kv_seed, tok0, K, W)
     if args.prefill_tokens > 0:
         out["prefill"] = prefill_leg(m, cfg, args.prefill_tokens)
+        out["prefill_mfma_attention"] = prefill_mfma_attention_leg(ctx, cfg, seed, args.prefill_tokens)
     if not args.no_hybrid:
         out["hybrid"] = hybrid_leg(ctx, 2048, K, W)
     if not args.no_configs:

@@ -128,6 +128,9 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
                            int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
                            const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, float* yf,
                            hipStream_t s);
+int hh_prefill_attn_mfma_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads,
+                                int n_kv, int max_seq, int pos0, int t0, int n, const float* gate, int gate_row,
+                                int kv_q8, int8_t* yq, float* yd, float* yf, hipStream_t s);
 // yf != null: the merged (gated) rows as f32 [S][n_heads*hd] instead of Q8_0
 // gate: qwen35 gated attention's projection rows (gate_row floats apart), or null;
 // kv_q8: the caches hold Q8_0 rows (quantized on write, dequantized on load)

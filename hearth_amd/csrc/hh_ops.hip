@@ -1144,6 +1144,187 @@ __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restr
 }
 
 // ---------------------------------------------------------------------------
+// Prefill attention on fp32 MFMA (opt-in, HH_PREFILL_ATTN=mfma): the causal
+// attention of a whole prompt as a flash-style pass per (token tile, kv head),
+// for the batched prefill only.  It regroups the fp32 sums (16x16x4 MFMA
+// products, an online softmax over 32-position chunks, exp2 of prescaled
+// scores), so it matches the split/merge path (and token-by-token decode) to
+// fp32 rounding, not bit for bit; that path stays the default.
+//
+// Workgroup = W = G*T waves, T = max(1, 8 / G) token tiles of 16 (4 to 8
+// waves); wave w handles query head kvh*G + w % G for tokens s0 + 16 (w / G)
+// + 0..15, so a staged chunk serves up to 8 query rows per position.  The 1-D
+// grid runs the kv heads fastest: with the round-robin dispatch over the 8
+// XCDs, one kv head's workgroups share an XCD and its L2 (n_kv dividing 8).
+// The workgroup stages each 32-position chunk of its kv head's K and V in LDS
+// (dequantized when the cache holds Q8_0 rows).  Per chunk and wave:
+//   S^T (positions x queries) = K Q^T: A = K rows, B = Q^T held in registers,
+//     dims permuted within 16-dim blocks (lane group g takes dims 16j + 4g + m
+//     in step m) on both operands, so each step still sums matching dims;
+//   online softmax per query column (each lane owns one query);
+//   O^T (dims x queries) += V^T P^T: P^T stays in the C registers of S^T, read
+//     in step r as position 4g + r of the lane's group, with A = V[4g + r][dim].
+// Then O / L, the qwen35 sigmoid gate, and the Q8_0 row of attn_output's input
+// in the GEMM's split layout (or the f32 row for a folded model).
+template <int HD, bool KV8>
+__global__ __launch_bounds__(512) void k_attn_prefill_mfma(const float* __restrict__ QB, const float* __restrict__ k_cache,
+                                                           const float* __restrict__ v_cache, int n_heads, int n_kv,
+                                                           int max_seq, int pos0, int t0, int n,
+                                                           const float* __restrict__ gate, int gate_row,
+                                                           int8_t* __restrict__ yq, float* __restrict__ yd,
+                                                           float* __restrict__ yf) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  // chunk positions (64 measured the same at head_dim 128), LDS row stride,
+  // dim blocks, 16-position tiles
+  constexpr int CHK = 32, RS = HD + 4, NJ = HD / 16, NQT = CHK / 16;
+  __shared__ __align__(16) float Ks[CHK * RS];
+  __shared__ __align__(16) float Vs[CHK * RS];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nth = blockDim.x;
+  const int mi = lane & 15, g = lane >> 4;
+  const int G = n_heads / n_kv, T = G >= 8 ? 1 : 8 / G;
+  const int kvh = (int)blockIdx.x % n_kv, h = wid % G, qh = kvh * G + h;
+  const int tile0 = t0 + ((int)blockIdx.x / n_kv) * 16 * T;   // first token of the workgroup
+  const int last = min(t0 + n, tile0 + 16 * T) - 1;           // its last valid token
+  const int sq_raw = tile0 + 16 * (wid / G) + mi;
+  const bool qvalid = sq_raw < t0 + n;
+  const int sq = min(sq_raw, t0 + n - 1);                     // out-of-range lanes compute a valid row
+  const int pq = pos0 + sq;
+  // q prescaled by log2(e) / sqrt(HD): the scores come out in base-2 units
+  const float qs = 1.4426950408889634f / sqrtf((float)HD);
+  f32x4 q4[NJ];
+  {
+    const float* qp = QB + ((size_t)sq * n_heads + qh) * HD + 4 * g;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float4 v = *(const float4*)(qp + 16 * j);
+      q4[j] = (f32x4){v.x * qs, v.y * qs, v.z * qs, v.w * qs};
+    }
+  }
+  f32x4 o[NJ];
+#pragma unroll
+  for (int t = 0; t < NJ; ++t) o[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  const int p_last = pos0 + last;
+  const int n_chunks = p_last / CHK + 1;
+  const KvQ8 kq(const_cast<float*>(k_cache), n_kv, max_seq, HD), vq(const_cast<float*>(v_cache), n_kv, max_seq, HD);
+  const size_t row0 = (size_t)kvh * max_seq;
+  for (int c = 0; c < n_chunks; ++c) {
+    const int pbase = c * CHK;
+    __syncthreads();   // every wave is done with the previous chunk
+    for (int i = tid; i < CHK * HD / 4; i += nth) {
+      const int r = i / (HD / 4), cc = i % (HD / 4);
+      const int p = min(pbase + r, p_last);   // rows past the last position: any valid row (masked below)
+      float4 kv, vv;
+      if constexpr (KV8) {
+        kv = kq.load(row0 + p, HD, cc);
+        vv = vq.load(row0 + p, HD, cc);
+      } else {
+        kv = *(const float4*)(k_cache + (row0 + p) * HD + 4 * cc);
+        vv = *(const float4*)(v_cache + (row0 + p) * HD + 4 * cc);
+      }
+      *(float4*)(Ks + r * RS + 4 * cc) = kv;
+      *(float4*)(Vs + r * RS + 4 * cc) = vv;
+    }
+    __syncthreads();
+    // S^T for the chunk's 16-position tiles
+    f32x4 sc[NQT];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const float* kr = Ks + (16 * qt + mi) * RS + 4 * g;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const float4 k4 = *(const float4*)(kr + 16 * j);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, q4[j][0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, q4[j][1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, q4[j][2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, q4[j][3], acc, 0, 0, 0);
+      }
+      sc[qt] = acc;
+    }
+    // causal mask and the chunk's maximum per query
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int p = pbase + 16 * qt + 4 * g + r;
+        if (p > pq) sc[qt][r] = -INFINITY;
+        cmax = fmaxf(cmax, sc[qt][r]);
+      }
+    cmax = fmaxf(cmax, xor_lane<16>(cmax));
+    cmax = fmaxf(cmax, xor_lane<32>(cmax));
+    const float m_new = fmaxf(m_run, cmax);   // position 0 is in chunk 0: finite from the start
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    float psum = 0.0f;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[qt][r] = __builtin_amdgcn_exp2f(sc[qt][r] - m_new);
+        psum += sc[qt][r];
+      }
+    psum += xor_lane<16>(psum);
+    psum += xor_lane<32>(psum);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) o[t] *= alpha;
+    // O^T += V^T P^T
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vr = Vs + (16 * qt + 4 * g + r) * RS + mi;
+#pragma unroll
+        for (int t = 0; t < NJ; ++t)
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * t], sc[qt][r], o[t], 0, 0, 0);
+      }
+  }
+  // lane holds dims 16 t + 4 g + r of token sq
+  const float rl = 1.0f / l_run;
+  const int K = n_heads * HD;
+#pragma unroll
+  for (int t = 0; t < NJ; ++t) {
+    o[t] *= rl;
+    if (gate) {   // qwen35.rs:1627-1629: attn_out /= 1 + exp(-gate)
+      const float4 gv = *(const float4*)(gate + (size_t)sq * gate_row + (size_t)qh * 2 * HD + HD + 16 * t + 4 * g);
+      const float gg[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[t][r] = o[t][r] / (1.0f + hx_exp(-gg[r]));
+    }
+  }
+  if (yf) {
+    if (qvalid)
+#pragma unroll
+      for (int t = 0; t < NJ; ++t)
+        *(float4*)(yf + (size_t)sq * K + qh * HD + 16 * t + 4 * g) = make_float4(o[t][0], o[t][1], o[t][2], o[t][3]);
+    return;
+  }
+#pragma unroll
+  for (int b = 0; b < NJ / 2; ++b) {   // Q8_0 block b = dims 32 b .. 32 b + 31 = tiles 2b, 2b + 1
+    float am = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) am = fmaxf(am, fabsf(o[2 * b + u][r]));
+    am = fmaxf(am, xor_lane<16>(am));
+    am = fmaxf(am, xor_lane<32>(am));
+    const float scq = q8_scale(am), rc = q8_rcp(scq);
+    if (qvalid) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) word |= ((uint32_t)q8_round_r(o[2 * b + u][r], scq, rc) & 0xffu) << (8 * r);
+        *(uint32_t*)(yq + (size_t)sq * K + qh * HD + 16 * (2 * b + u) + 4 * g) = word;
+      }
+      if (g == 0) yd[(size_t)sq * (K / 32) + (qh * HD) / 32 + b] = h2f(f2h(scq));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Greedy selection over a logits vector (standalone operator).
 // ---------------------------------------------------------------------------
 HH_DEV bool better(int rule, float v2, int i2, float v1, int i1) {
@@ -1567,6 +1748,29 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
   }
 #undef HH_PSPLIT_G
 #undef HH_PSPLIT
+  return ok();
+}
+
+// The whole prompt's attention on fp32 MFMA (k_attn_prefill_mfma): tokens
+// [t0, t0 + n) at positions pos0 + t0 ..; no partials.
+int hh_prefill_attn_mfma_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads,
+                                int n_kv, int max_seq, int pos0, int t0, int n, const float* gate, int gate_row,
+                                int kv_q8, int8_t* yq, float* yd, float* yf, hipStream_t s) {
+  const int G = n_heads / n_kv;
+  if (G < 1 || G > 8 || n_kv * G != n_heads || n <= 0) return 1;
+  const int T = G >= 8 ? 1 : 8 / G;
+  dim3 grid(((n + 16 * T - 1) / (16 * T)) * n_kv), block(64 * G * T);
+#define HH_PMFMA(HDV, KV) \
+  hipLaunchKernelGGL((k_attn_prefill_mfma<HDV, KV>), grid, block, 0, s, QB, k_cache, v_cache, n_heads, n_kv, max_seq, \
+                     pos0, t0, n, gate, gate_row, yq, yd, yf)
+  if (hd == 128) {
+    if (kv_q8) HH_PMFMA(128, true); else HH_PMFMA(128, false);
+  } else if (hd == 256) {
+    if (kv_q8) HH_PMFMA(256, true); else HH_PMFMA(256, false);
+  } else {
+    return 1;
+  }
+#undef HH_PMFMA
   return ok();
 }
 

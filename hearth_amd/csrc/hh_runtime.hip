@@ -195,6 +195,9 @@ struct hh_model {
   // the chunked form needs every ssm_a < 0 (its decays exp(G_t - G_s) then stay
   // <= 1): -1 unchecked since the last weight write, 0 some ssm_a >= 0, 1 all negative
   int ssm_a_negative = -1;
+  // HH_PREFILL_ATTN=mfma: the batched prefill's attention runs on fp32 MFMA
+  // (k_attn_prefill_mfma; fp32-rounding parity instead of bit parity)
+  int prefill_attn_mfma = 0;
   // Hadamard fold: one device sign vector per folded width (+1 until set), and
   // the f32 hand-off of the matmul inputs that are rotated in the consumer's prologue
   float* had_signs = nullptr;
@@ -650,10 +653,14 @@ int prefill_batched(hh_model* m, const uint32_t* toks, int S, int pos0) {
       KTRY(hh_prefill_qk_launch(hd, QKV, L.n_in, c.n_heads, c.n_kv_heads, c.qk_norm ? L.q_norm : nullptr,
                                 c.qk_norm ? L.k_norm : nullptr, c.eps, m->rope, m->rope_dim, m->kv_rows, pos0, S,
                                 gated, kv8, L.k_cache, L.v_cache, QB, s));
-      for (int t0 = 0; t0 < S; t0 += TA)
-        KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, m->kv_rows, pos0, t0,
-                                    std::min(TA, S - t0), n_chunks, PO, PML, gated ? QKV : nullptr, L.n_in, kv8,
-                                    Xq, Xd, Rot, s));
+      if (m->prefill_attn_mfma)
+        KTRY(hh_prefill_attn_mfma_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, m->kv_rows, pos0, 0,
+                                         S, gated ? QKV : nullptr, L.n_in, kv8, Xq, Xd, Rot, s));
+      else
+        for (int t0 = 0; t0 < S; t0 += TA)
+          KTRY(hh_prefill_attn_launch(hd, QB, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, m->kv_rows, pos0, t0,
+                                      std::min(TA, S - t0), n_chunks, PO, PML, gated ? QKV : nullptr, L.n_in, kv8,
+                                      Xq, Xd, Rot, s));
       if (had)
         KTRY(hh_rot_q8_rows_launch(Rot, nullptr, 0.0f, nq, S, signs_of(m, nq), c.had_block, 0, 0, Xq, Xd, s));
       k_out = nq;
@@ -911,6 +918,43 @@ int hh_attention(hh_ctx* c, const float* q, const float* k, const float* v, int 
   a.out_f32 = out;
   int rc = hh_attn_launch(a, c->stream);
   if (rc) return fail(HH_ERR_HIP, std::string("attention launch: ") + hipGetErrorString(hipGetLastError()));
+  return HH_OK;
+}
+
+int hh_attention_prefill(hh_ctx* c, const float* q, const float* k, const float* v, int n_heads, int n_kv, int hd,
+                         int max_seq, int pos0, int n_tok, int mode, float* out) {
+  if (!c || !q || !k || !v || !out) return fail(HH_ERR_INVALID, "null argument");
+  if (n_kv <= 0 || n_heads % n_kv || (hd != 128 && hd != 256))
+    return fail(HH_ERR_DIM, "unsupported attention geometry (head_dim 128 or 256)");
+  if (n_heads / n_kv > 8) return fail(HH_ERR_DIM, "more than 8 query heads per kv head (n_heads / n_kv_heads)");
+  if (pos0 < 0 || n_tok <= 0 || pos0 + n_tok > max_seq) return fail(HH_ERR_RANGE, "positions out of range");
+  if (mode != 0 && mode != 1) return fail(HH_ERR_INVALID, "mode must be 0 (split/merge) or 1 (MFMA)");
+  // the output rows go out as f32 (the folded-model hand-off); the Q8_0 row
+  // arguments are unused then
+  if (mode == 1) {
+    if (hh_prefill_attn_mfma_launch(hd, q, k, v, n_heads, n_kv, max_seq, pos0, 0, n_tok, nullptr, 0, 0, nullptr,
+                                    nullptr, out, c->stream))
+      return fail(HH_ERR_HIP, std::string("prefill attention launch: ") + hipGetErrorString(hipGetLastError()));
+    return HH_OK;
+  }
+  const int G = n_heads / n_kv, n_chunks = (pos0 + n_tok + 8192 / hd - 1) / (8192 / hd);
+  const size_t per_tok = (size_t)n_kv * n_chunks * G * (hd + 2) * sizeof(float);
+  const int TA = (int)std::max<size_t>(16, std::min<size_t>((n_tok + 15) / 16 * 16, ((size_t)1 << 30) / per_tok / 16 * 16));
+  const size_t need = per_tok * TA;
+  if (c->attn_scratch_bytes < need) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->attn_scratch) HIP_TRY(hipFree(c->attn_scratch));
+    c->attn_scratch = nullptr;
+    c->attn_scratch_bytes = 0;
+    HIP_TRY(hipMalloc(&c->attn_scratch, need));
+    c->attn_scratch_bytes = need;
+  }
+  float* po = (float*)c->attn_scratch;
+  float* pml = po + (size_t)TA * n_kv * n_chunks * G * hd;
+  for (int t0 = 0; t0 < n_tok; t0 += TA)
+    if (hh_prefill_attn_launch(hd, q, k, v, n_heads, n_kv, max_seq, pos0, t0, std::min(TA, n_tok - t0), n_chunks, po,
+                               pml, nullptr, 0, 0, nullptr, nullptr, out, c->stream))
+      return fail(HH_ERR_HIP, std::string("prefill attention launch: ") + hipGetErrorString(hipGetLastError()));
   return HH_OK;
 }
 
@@ -1198,6 +1242,8 @@ int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out) {
     m->batched_prefill = (e && e[0] == '0') ? 0 : 1;
     const char* g = getenv("HH_GDN_CHUNKED");
     m->gdn_chunked = (g && g[0] == '1') ? 1 : 0;
+    const char* pa = getenv("HH_PREFILL_ATTN");
+    m->prefill_attn_mfma = (pa && strcmp(pa, "mfma") == 0) ? 1 : 0;
     // hh_model_generate replays 8 decode steps per graph launch (the launch
     // boundary costs ~5 us per step otherwise: 8B step 1.662 -> 1.657 ms)
     m->graph_steps = 8;

@@ -147,6 +147,8 @@ _EXPORTS = {
                                 C.c_int, C.c_int, C.c_void_p]),
     "hh_attention_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                 C.c_int, C.c_int, C.c_void_p]),
+    "hh_attention_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]),
     "hh_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_float, C.c_int,
                              C.c_void_p]),
     "hh_model_create": (C.c_int, [C.c_void_p, C.POINTER(ModelConfigC), C.POINTER(C.c_void_p)]),
@@ -298,6 +300,12 @@ class Ctx:
         """hh_attention with the partials in the library's fixed per-GPU scratch (no allocation)."""
         _check(self.lib.hh_attention_noalloc(self.h, _ptr(q), _ptr(k), _ptr(v), n_heads, n_kv, head_dim, max_seq,
                                              seq_len, _ptr(out)))
+
+    def attention_prefill(self, q, k, v, n_heads, n_kv, head_dim, max_seq, pos0, n_tokens, mode, out) -> None:
+        """Causal attention of n_tokens prompt tokens at positions pos0.. (mode 0:
+        the split/merge kernels, 1: the fp32-MFMA flash form)."""
+        _check(self.lib.hh_attention_prefill(self.h, _ptr(q), _ptr(k), _ptr(v), n_heads, n_kv, head_dim, max_seq,
+                                             pos0, n_tokens, mode, _ptr(out)))
 
     def argmax(self, logits, n: int, past, n_past: int, pen: float, rule: int, out) -> None:
         _check(self.lib.hh_argmax(self.h, _ptr(logits), n, _ptr(past), n_past, pen, rule, _ptr(out)))

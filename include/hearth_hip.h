@@ -120,6 +120,17 @@ int hh_rope(hh_ctx* ctx, float* x, int n_heads, int head_dim, int rope_dim, cons
 int hh_attention(hh_ctx* ctx, const float* q, const float* k_cache, const float* v_cache,
                  int n_heads, int n_kv_heads, int head_dim, int max_seq, int seq_len, float* out);
 
+/* Causal attention of a batch of prompt tokens, as forward_batch runs it per
+ * token (mod.rs:1101-1140, each token through ops.rs:353-406 over the rows
+ * before it): q [n_tokens][n_heads][hd] (already normed and rotated), k/v
+ * cache [n_kv][max_seq][hd] f32 holding positions 0 .. pos0 + n_tokens - 1;
+ * token t attends positions 0 .. pos0 + t.  out [n_tokens][n_heads][hd] f32.
+ * mode 0: the batched prefill's split/merge kernels (each token's row equals
+ * hh_attention at seq_len pos0 + t + 1 bit for bit); mode 1: the fp32-MFMA
+ * flash form (HH_PREFILL_ATTN=mfma), equal to fp32 rounding. */
+int hh_attention_prefill(hh_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, int n_heads,
+                         int n_kv_heads, int head_dim, int max_seq, int pos0, int n_tokens, int mode, float* out);
+
 /* hh_attention without any allocation: no counterpart in the reference.  For
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  Same arguments, kernels
