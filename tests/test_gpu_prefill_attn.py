@@ -105,3 +105,16 @@ def test_mfma_prefill_model_logits(ctx, oracle, name, kv_type):
     err = float(np.abs(res[0] - res[1]).max() / np.abs(res[0]).max())
     print(f"{name} kv{kv_type}: logits rel err MFMA vs default prefill attention {err:.2e}", flush=True)
     assert np.isfinite(res[1]).all() and err < 5e-2, err
+
+
+def test_attention_prefill_errors(ctx):
+    from hearth_amd import HHError
+    z = torch.zeros(16 * 4 * 128 * 64, dtype=torch.float32, device="cuda")
+    cases = [((16, 4, 128, 64, 0, 16, 2), 1),      # mode
+             ((16, 4, 128, 64, 60, 8, 0), 7),      # past max_seq
+             ((16, 4, 96, 64, 0, 8, 1), 3),        # head_dim
+             ((18, 1, 128, 64, 0, 8, 1), 3)]       # more than 8 query heads per kv head
+    for (nh, nkv, hd, ms, pos0, n, mode), status in cases:
+        with pytest.raises(HHError) as e:
+            ctx.attention_prefill(z, z, z, nh, nkv, hd, ms, pos0, n, mode, z)
+        assert e.value.status == status, (nh, nkv, hd, ms, pos0, n, mode, e.value)
