@@ -48,7 +48,16 @@ template <int TN> struct Stage {
   int8_t w[TN * AROW];     // weights widened to int8 (code - 1, or +-1)
   float da[4 * TM];        // activation scale per (sub-block, token)
   float dw[TN * 4];        // weight scale per row (Q2/Q1: [0]; Q8: per sub-block)
+  float nmd[TM];           // -GEMM_MAGIC * d_a of sub-block 0, per token
 };
+
+// Sub-block 0 of each block starts its MFMA from GEMM_MAGIC_BITS, so the int32
+// result c = MAGIC_BITS + i reads as the float GEMM_MAGIC + i exactly (|i| <
+// 2^22), and fma(c, d_a, -GEMM_MAGIC * d_a) is i * d_a exactly (both terms and
+// the result fit f32's 24 bits): the block accumulator's first term, as
+// fma((float)i, d_a, 0) gives it, without the int -> float convert.
+constexpr float GEMM_MAGIC = 12582912.0f;   // 1.5 * 2^23
+constexpr int GEMM_MAGIC_BITS = 0x4B400000;
 
 // Q2_0 codes (8 per u16, LSB first) -> 8 int8 (code - 1): spread the four
 // 2-bit fields of a byte to byte lanes, then (c + 0x7f) ^ 0x80 per lane.
@@ -138,6 +147,7 @@ HH_DEV void stage_store(Stage<TN>& st, const Regs<FMT, TN>& R) {
     dst[1] = make_uint2(R.a[i].z, R.a[i].w);
   }
   st.da[(tid & 3) * TM + (tid >> 2)] = R.ad;        // loaded as (t = tid / 4, sub = tid % 4)
+  if ((tid & 3) == 0) st.nmd[tid >> 2] = -GEMM_MAGIC * R.ad;
   constexpr int CU = w_code_units<FMT>();
 #pragma unroll
   for (int i = 0; i < w_regs<FMT, TN>(); ++i) {
@@ -220,10 +230,24 @@ __global__ __launch_bounds__(NTG) void k_gemm(const uint8_t* __restrict__ w, con
       const long a = *(const long*)(S.a + arow * AROW + sub * 32 + kg);
       const float4 da4 = *(const float4*)(S.da + sub * TM + tok0);
       const float da[4] = {da4.x, da4.y, da4.z, da4.w};
+      float nm[4] = {0.f, 0.f, 0.f, 0.f};
+      if (FMT != FMT_Q8 && sub == 0) {
+        const float4 n4 = *(const float4*)(S.nmd + tok0);
+        nm[0] = n4.x; nm[1] = n4.y; nm[2] = n4.z; nm[3] = n4.w;
+      }
 #pragma unroll
       for (int t = 0; t < NTT; ++t) {
         const int col = 16 * t + (lane & 15);
         const long b = *(const long*)(S.w + col * AROW + sub * 32 + kg);
+        if constexpr (FMT != FMT_Q8) {
+          if (sub == 0) {   // compile-time after unrolling
+            const v4i cm = {GEMM_MAGIC_BITS, GEMM_MAGIC_BITS, GEMM_MAGIC_BITS, GEMM_MAGIC_BITS};
+            const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, cm, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bacc[t][r] = fmaf(__int_as_float(c[r]), da[r], nm[r]);
+            continue;
+          }
+        }
         v4i c = {0, 0, 0, 0};
         c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
         if constexpr (FMT == FMT_Q8) {
