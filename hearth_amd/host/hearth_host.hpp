@@ -355,6 +355,19 @@ struct Generation {
   double prefill_ms = 0.0, decode_ms = 0.0;
 };
 
+// ModelConfig::from_gguf (config.rs:57-217, qwen35.rs:470-530) with the KV
+// context cap of kv_budget.rs:19-58 (ctx_cap_override > 0 replaces it).
+inline Result<hh_model_config> read_config(const std::string& path, int ctx_cap_override = 0) {
+  hh_gguf* g = nullptr;
+  if (hh_gguf_open(path.c_str(), &g) != HH_OK) return Result<hh_model_config>::err(last_error("open"));
+  hh_model_config c{};
+  const int rc = hh_gguf_model_config(g, ctx_cap_override, &c);
+  std::string e = rc != HH_OK ? last_error("config") : std::string();
+  hh_gguf_close(g);
+  if (rc != HH_OK) return Result<hh_model_config>::err(e);
+  return Result<hh_model_config>::ok(c);
+}
+
 class Model {
  public:
   Model(Model&&) = default;

@@ -5,6 +5,7 @@
 //
 //   test_host --cpu    tests that need no device (the CPU suite runs these)
 //   test_host          every test (on a GPU box)
+//   --gguf PATH --seed N   also load PATH, a GGUF written from a model synthesized with seed N
 //
 // Each test prints "ok <name>" or "FAIL <name>: <reason>"; the exit status is
 // the number of failures (capped at 100).
@@ -445,10 +446,42 @@ TEST_GPU(test_model_errors) {
   REQUIRE(h.is_ok(), "forward after the errors: %s", h.error().c_str());
 }
 
+std::string g_gguf;     // --gguf PATH: a model file written from a synthesized model
+uint64_t g_gguf_seed = 0;
+
+// LlamaModel::load (mod.rs:103-150) of a GGUF file written from a model
+// synthesized with g_gguf_seed: the configuration reads back, and logits and
+// greedy tokens equal the synthesized model's bit for bit.
+TEST_GPU(test_load_gguf_matches_synthesized) {
+  if (g_gguf.empty()) return;   // run by tests/test_host_cpp.py with --gguf
+  hh_model_config cfg = must(read_config(g_gguf, 128), "read_config");
+  REQUIRE(cfg.max_seq == 128 && cfg.d_model > 0 && cfg.vocab > 0, "config %d %d %d", cfg.max_seq, cfg.d_model,
+          cfg.vocab);
+  Model ref = must(Model::create(gpu(), cfg), "create");
+  must(ref.synthesize(g_gguf_seed), "synthesize");
+  Model m = must(Model::load(gpu(), g_gguf, 128), "load");
+  std::vector<float> la = must(ref.forward(11, 0, cfg.vocab), "forward");
+  std::vector<float> lb = must(m.forward(11, 0, cfg.vocab), "forward");
+  REQUIRE(std::memcmp(la.data(), lb.data(), la.size() * 4) == 0, "logits differ");
+  must(ref.reset(), "reset");
+  must(m.reset(), "reset");
+  const std::vector<uint32_t> prompt = {11, 400, 7, 123};
+  Generation a = must(ref.generate(prompt, 8, SamplerConfig{1.0f}), "generate");
+  Generation b = must(m.generate(prompt, 8, SamplerConfig{1.0f}), "generate");
+  REQUIRE(a.tokens == b.tokens, "tokens differ");
+  auto missing = Model::load(gpu(), g_gguf + ".missing", 128);
+  REQUIRE(missing.is_err(), "a missing file loaded");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
-  const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+  bool cpu_only = false;
+  for (int i = 1; i < argc; ++i) {
+    if (std::strcmp(argv[i], "--cpu") == 0) cpu_only = true;
+    else if (std::strcmp(argv[i], "--gguf") == 0 && i + 1 < argc) g_gguf = argv[++i];
+    else if (std::strcmp(argv[i], "--seed") == 0 && i + 1 < argc) g_gguf_seed = std::strtoull(argv[++i], nullptr, 10);
+  }
   int failed = 0, ran = 0;
   for (const TestCase& t : registry()) {
     if (cpu_only && t.gpu) continue;

@@ -24,9 +24,30 @@ def test_host_cpu_tests():
     assert "FAIL" not in p.stdout and " 0 failed" in p.stdout, p.stdout
 
 
+def _write_synth_gguf(path, seed):
+    """A GGUF holding every tensor of a model synthesized on the device."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import gguf_writer as gw
+    import make_golden
+    from hearth_amd import Ctx, Model
+    ctx = Ctx(0)
+    m = Model(ctx, make_golden.DENSE)
+    m.synthesize(seed)
+    tensors = []
+    for name, t, ne0, ne1, nb in m.tensors():
+        shape = (ne0,) if ne1 == 1 and t == 0 else (ne0, ne1)
+        tensors.append((name, t, shape, m.download(name, nb).tobytes()))
+    gw.write_gguf(path, gw.model_meta(m.cfg), tensors)
+    m.close()
+    ctx.close()
+
+
 @pytest.mark.gpu
-def test_host_gpu_tests():
-    p = _run([], 600)
+def test_host_gpu_tests(tmp_path):
+    path = str(tmp_path / "dense.gguf")
+    _write_synth_gguf(path, 7)
+    p = _run(["--gguf", path, "--seed", "7"], 600)
     print(p.stdout)
     assert p.returncode == 0, p.stdout + p.stderr
     assert "FAIL" not in p.stdout and " 0 failed" in p.stdout, p.stdout
