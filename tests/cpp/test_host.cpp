@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <array>
 #include <functional>
 #include <random>
 #include <string>
@@ -361,6 +362,46 @@ TEST_GPU(test_rms_norm_rope_attention) {
   REQUIRE(md2 / mw2 < 1e-4, "attention rel %g", md2 / mw2);
 }
 
+// flash_attention_prefill (lib.rs:599-668; forward_batch's per-token attention,
+// mod.rs:1101-1140): the split/merge form gives each token's row bit for bit as
+// the decode operator at seq_len pos0 + t + 1; the fp32-MFMA form agrees to fp32
+// rounding (1e-5 of the largest output).
+TEST_GPU(test_flash_attention_prefill_modes) {
+  std::mt19937 rng(9);
+  std::normal_distribution<float> nd(0.0f, 1.0f);
+  for (auto geo : {std::array<int, 3>{32, 8, 128}, std::array<int, 3>{16, 4, 256}}) {
+    const int nh = geo[0], nkv = geo[1], hd = geo[2], pos0 = 37, ntok = 45, ms = 96;
+    std::vector<float> q((size_t)ntok * nh * hd), kc((size_t)nkv * ms * hd), vc((size_t)nkv * ms * hd);
+    for (auto& e : q) e = nd(rng);
+    for (auto& e : kc) e = nd(rng);
+    for (auto& e : vc) e = nd(rng);
+    auto qd = must(gpu().upload_f32(q), "upload");
+    auto kd = must(gpu().upload_f32(kc), "upload");
+    auto vd = must(gpu().upload_f32(vc), "upload");
+    auto o0 = gpu().readback_f32(
+        must(gpu().flash_attention_prefill(qd, kd, vd, PrefillAttnShape{nh, nkv, hd, ms, pos0, ntok, 0}), "prefill"),
+        q.size());
+    auto o1 = gpu().readback_f32(
+        must(gpu().flash_attention_prefill(qd, kd, vd, PrefillAttnShape{nh, nkv, hd, ms, pos0, ntok, 1}), "prefill"),
+        q.size());
+    double md = 0, mx = 0;
+    for (size_t i = 0; i < q.size(); ++i) {
+      md = std::fmax(md, std::fabs((double)o0[i] - o1[i]));
+      mx = std::fmax(mx, std::fabs((double)o0[i]));
+    }
+    REQUIRE(md <= 1e-5 * mx, "hd %d: flash form differs by %g of %g", hd, md, mx);
+    for (int t : {0, 17, ntok - 1}) {
+      std::vector<float> qt(q.begin() + (size_t)t * nh * hd, q.begin() + (size_t)(t + 1) * nh * hd);
+      auto qtd = must(gpu().upload_f32(qt), "upload");
+      auto dec = gpu().readback_f32(
+          must(gpu().flash_attention(qtd, kd, vd, FlashAttnShape{nh, nkv, hd, ms, pos0 + t + 1}), "attention"),
+          qt.size());
+      REQUIRE(std::memcmp(dec.data(), o0.data() + (size_t)t * nh * hd, dec.size() * 4) == 0,
+              "hd %d token %d: prefill row differs from the decode operator", hd, t);
+    }
+  }
+}
+
 hh_model_config tiny_dense() {
   hh_model_config c{};
   c.arch = 0; c.d_model = 1024; c.n_layers = 2; c.n_heads = 8; c.n_kv_heads = 4; c.head_dim = 128;
@@ -387,10 +428,12 @@ ho_config to_oracle(const hh_model_config& c) {
 }
 
 // generate_text's token loop (mod.rs:2718-3012 / qwen35.rs:1654-1804) on a
-// synthesized model: tokens and last logits equal the oracle's in the device's
-// association order, bit for bit.
+// synthesized model (dense, hybrid, dense with a Q8_0 KV cache): tokens equal
+// the oracle's in the device's association order.
 TEST_GPU(test_generate_matches_oracle) {
-  for (const hh_model_config& cfg : {tiny_dense(), tiny_hybrid()}) {
+  hh_model_config q8kv = tiny_dense();
+  q8kv.kv_type = HH_Q8_0;   // KVStorage::Q8_0 (kvcache.rs:41-57)
+  for (const hh_model_config& cfg : {tiny_dense(), tiny_hybrid(), q8kv}) {
     Model m = must(Model::create(gpu(), cfg), "create");
     must(m.synthesize(1234), "synthesize");
     const ho_config oc = to_oracle(cfg);
