@@ -247,6 +247,9 @@ def config_legs(ctx) -> dict:
     out["hbm_copy"] = microbench.copy_bandwidth()
     print(f"[bench] HBM copy {out['hbm_copy']['MiB']} MiB: {out['hbm_copy']['GB/s']} GB/s (read + write)",
           file=sys.stderr, flush=True)
+    out["hbm_read"] = microbench.read_bandwidth()
+    print(f"[bench] HBM read-only {out['hbm_read']['MiB']} MiB: {out['hbm_read']['GB/s']} GB/s",
+          file=sys.stderr, flush=True)
     g = microbench.run(reps=1000, formats=("Q1_0", "Q2_0"), shapes=microbench.SHAPES[:3])
     out["cfg1_gemv"] = [{k: r[k] for k in ("format", "n", "k", "us", "GB/s", "frac_peak", "cache_resident_us",
                                            "cache_resident_GB/s")} for r in g]

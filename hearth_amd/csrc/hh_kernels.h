@@ -204,3 +204,6 @@ int hh_gdn_launch(const GdnArgs& a, hipStream_t s);
 int hh_gdn_rows_launch(const GdnArgs& a, float* chunk_scratch, hipStream_t s);
 size_t hh_gdn_chunk_scratch_bytes(int n_v, int S);
 int hh_gdn_chunked_rec_launch(const GdnArgs& a, float* scratch, hipStream_t s);
+
+// Measurement: one read-only pass over nbytes (multiple of 16 * 8 * 512 * 1024).
+int hh_read_probe_launch(const void* p, int64_t nbytes, int* sink, hipStream_t s);

@@ -1386,6 +1386,23 @@ __global__ void k_count_tokens(const uint32_t* past, int64_t n, int* counts) {
   if (i < n) atomicAdd(counts + past[i], 1);
 }
 
+// Measurement: stream n16 16-byte words, 8 loads in flight per lane, and keep
+// nothing (the store needs a sum no launch produces: `never` is -1).  Its rate
+// is the read-only HBM ceiling the decode step's streams are judged against.
+__global__ __launch_bounds__(1024) void k_read_probe(const uint4* __restrict__ p, int64_t n16, int* sink, int never) {
+  uint32_t acc = 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 7 * stride < n16; i += 8 * stride) {
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[i + u * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].w;
+  }
+  if (acc == 0x12345678u && (int)threadIdx.x == never) *sink = (int)acc;
+}
+
 __global__ void k_fill_i32(int* p, int64_t n, int v) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -1774,3 +1791,8 @@ int hh_prefill_attn_mfma_launch(int hd, const float* QB, const float* k_cache, c
   return ok();
 }
 
+
+int hh_read_probe_launch(const void* p, int64_t nbytes, int* sink, hipStream_t s) {
+  hipLaunchKernelGGL(k_read_probe, dim3(512), dim3(1024), 0, s, (const uint4*)p, nbytes / 16, sink, -1);
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}

@@ -1478,6 +1478,40 @@ int hh_model_generate(hh_model* m, const uint32_t* prompt, int n_prompt, int sta
   return HH_OK;
 }
 
+int hh_read_bandwidth(hh_ctx* c, size_t nbytes, int reps, double* gbps) {
+  if (!c || !gbps || reps <= 0) return fail(HH_ERR_INVALID, "null argument");
+  const size_t unit = (size_t)16 * 8 * 512 * 1024;   // one pass of the probe's grid
+  if (nbytes < unit || nbytes % unit) return fail(HH_ERR_DIM, "nbytes must be a positive multiple of 64 MiB");
+  HIP_TRY(hipSetDevice(c->device));
+  void* p = nullptr;
+  HIP_TRY(hipMalloc(&p, nbytes));
+  struct Free {
+    void* p;
+    ~Free() { hipFree(p); }
+  } guard{p};
+  HIP_TRY(hipMemsetAsync(p, 1, nbytes, c->stream));
+  hipEvent_t a = nullptr, b = nullptr;
+  HIP_TRY(hipEventCreate(&a));
+  struct FreeEv {
+    hipEvent_t e[2];
+    ~FreeEv() {
+      for (hipEvent_t x : e)
+        if (x) hipEventDestroy(x);
+    }
+  } evs{{a, nullptr}};
+  HIP_TRY(hipEventCreate(&b));
+  evs.e[1] = b;
+  KTRY(hh_read_probe_launch(p, (int64_t)nbytes, c->counter, c->stream));   // warm-up
+  HIP_TRY(hipEventRecord(a, c->stream));
+  for (int r = 0; r < reps; ++r) KTRY(hh_read_probe_launch(p, (int64_t)nbytes, c->counter, c->stream));
+  HIP_TRY(hipEventRecord(b, c->stream));
+  HIP_TRY(hipEventSynchronize(b));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, a, b));
+  *gbps = (double)nbytes * reps / (ms * 1e-3) / 1e9;
+  return HH_OK;
+}
+
 int hh_model_time_stages(hh_model* m, int layer, int iters, double* out_ms, int n_out) {
   if (!m || !out_ms || iters <= 0) return fail(HH_ERR_INVALID, "bad argument");
   if (layer < 0 || layer >= m->cfg.n_layers) return fail(HH_ERR_RANGE, "layer out of range");

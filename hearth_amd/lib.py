@@ -170,6 +170,7 @@ _EXPORTS = {
                                      C.c_void_p]),
     "hh_model_last_decode_ms": (C.c_int, [C.c_void_p, C.POINTER(C.c_double)]),
     "hh_model_time_stages": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int]),
+    "hh_read_bandwidth": (C.c_int, [C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]),
     "hh_model_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     "hh_model_last_prefill_ms": (C.c_int, [C.c_void_p, C.POINTER(C.c_double)]),
     "hh_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),

@@ -14,6 +14,7 @@ as such) are reported beside the HBM figures.
         27B and 8B FFN shapes, 2048 tokens, against the dense int8 MFMA peak)
 """
 import argparse
+import ctypes as C
 import json
 import sys
 
@@ -141,6 +142,17 @@ def copy_bandwidth(mb: int = 1024, reps: int = 20) -> dict:
     del src, dst
     torch.cuda.empty_cache()
     return {"MiB": mb, "ms": round(ms, 4), "GB/s": round(2 * n / (ms * 1e-3) / 1e9, 1)}
+
+
+def read_bandwidth(mb: int = 2048, reps: int = 10) -> dict:
+    """The read-only HBM ceiling (hh_read_bandwidth): reps passes over mb MiB,
+    each lane keeping 8 16-byte loads in flight, bytes read per second."""
+    from hearth_amd.lib import Ctx, _check
+    ctx = Ctx(0)
+    v = C.c_double()
+    _check(ctx.lib.hh_read_bandwidth(ctx.h, mb << 20, reps, C.byref(v)))
+    ctx.close()
+    return {"MiB": mb, "GB/s": round(v.value, 1)}
 
 
 def copy_calibration(mb: int, reps: int = 4) -> None:

@@ -255,6 +255,12 @@ int hh_model_last_decode_ms(hh_model* m, double* ms);
  * outside a generation. */
 int hh_model_time_stages(hh_model* m, int layer, int iters, double* out_ms, int n_out);
 
+/* Measurement, no counterpart in the reference: the read-only HBM rate (GB/s) of
+ * reps passes over a fresh nbytes buffer (a multiple of 64 MiB), each lane
+ * keeping 8 16-byte loads in flight.  The ceiling a decode step, which is
+ * almost all reads, is measured against beside the published 8 TB/s. */
+int hh_read_bandwidth(hh_ctx* ctx, size_t nbytes, int reps, double* gbps);
+
 /* ---- GGUF files ----
  * A GGUF v2/v3 file, memory-mapped and parsed: header, metadata and tensor table
  * (hearth-gguf GgufFile::open, gguf.rs:138-218; tensor byte sizes from the

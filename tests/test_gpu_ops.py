@@ -303,3 +303,17 @@ def test_gemv_and_gemm_random_bytes(ctx, oracle, t, n_rows, kb, seq, seed):
         got = host(out).reshape(seq, n_rows)
         for s in range(seq):
             assert np.array_equal(got[s], want[s]), s
+
+
+def test_read_bandwidth_probe(ctx):
+    """hh_read_bandwidth (measurement): a rate below the published 8 TB/s, and
+    sizes the probe's grid does not tile are a dimension error."""
+    import ctypes as C
+    from hearth_amd import HHError
+    from hearth_amd.lib import _check
+    v = C.c_double()
+    _check(ctx.lib.hh_read_bandwidth(ctx.h, 256 << 20, 3, C.byref(v)))
+    assert 500.0 < v.value < 8000.0, v.value
+    with pytest.raises(HHError) as e:
+        _check(ctx.lib.hh_read_bandwidth(ctx.h, (64 << 20) + 16, 1, C.byref(v)))
+    assert e.value.status == 3
