@@ -74,7 +74,9 @@ def test_chunked_generate_tokens(ctx, oracle):
     token or one whose gap in the sequential logits is within the spread of
     the reference's own scalar and AVX2 arms (q2_0.rs:537-574 / :308-392),
     measured on the same model along the same sequence (first-max rule,
-    qwen35.rs:1735-1745)."""
+    qwen35.rs:1735-1745).  Measured on one MI355X: 16/16 tokens equal, worst
+    logit deviation 2.55e-2 relative, against 2.50e-2 between the reference's
+    two arms on the same sequence."""
     cfg = CONFIGS["9b-hybrid-q2"].replace(n_layers=4, max_seq=512)
     prompt = [oracle.synth_token(6, i, cfg.vocab) for i in range(200)]
     n_gen = 16
@@ -100,10 +102,11 @@ def test_chunked_generate_tokens(ctx, oracle):
     for i, t in enumerate(prompt[:-1]):
         ref.lib.ho_forward(ref.h, t, i, None)
         avx.lib.ho_forward(avx.h, t, i, None)
-    spread = 0.0
+    spread, spread_rel = 0.0, 0.0
     for i, t in enumerate(feed):
         a, b = ref.forward(t, len(prompt) - 1 + i), avx.forward(t, len(prompt) - 1 + i)
         spread = max(spread, float(np.abs(a.astype(np.float64) - b).max()))
+        spread_rel = max(spread_rel, float(np.abs(a.astype(np.float64) - b).max() / np.abs(a).max()))
     ref.close()
     avx.close()
     same, worst = 0, 0.0
@@ -118,7 +121,7 @@ def test_chunked_generate_tokens(ctx, oracle):
             gap = float(ls[i][ts[i]] - ls[i][got])
             assert gap <= spread, f"step {i}: token {got} != {ts[i]}, gap {gap:.3g} > arm spread {spread:.3g}"
     print(f"chunked: tokens equal {same}/{n_gen}, worst logit rel err {worst:.2e}, "
-          f"reference arm spread {spread:.3g}", flush=True)
+          f"reference arm spread {spread:.3g} ({spread_rel:.2e} relative)", flush=True)
 
 
 def test_chunked_falls_back_unless_every_ssm_a_is_negative(ctx, oracle):
