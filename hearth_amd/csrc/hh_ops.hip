@@ -342,7 +342,6 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   static_assert(NR * RPI == C && NR >= 1, "geometry");
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int s = blockIdx.x, kvh = blockIdx.y;
   const int G = GT > 0 ? GT : a.n_heads / a.n_kv;
   int seq, pos;
   bool prep;
@@ -352,7 +351,24 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
     pos = a.state->pos; seq = pos + 1; prep = true;
   }
   const int n_active = (seq + C - 1) / C;
-  if (s >= n_active) return;
+  // workgroup -> (chunk s, kv head): the last (partial) chunk of every kv head
+  // first, then the other chunks chunk-major; the grid's spare workgroups exit.
+  // A launch with more workgroups than CUs places the last ones beside
+  // another workgroup, where they run late; this puts the light chunk first
+  // and leaves the late places to whole chunks (8B at 2k context: the
+  // attention stage 13.2 -> 12.9 us in a timing build).
+  int s, kvh;
+  {
+    const int L = blockIdx.x, nk = a.n_kv;
+    if (L < nk) {
+      s = n_active - 1;
+      kvh = L;
+    } else {
+      s = (L - nk) / nk;
+      kvh = L - nk - s * nk;
+      if (s >= n_active - 1) return;
+    }
+  }
   const int p0 = s * C, np = min(C, seq - p0);
   const bool has_new = prep && pos >= p0 && pos < p0 + np;
   const int sub = tid / LPR, c = tid % LPR;
@@ -1582,7 +1598,7 @@ int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
   if (a.chunk != 8192 / a.hd || a.n_kv * G != a.n_heads || G > 8) return 1;
   const size_t split_lds = 4 * ((size_t)G * a.chunk + 2 * G + 8 + (ATTN_NT / 64) * 4 * (size_t)a.hd);
   const size_t merge_lds = 4 * ((size_t)a.max_splits + 256 + 4);
-  const dim3 g(a.max_splits, a.n_kv), b(ATTN_NT);
+  const dim3 g(a.max_splits * a.n_kv), b(ATTN_NT);
   auto split = [&](auto hd_c, auto kv8_c) {
     constexpr int HD = decltype(hd_c)::value;
     constexpr bool KV8 = decltype(kv8_c)::value;
