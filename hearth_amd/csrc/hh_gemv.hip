@@ -354,6 +354,10 @@ constexpr int PK_L = NT;
 // t + NORM_L*j (j < NJ).  Sum of squares in the order of block_sumsq_f4:
 // slot s sums its float4s in c order as ss + (((x0^2 + x1^2) + x2^2) + x3^2),
 // slots 64w .. 64w+63 reduce by butterfly into W_w, the total is tree16(W).
+// Words per row of the GEMV block-product buffer: 2P products rounded up to a
+// multiple of 8, plus 4.
+__host__ __device__ inline int gemv_part_stride(int P) { return ((2 * P + 7) & ~7) + 4; }
+
 constexpr int NORM_CH = 2;   // K <= 8192
 template <int NL> struct NormRegsT {
   static constexpr int NJ = 1024 / NL;
@@ -728,11 +732,19 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   const int nunits_act = K / UnitT<FMT>::EL;
   int8_t* aq = (int8_t*)smem;
   float* ds = (float*)(smem + nunits_act * qstride<FMT>());
-  // block products, transposed: part[j * RS + row] for product j = 2*unit + blk,
-  // RS = rows + 1, so the row-sum pass (one lane per row) reads consecutive words
-  float* part = ds + nunits_act * dss<FMT>();
+  // Block products by row: part[row * RSJ + j] for product j = 2*unit + blk,
+  // RSJ = 4 (mod 8) words, so the row-sum pass (one lane per row, 16-byte
+  // reads) puts each 8 lanes' reads on distinct banks; they follow rowsum and
+  // the prologue buffers (below).  The rotating prologues keep them
+  // transposed, part[j * RS + row] with RS = rows + 1, ahead of the wave
+  // partials: there the by-row form costs the compiler 12-48 more bytes of
+  // spills per lane.
+  constexpr bool PART_T = PRO == PRO_NORMROT || PRO == PRO_F32ROT;
+  const int NPR = 2 * P;
+  const int RSJ = gemv_part_stride(P);
   const int RS = rows_total + 1;
-  float* red = part + 2 * P * RS;   // 16 wave partials
+  float* part = ds + nunits_act * dss<FMT>();
+  float* red = PART_T ? part + 2 * P * RS : part;   // 16 wave partials
   float* rowsum = red + 16;
 
   auto unit_addr = [&](int lu) -> const uint8_t* {
@@ -789,8 +801,12 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
         float pr[2];
         const float* ud = ds + t * dss<FMT>();
         unit_dot<FMT>(wr[d], aq + t * qstride<FMT>(), ud, (const int*)(ud + UnitT<FMT>::SUBS), pr);
-        part[(2 * t) * RS + rl] = pr[0];
-        part[(2 * t + 1) * RS + rl] = pr[1];
+        if constexpr (PART_T) {
+          part[(2 * t) * RS + rl] = pr[0];
+          part[(2 * t + 1) * RS + rl] = pr[1];
+        } else {
+          *(float2*)(part + rl * RSJ + 2 * t) = make_float2(pr[0], pr[1]);
+        }
       }
     }
   };
@@ -805,8 +821,10 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
     if (ab) {
       if constexpr (PRO == PRO_RMSNORM || PRO == PRO_RMSNORM_ALL) act.r.nbuf = lds_tail;
       else act.nbuf = lds_tail;
+      lds_tail += K;
     }
   }
+  if constexpr (!PART_T) part = lds_tail;
   act.issue(p);                      // activation first (in-order retirement)
   // the residual of this lane's row (EPI_ADD), read now rather than after the
   // row sums, where its round trip would be the kernel's last step
@@ -881,19 +899,42 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   __syncthreads();
 
   // per-row sums over the block products in block order (the scalar loop);
-  // 16 products are fetched per round trip, the additions stay sequential
-  const int NPR = 2 * P;
+  // 16 products per round trip; the additions stay sequential
   for (int r = tid; r < rows_total; r += NT) {
     float s = 0.0f;
     int j = 0;
-    for (; j + 16 <= NPR; j += 16) {
-      float v[16];
+    if constexpr (PART_T) {
+      for (; j + 16 <= NPR; j += 16) {
+        float v[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = part[(j + i) * RS + r];
+        for (int i = 0; i < 16; ++i) v[i] = part[(j + i) * RS + r];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s += v[i];
+        for (int i = 0; i < 16; ++i) s += v[i];
+      }
+      for (; j < NPR; ++j) s += part[j * RS + r];
+    } else {
+      const float* pr = part + r * RSJ;
+      for (; j + 16 <= NPR; j += 16) {
+        float4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = ((const float4*)(pr + j))[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s += v[i].x;
+          s += v[i].y;
+          s += v[i].z;
+          s += v[i].w;
+        }
+      }
+      for (; j + 4 <= NPR; j += 4) {
+        const float4 v = *(const float4*)(pr + j);
+        s += v.x;
+        s += v.y;
+        s += v.z;
+        s += v.w;
+      }
+      for (; j < NPR; ++j) s += pr[j];
     }
-    for (; j < NPR; ++j) s += part[j * RS + r];
     rowsum[r] = s;
   }
   // EPI_STORE / EPI_ADD read rowsum[r] in the lane that wrote it (and the
@@ -1268,7 +1309,9 @@ size_t hh_gemv_lds(int fmt, int K, int rows_total_per_wg) {
   int P = K / el;
   size_t qb = (size_t)(K / el) * (el + 16);
   size_t dsb = (size_t)(K / el) * (fmt == FMT_Q8 ? 8 : 20) * 4;
-  size_t b = qb + dsb + (size_t)(rows_total_per_wg + 1) * P * 8 + 16 * 4 + (size_t)rows_total_per_wg * 4;
+  // block products: by row (gemv_part_stride) or transposed (rows + 1 per product)
+  const size_t pw = std::max((size_t)rows_total_per_wg * gemv_part_stride(P), (size_t)(rows_total_per_wg + 1) * 2 * P);
+  size_t b = qb + dsb + 16 * 4 + (size_t)rows_total_per_wg * 4 + 16 + pw * 4;
   return (b + 15) & ~(size_t)15;
 }
 
