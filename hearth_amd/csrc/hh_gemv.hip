@@ -899,7 +899,8 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
   __syncthreads();
 
   // per-row sums over the block products in block order (the scalar loop);
-  // 16 products per round trip; the additions stay sequential
+  // by row: up to 32 products per LDS round trip (16-byte reads); transposed:
+  // 16; the additions stay sequential
   for (int r = tid; r < rows_total; r += NT) {
     float s = 0.0f;
     int j = 0;
@@ -914,6 +915,18 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs p) {
       for (; j < NPR; ++j) s += part[j * RS + r];
     } else {
       const float* pr = part + r * RSJ;
+      for (; j + 32 <= NPR; j += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ((const float4*)(pr + j))[i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          s += v[i].x;
+          s += v[i].y;
+          s += v[i].z;
+          s += v[i].w;
+        }
+      }
       for (; j + 16 <= NPR; j += 16) {
         float4 v[4];
 #pragma unroll
