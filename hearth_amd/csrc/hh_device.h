@@ -391,6 +391,18 @@ HH_DEV int32_t synth_int(uint64_t key, uint64_t idx) {
 // is lgkmcnt(0)), putting the state's round trip ahead of them.
 HH_DEV int state_lanes(const void* st) { return ((const int*)st)[threadIdx.x & 7]; }
 
+// Positions per attention split (one workgroup per chunk and kv head): 8192 /
+// hd, or twice that once the chunks of all kv heads at that width would
+// outnumber MI355X's 256 CUs.  Past that count the last workgroups share a CU
+// with another and finish late, and wider chunks take fewer barriers per
+// position; below it the narrow chunk keeps more workgroups busy.  8B decode
+// step, narrow only -> this rule: 1k context 1.387 -> 1.391 ms, 2k 1.497 ->
+// 1.490, 4k 1.679 -> 1.616, 8k 2.007 -> 1.886.
+__host__ __device__ inline int attn_chunk_for(int seq, int hd, int n_kv) {
+  const int c = 8192 / hd;
+  return (long long)((seq + c - 1) / c) * n_kv > 256 ? 2 * c : c;
+}
+
 struct StepState {
   int pos;        // position of the token being fed
   int step;       // steps executed in this session

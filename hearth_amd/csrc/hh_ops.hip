@@ -336,20 +336,13 @@ HH_DEV float4 kv_q8_store(float4 x, const KvQ8& kv, size_t row, int hd, int c, b
 
 // GT: the GQA group size n_heads / n_kv when it is one of the instantiated
 // values (the per-head loops then have exact trip counts), 0 = read at run time.
-template <int HD, int NTA, bool KV8, int GT>
-__global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
-  constexpr int LPR = HD / 4, RPI = NTA / LPR, C = 8192 / HD, NR = C / RPI, NW = NTA / 64;
-  static_assert(NR * RPI == C && NR >= 1, "geometry");
+// The split body for chunks of C positions (attn_chunk_for).
+template <int HD, int NTA, bool KV8, int GT, int C>
+HH_DEV void attn_split_body(const AttnArgs& a, int G, int seq, int pos, bool prep) {
+  constexpr int LPR = HD / 4, RPI = NTA / LPR, NR = C / RPI, NW = NTA / 64;
+  static_assert(NR * RPI == C && NR >= 1 && C <= 128, "geometry");
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int G = GT > 0 ? GT : a.n_heads / a.n_kv;
-  int seq, pos;
-  bool prep;
-  if (a.fixed_seq > 0) {
-    seq = a.fixed_seq; pos = -1; prep = false;
-  } else {
-    pos = a.state->pos; seq = pos + 1; prep = true;
-  }
   const int n_active = (seq + C - 1) / C;
   // workgroup -> (chunk s, kv head): the last (partial) chunk of every kv head
   // first, then the other chunks chunk-major; the grid's spare workgroups exit.
@@ -478,14 +471,26 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
     if (h < G && (lane & ((1 << KSH) - 1)) == 0) sc[h * C + j] = (j < np) ? r * inv_sqrt : -INFINITY;
   }
   __syncthreads();
-  // 5. per-head softmax statistics over the chunk (C <= 64)
+  // 5. per-head softmax statistics over the chunk (C = 128: two positions per
+  // lane, added before the butterfly)
   for (int h = wid; h < G; h += NW) {
-    float x = lane < C ? sc[h * C + lane] : -INFINITY;
-    float m = wave_max_nonan(x);
-    float e = (lane < np) ? hx_exp(x - m) : 0.0f;
-    float l = wave_sum(e);
-    if (lane < C) sc[h * C + lane] = e;
-    if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
+    if constexpr (C <= 64) {
+      float x = lane < C ? sc[h * C + lane] : -INFINITY;
+      float m = wave_max_nonan(x);
+      float e = (lane < np) ? hx_exp(x - m) : 0.0f;
+      float l = wave_sum(e);
+      if (lane < C) sc[h * C + lane] = e;
+      if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
+    } else {
+      const float x0 = sc[h * C + lane], x1 = sc[h * C + 64 + lane];
+      const float m = wave_max_nonan(fmaxf(x0, x1));
+      const float e0 = (lane < np) ? hx_exp(x0 - m) : 0.0f;
+      const float e1 = (64 + lane < np) ? hx_exp(x1 - m) : 0.0f;
+      const float l = wave_sum(e0 + e1);
+      sc[h * C + lane] = e0;
+      sc[h * C + 64 + lane] = e1;
+      if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
+    }
   }
   __syncthreads();
   // 6. o = sum_j e_j v_j
@@ -544,6 +549,20 @@ __global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
   }
 }
 
+template <int HD, int NTA, bool KV8, int GT>
+__global__ __launch_bounds__(NTA) void k_attn_split(AttnArgs a) {
+  const int G = GT > 0 ? GT : a.n_heads / a.n_kv;
+  int seq, pos;
+  bool prep;
+  if (a.fixed_seq > 0) {
+    seq = a.fixed_seq; pos = -1; prep = false;
+  } else {
+    pos = a.state->pos; seq = pos + 1; prep = true;
+  }
+  if (attn_chunk_for(seq, HD, a.n_kv) == 8192 / HD) attn_split_body<HD, NTA, KV8, GT, 8192 / HD>(a, G, seq, pos, prep);
+  else attn_split_body<HD, NTA, KV8, GT, 16384 / HD>(a, G, seq, pos, prep);
+}
+
 // Merge kernel: workgroup (qh, 64-column slice).  M = max m_t, w_t =
 // exp(m_t - M), L = sum w_t l_t (lane-strided over t, then a butterfly);
 // wave g sums the splits t = g (mod 4) as an fma chain in increasing t, and
@@ -558,7 +577,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int qh = blockIdx.x, d = blockIdx.y * 64 + lane;
   const int G = a.n_heads / a.n_kv, kvh = qh / G, h = qh % G;
-  constexpr int C = (256 / (HD / 4)) * 8;
+
   // The step position is a vector load among the others (a scalar load's
   // wait would also cover the kernel arguments, putting its round trip ahead
   // of every load below); the loads of the first 64 splits clamp to the grid,
@@ -586,6 +605,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
     pv[i] = pb[(size_t)t * tstride];
   }
   const int seq = a.fixed_seq > 0 ? a.fixed_seq : __builtin_amdgcn_readfirstlane(sv) + 1;
+  const int C = attn_chunk_for(seq, HD, a.n_kv);
   const int n_active = (seq + C - 1) / C;
   if (wid == 0) {
     float M = lane < n_active ? ml0.x : -INFINITY;
@@ -880,12 +900,12 @@ __global__ __launch_bounds__(512) void k_prefill_qk(const float* __restrict__ QK
 // order) once per token of the tile whose position reaches the chunk, NTOK
 // tokens per pass.  GMAX bounds the query heads per kv head (registers).
 // Partials: PO[((sl*n_kv + kvh)*n_chunks + c)*G + h][HD], PML likewise x2.
-template <int HD, int NTA, bool KV8, int GMAX, int NTOK, int GT>
+template <int HD, int NTA, bool KV8, int GMAX, int NTOK, int GT, int C>
 __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restrict__ QB, const float* __restrict__ k_cache,
                                                             const float* __restrict__ v_cache, int n_heads, int n_kv,
                                                             int max_seq, int pos0, int S, int t0, int TT, int n_chunks,
                                                             float* __restrict__ PO, float* __restrict__ PML) {
-  constexpr int LPR = HD / 4, RPI = NTA / LPR, C = 8192 / HD, NR = C / RPI, NW = NTA / 64;
+  constexpr int LPR = HD / 4, RPI = NTA / LPR, NR = C / RPI, NW = NTA / 64;
   extern __shared__ __align__(16) float sm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c = blockIdx.x, kvh = blockIdx.y, G = GT > 0 ? GT : n_heads / n_kv;
@@ -972,12 +992,23 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
       const int u = pr / G, h = pr % G;
       const int np = min(C, pos0 + t0 + sl + u + 1 - p0);
       float* row = sc + (u * G + h) * C;
-      float x = lane < C ? row[lane] : -INFINITY;
-      float m = wave_max_nonan(x);
-      float e = (lane < np) ? hx_exp(x - m) : 0.0f;
-      float l = wave_sum(e);
-      if (lane < C) row[lane] = e;
-      if (lane == 0) { ml[(u * G + h) * 2] = m; ml[(u * G + h) * 2 + 1] = l; }
+      if constexpr (C <= 64) {
+        float x = lane < C ? row[lane] : -INFINITY;
+        float m = wave_max_nonan(x);
+        float e = (lane < np) ? hx_exp(x - m) : 0.0f;
+        float l = wave_sum(e);
+        if (lane < C) row[lane] = e;
+        if (lane == 0) { ml[(u * G + h) * 2] = m; ml[(u * G + h) * 2 + 1] = l; }
+      } else {   // C = 128, as the decode split
+        const float x0 = row[lane], x1 = row[64 + lane];
+        const float m = wave_max_nonan(fmaxf(x0, x1));
+        const float e0 = (lane < np) ? hx_exp(x0 - m) : 0.0f;
+        const float e1 = (64 + lane < np) ? hx_exp(x1 - m) : 0.0f;
+        const float l = wave_sum(e0 + e1);
+        row[lane] = e0;
+        row[64 + lane] = e1;
+        if (lane == 0) { ml[(u * G + h) * 2] = m; ml[(u * G + h) * 2 + 1] = l; }
+      }
     }
     __syncthreads();
     for (int hg = 0; hg < G; hg += 4) {
@@ -1068,11 +1099,11 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
 // input in the GEMM's split layout.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prefill_merge(const float* __restrict__ PO, const float* __restrict__ PML,
-                                                            int n_heads, int n_kv, int n_chunks, int pos0, int t0, int n,
-                                                            const float* __restrict__ gate, int gate_row,
+                                                            int n_heads, int n_kv, int n_chunks, int C, int pos0, int t0,
+                                                            int n, const float* __restrict__ gate, int gate_row,
                                                             int8_t* __restrict__ yq, float* __restrict__ yd,
                                                             float* __restrict__ yf) {
-  constexpr int CPL = HD / 64, C = 8192 / HD;
+  constexpr int CPL = HD / 64;
   extern __shared__ __align__(16) float wm[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   float* wts = wm + wid * n_chunks;        // this wave's split weights
@@ -1596,7 +1627,7 @@ int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
   const int G = a.n_heads / a.n_kv;
   if (a.hd != 128 && a.hd != 256) return 1;
   if (a.chunk != 8192 / a.hd || a.n_kv * G != a.n_heads || G > 8) return 1;
-  const size_t split_lds = 4 * ((size_t)G * a.chunk + 2 * G + 8 + (ATTN_NT / 64) * 4 * (size_t)a.hd);
+  const size_t split_lds = 4 * ((size_t)G * 2 * a.chunk + 2 * G + 8 + (ATTN_NT / 64) * 4 * (size_t)a.hd);   // wide chunks
   const size_t merge_lds = 4 * ((size_t)a.max_splits + 256 + 4);
   const dim3 g(a.max_splits * a.n_kv), b(ATTN_NT);
   auto split = [&](auto hd_c, auto kv8_c) {
@@ -1742,7 +1773,10 @@ int hh_prefill_qk_launch(int hd, const float* QKV, int n_in, int n_heads, int n_
   return ok();
 }
 
-// Attention for tokens [t0, t0 + n) of a prefill; PO/PML hold n tokens' partials.
+// Attention for tokens [t0, t0 + n) of a prefill; PO/PML hold n tokens'
+// partials at a stride of n_chunks narrow chunks.  Each token uses the chunk
+// width the decode step uses at its sequence length (attn_chunk_for): the
+// tokens below the width's threshold and those past it go as two passes.
 int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const float* v_cache, int n_heads, int n_kv,
                            int max_seq, int pos0, int t0, int n, int n_chunks, float* PO, float* PML,
                            const float* gate, int gate_row, int kv_q8, int8_t* yq, float* yd, float* yf,
@@ -1751,37 +1785,57 @@ int hh_prefill_attn_launch(int hd, const float* QB, const float* k_cache, const 
   // 9B/27B shapes; more tokens per pass cost occupancy at 256)
   const int NTOK = hd == 128 ? 4 : 1;
   const int G = n_heads / n_kv, TT = 16;
-  if (G > 8 || n_kv * G != n_heads) return 1;
-  const size_t split_lds =
-      4 * (NTOK * ((size_t)G * (8192 / hd) + 2 * G + (ATTN_NT / 64) * 4 * (size_t)hd) + 8);
-  const size_t merge_lds = 4 * (4 * (size_t)n_chunks);
-  dim3 g1(n_chunks, n_kv, (n + TT - 1) / TT), g2((n * n_heads + 3) / 4);
-#define HH_PSPLIT(HDV, KV, GM, GTV)                                                                          \
-  hipLaunchKernelGGL((k_attn_prefill_split<HDV, ATTN_NT, KV, GM, HDV == 128 ? 4 : 1, GTV>), g1, dim3(ATTN_NT), \
-                     split_lds, s, QB, k_cache, v_cache, n_heads, n_kv, max_seq, pos0, t0 + n, t0, TT, n_chunks, PO, \
+  if (G > 8 || n_kv * G != n_heads || (hd != 128 && hd != 256)) return 1;
+  const int cn = 8192 / hd;
+  // token t (sequence length pos0 + t + 1) takes the wide chunk past seq_wide
+  const int seq_wide = cn * (256 / n_kv);
+  const int tw = std::min(t0 + n, std::max(t0, seq_wide - pos0));
+  auto pass = [&](int ta, int na, int C) -> int {
+    if (na <= 0) return 0;
+    // the grid's chunk count: the caller's stride for the narrow pass (its XCD
+    // spread), for the wide one the chunks it reaches rounded up to 3 mod 8 the
+    // same way; workgroups past a token tile's last chunk exit
+    int nc = n_chunks;
+    if (C != cn) {
+      nc = (pos0 + ta + na + C - 1) / C;
+      nc += (3 - nc % 8 + 8) % 8;
+    }
+    const size_t split_lds = 4 * (NTOK * ((size_t)G * C + 2 * G + (ATTN_NT / 64) * 4 * (size_t)hd) + 8);
+    const size_t merge_lds = 4 * (4 * (size_t)n_chunks);
+    dim3 g1(nc, n_kv, (na + TT - 1) / TT), g2((na * n_heads + 3) / 4);
+#define HH_PSPLIT(HDV, KV, GM, GTV, CV)                                                                           \
+  hipLaunchKernelGGL((k_attn_prefill_split<HDV, ATTN_NT, KV, GM, HDV == 128 ? 4 : 1, GTV, CV>), g1, dim3(ATTN_NT), \
+                     split_lds, s, QB, k_cache, v_cache, n_heads, n_kv, max_seq, pos0, ta + na, ta, TT, n_chunks, PO, \
                      PML)
-  // group sizes 4 and 8 get exact trip counts (GT), others read G at run time
-#define HH_PSPLIT_G(HDV, KV)                                          \
+    // group sizes 4 and 8 get exact trip counts (GT), others read G at run time
+#define HH_PSPLIT_G(HDV, KV, CV)                                      \
   do {                                                                \
-    if (G == 4) HH_PSPLIT(HDV, KV, 4, 4);                             \
-    else if (G < 4) HH_PSPLIT(HDV, KV, 4, 0);                         \
-    else if (G == 8) HH_PSPLIT(HDV, KV, 8, 8);                        \
-    else HH_PSPLIT(HDV, KV, 8, 0);                                    \
+    if (G == 4) HH_PSPLIT(HDV, KV, 4, 4, CV);                         \
+    else if (G < 4) HH_PSPLIT(HDV, KV, 4, 0, CV);                     \
+    else if (G == 8) HH_PSPLIT(HDV, KV, 8, 8, CV);                    \
+    else HH_PSPLIT(HDV, KV, 8, 0, CV);                                \
   } while (0)
-  if (hd == 128) {
-    if (kv_q8) HH_PSPLIT_G(128, true); else HH_PSPLIT_G(128, false);
-    hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, n, gate, gate_row, yq, yd, yf);
-  } else if (hd == 256) {
-    if (kv_q8) HH_PSPLIT_G(256, true); else HH_PSPLIT_G(256, false);
-    hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, pos0,
-                       t0, n, gate, gate_row, yq, yd, yf);
-  } else {
-    return 1;
-  }
+#define HH_PSPLIT_C(HDV, KV)                                          \
+  do {                                                                \
+    if (C == 8192 / HDV) HH_PSPLIT_G(HDV, KV, 8192 / HDV);            \
+    else HH_PSPLIT_G(HDV, KV, 16384 / HDV);                           \
+  } while (0)
+    if (hd == 128) {
+      if (kv_q8) HH_PSPLIT_C(128, true); else HH_PSPLIT_C(128, false);
+      hipLaunchKernelGGL(k_attn_prefill_merge<128>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, C,
+                         pos0, ta, na, gate, gate_row, yq, yd, yf);
+    } else {
+      if (kv_q8) HH_PSPLIT_C(256, true); else HH_PSPLIT_C(256, false);
+      hipLaunchKernelGGL(k_attn_prefill_merge<256>, g2, dim3(256), merge_lds, s, PO, PML, n_heads, n_kv, n_chunks, C,
+                         pos0, ta, na, gate, gate_row, yq, yd, yf);
+    }
+#undef HH_PSPLIT_C
 #undef HH_PSPLIT_G
 #undef HH_PSPLIT
-  return ok();
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+  };
+  if (pass(t0, tw - t0, cn)) return 1;
+  return pass(tw, t0 + n - tw, 2 * cn);
 }
 
 // The whole prompt's attention on fp32 MFMA (k_attn_prefill_mfma): tokens

@@ -1004,15 +1004,27 @@ static float bfly_n(const float* v, int n) {
 /* Lanes per workgroup of the device's attention split kernel (ATTN_NT). */
 #define DEV_ATTN_NT 512
 
-/* Split-sequence attention in the device's grouping: chunks of C = 8192/hd
- * positions; a score is the butterfly over hd/4 column slices of a 4-term
- * fma chain; the chunk's o is summed per row group (rows i*RPI + sub) as an
- * fma chain over i and the groups are combined pairwise; splits merge with
- * w_t = exp(m_t - M) as four strided fma chains added pairwise.  The
- * reference computes the same softmax-weighted sum in one pass
- * (ops.rs:353-406). */
-static void dev_attention(const float* q, const float* k, const float* v, int seq, int hd, float* out) {
-  const int C = 8192 / hd, LPR = hd / 4, RPI = DEV_ATTN_NT / LPR, NR = C / RPI, NW = DEV_ATTN_NT / 64;
+/* CUs of the device whose split geometry the device order follows (MI355X). */
+#define DEV_ATTN_CUS 256
+
+/* Positions per split: 8192/hd, or twice that once the (chunk, kv head) pairs
+ * at that width outnumber the device's CUs. */
+static int dev_attn_chunk(int seq, int hd, int n_kv) {
+  int c = 8192 / hd;
+  return (int64_t)((seq + c - 1) / c) * n_kv > DEV_ATTN_CUS ? 2 * c : c;
+}
+
+/* Split-sequence attention in the device's grouping: chunks of C positions
+ * (dev_attn_chunk); a score is the butterfly over hd/4 column slices of a
+ * 4-term fma chain; a chunk's softmax sum is the 64-lane butterfly of its e
+ * values (C = 128: of e_l + e_{64+l}); the chunk's o is summed per row group
+ * (rows i*RPI + sub) as an fma chain over i and the groups are combined
+ * pairwise; splits merge with w_t = exp(m_t - M) as four strided fma chains
+ * added pairwise.  The reference computes the same softmax-weighted sum in
+ * one pass (ops.rs:353-406). */
+static void dev_attention(const float* q, const float* k, const float* v, int seq, int hd, int n_kv, float* out) {
+  const int C = dev_attn_chunk(seq, hd, n_kv), LPR = hd / 4, RPI = DEV_ATTN_NT / LPR, NR = C / RPI,
+            NW = DEV_ATTN_NT / 64;
   const int ns = (seq + C - 1) / C;
   float inv_sqrt = 1.0f / sqrtf((float)hd);
   float* ms = (float*)malloc(sizeof(float) * (size_t)ns * (hd + 3));
@@ -1021,8 +1033,8 @@ static void dev_attention(const float* q, const float* k, const float* v, int se
   float* os = wts + ns;
   for (int s = 0; s < ns; s++) {
     int p0 = s * C, np = seq - p0 < C ? seq - p0 : C;
-    float sc[64], e[64], parts[64];
-    for (int l = 0; l < 64; l++) sc[l] = -INFINITY;
+    float sc[128], e[128], parts[64], lanes[64];
+    for (int l = 0; l < 128; l++) sc[l] = -INFINITY;
     for (int j = 0; j < np; j++) {
       const float* kr = k + (size_t)(p0 + j) * hd;
       for (int c = 0; c < LPR; c++) {
@@ -1035,10 +1047,11 @@ static void dev_attention(const float* q, const float* k, const float* v, int se
       sc[j] = bfly_n(parts, LPR) * inv_sqrt;
     }
     float m = -INFINITY;
-    for (int l = 0; l < 64; l++) m = fmaxf(m, sc[l]);
-    for (int l = 0; l < 64; l++) e[l] = l < np ? ho_exp(sc[l] - m) : 0.0f;
+    for (int l = 0; l < 128; l++) m = fmaxf(m, sc[l]);
+    for (int l = 0; l < 128; l++) e[l] = l < np ? ho_exp(sc[l] - m) : 0.0f;
     ms[s] = m;
-    ls[s] = bfly64(e);
+    for (int l = 0; l < 64; l++) lanes[l] = C > 64 ? e[l] + e[64 + l] : e[l];
+    ls[s] = bfly64(lanes);
     for (int d = 0; d < hd; d++) {
       float A[64] = {0}, X[32];
       for (int sub = 0; sub < RPI; sub++) {
@@ -1541,7 +1554,7 @@ static int forward_dense(ho_model* m, uint32_t token, int pos, float* logits) {
     for (int qh = 0; qh < nh; qh++) {
       int kvh = qh / rep;
       if (m->order)
-        dev_attention(m->q + qh * hd, kbase + kvh * head_stride, vbase + kvh * head_stride, seq_len, hd,
+        dev_attention(m->q + qh * hd, kbase + kvh * head_stride, vbase + kvh * head_stride, seq_len, hd, nkvh,
                       m->attn_out + qh * hd);
       else
         ho_attention(m->q + qh * hd, kbase + kvh * head_stride, vbase + kvh * head_stride, seq_len, hd,
@@ -1745,7 +1758,7 @@ static void attn_layer_q35(ho_model* m, int pos, layer_t* ly) {
     int kvh = qh / rep;
     const float* qq = m->q + qh * hd;
     if (m->order) {
-      dev_attention(qq, kb + kvh * hs, vb + kvh * hs, seq_len, hd, m->attn_out + qh * hd);
+      dev_attention(qq, kb + kvh * hs, vb + kvh * hs, seq_len, hd, nkvh, m->attn_out + qh * hd);
       continue;
     }
     for (int t = 0; t < seq_len; t++) {

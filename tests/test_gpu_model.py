@@ -294,10 +294,14 @@ def _model_with_env(ctx, cfg, seed, env):
                                           (CONFIGS["8b-q2"].replace(n_layers=2, max_seq=640, kv_type=8), 300),
                                           (TINY.replace(n_heads=16, n_kv_heads=2, max_seq=160), 70),
                                           (TINY.replace(n_heads=12, n_kv_heads=4, max_seq=160), 70),
-                                          (TINY.replace(n_heads=4, n_kv_heads=4, max_seq=160), 70)],
+                                          (TINY.replace(n_heads=4, n_kv_heads=4, max_seq=160), 70),
+                                          (TINY.replace(n_heads=32, n_kv_heads=32, max_seq=640), 600),
+                                          (TINY.replace(n_heads=32, n_kv_heads=32, max_seq=640, kv_type=8), 600),
+                                          (TINY.replace(head_dim=256, n_heads=16, n_kv_heads=16, max_seq=640), 600)],
                          ids=["dense-q2", "dense-q1", "8b-2layer-300", "dense-ptq1", "hybrid-2", "hybrid-8",
                               "hybrid-pq2-36", "9b-4layer-300", "dense-kvq8", "hybrid-kvq8", "8b-kvq8-300",
-                              "dense-g8-70", "dense-g3-70", "dense-g1-70"])
+                              "dense-g8-70", "dense-g3-70", "dense-g1-70", "wide-chunks-600", "wide-chunks-kvq8-600",
+                              "wide-chunks-hd256-600"])
 def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
     """forward_batch on the MFMA GEMM leaves the same KV cache (and, on the
     hybrids, the same conv windows and GDN states) as feeding the prompt one
@@ -307,7 +311,10 @@ def test_batched_prefill_equals_token_by_token(ctx, oracle, cfg, n_prompt):
     tokens than the conv window holds; the kvq8 cases write a Q8_0 cache
     (quantized on write as the decode step does); the g8 / g3 / g1 cases take
     the attention kernels' other query-group sizes (8 and 1 exact, 3 read at
-    run time) over more than one 64-position chunk."""
+    run time) over more than one 64-position chunk.  The wide-chunks cases have
+    32 kv heads (16 at head_dim 256), so past 512 positions the attention
+    splits take twice the positions per workgroup: the prompt's later tokens
+    and the decode steps after it run the wide arithmetic."""
     print(f"prefill {cfg.d_model} {cfg.n_layers} n={n_prompt}", flush=True)
     pen = 1.1 if cfg.arch == 0 else 1.0
     prompt = [oracle.synth_token(11, i, cfg.vocab) for i in range(n_prompt)]
