@@ -259,7 +259,8 @@ template <int N, int O> struct ReduceScatterSel {
 };
 
 // Split kernel: workgroup (s, kvh) owns positions [s*C, s*C + C) of kv head
-// kvh (C = 8192/hd) for its G query heads, with ATTN_NT lanes.  Thread t
+// kvh (C = attn_chunk_for: 8192/hd or twice that) for its G query heads,
+// with ATTN_NT lanes.  Thread t
 // holds one float4 column slice (c = t % LPR) of rows j = i*RPI + t/LPR,
 // i < NR, of K and V in registers, so the chunk is read from HBM exactly
 // once and never staged through LDS.
@@ -577,7 +578,6 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int qh = blockIdx.x, d = blockIdx.y * 64 + lane;
   const int G = a.n_heads / a.n_kv, kvh = qh / G, h = qh % G;
-
   // The step position is a vector load among the others (a scalar load's
   // wait would also cover the kernel arguments, putting its round trip ahead
   // of every load below); the loads of the first 64 splits clamp to the grid,
