@@ -1092,6 +1092,13 @@ static void dev_attention(const float* q, const float* k, const float* v, int se
   free(ms);
 }
 
+/* The device-order attention of one query head (test entry point) and its
+ * chunk width. */
+int ho_attn_chunk(int seq, int hd, int n_kv) { return dev_attn_chunk(seq, hd, n_kv); }
+void ho_attention_dev(const float* q, const float* k, const float* v, int seq, int hd, int n_kv, float* out) {
+  dev_attention(q, k, v, seq, hd, n_kv, out);
+}
+
 /* ------------------------------------------------------------------------- */
 /* model                                                                     */
 /* ------------------------------------------------------------------------- */

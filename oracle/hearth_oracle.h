@@ -64,6 +64,11 @@ void ho_silu(float* x, int64_t n);                                              
 void ho_softmax(float* x, int64_t n);                                             /* :308-351 */
 void ho_attention(const float* q, const float* k, const float* v, int seq_len, int head_dim,
                   float* out, float* scratch);                                    /* :353-406 */
+/* The same attention in the device's grouping (split chunks of ho_attn_chunk
+ * positions, the kernels' butterflies and trees), for the tests. */
+int ho_attn_chunk(int seq_len, int head_dim, int n_kv_heads);
+void ho_attention_dev(const float* q, const float* k, const float* v, int seq_len, int head_dim, int n_kv_heads,
+                      float* out);
 
 /* ---- Hadamard fold (qwen35.rs:51-118) ---- */
 void ho_wht(float* x, int64_t n);                         /* walsh_hadamard_in_place :51-68 */

@@ -64,6 +64,8 @@ def load() -> C.CDLL:
         "ho_silu": (None, [f32p, C.c_int64]),
         "ho_softmax": (None, [f32p, C.c_int64]),
         "ho_attention": (None, [f32p, f32p, f32p, C.c_int, C.c_int, f32p, f32p]),
+        "ho_attn_chunk": (C.c_int, [C.c_int, C.c_int, C.c_int]),
+        "ho_attention_dev": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, f32p]),
         "ho_sample_greedy_dense": (C.c_uint32, [f32p, C.c_int64, u32p, C.c_int64, C.c_float]),
         "ho_argmax_first": (C.c_uint32, [f32p, C.c_int64]),
         "ho_name_key": (C.c_uint64, [C.c_uint64, C.c_char_p]),

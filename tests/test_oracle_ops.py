@@ -168,3 +168,33 @@ def test_device_order_matches_reference_order(oracle):
     scr = np.zeros(seq, np.float32)
     lib.ho_attention(q.ctypes.data, k.ctypes.data, v.ctypes.data, seq, hd, out.ctypes.data, scr.ctypes.data)
     assert np.allclose(out, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_device_order_attention_widths(oracle):
+    """The device-order attention (the split kernels' grouping) against float64
+    softmax attention at both chunk widths.  The width rule: 8192/hd positions
+    per split, twice that once ceil(seq / (8192/hd)) * n_kv exceeds 256 (the
+    MI355X CU count), checked against its closed form at the boundary."""
+    lib = oracle.load()
+    for hd, n_kv in ((128, 8), (256, 4), (128, 32)):
+        c = 8192 // hd
+        edge = c * (256 // n_kv)           # longest sequence on the narrow width
+        assert lib.ho_attn_chunk(edge, hd, n_kv) == c
+        assert lib.ho_attn_chunk(edge + 1, hd, n_kv) == 2 * c
+        assert lib.ho_attn_chunk(1, hd, n_kv) == c
+    rng = np.random.default_rng(8)
+    for hd, n_kv, seq in ((128, 8, 2048), (128, 8, 2049), (128, 8, 2177), (256, 4, 2049), (256, 4, 300),
+                          (128, 32, 600)):
+        q = rng.standard_normal(hd).astype(np.float32)
+        k = rng.standard_normal((seq, hd)).astype(np.float32)
+        v = rng.standard_normal((seq, hd)).astype(np.float32)
+        s = k.astype(np.float64) @ q / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        ref = (p / p.sum()) @ v
+        out = np.zeros(hd, np.float32)
+        lib.ho_attention_dev(q.ctypes.data, k.ctypes.data, v.ctypes.data, seq, hd, n_kv, out.ctypes.data)
+        assert np.allclose(out, ref, rtol=1e-4, atol=1e-5), (hd, n_kv, seq, np.abs(out - ref).max())
+        # a dropped term breaks it: the same data one position shorter differs
+        out2 = np.zeros(hd, np.float32)
+        lib.ho_attention_dev(q.ctypes.data, k.ctypes.data, v.ctypes.data, seq - 1, hd, n_kv, out2.ctypes.data)
+        assert not np.allclose(out2, ref, rtol=1e-4, atol=1e-5)
