@@ -576,8 +576,13 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   float* pw = wm + a.max_splits;           // 4 x 64
   float* sL = pw + 256;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int qh = blockIdx.x, d = blockIdx.y * 64 + lane;
-  const int G = a.n_heads / a.n_kv, kvh = qh / G, h = qh % G;
+  const int G = a.n_heads / a.n_kv;
+  // workgroup id -> (kv head, query head in the group, 64-column slice), kv
+  // head fastest: with round-robin dispatch the merge of kv head k runs on the
+  // XCD whose split workgroups wrote its partials (split ids also put the kv
+  // head fastest)
+  const int kvh = (int)blockIdx.x % a.n_kv, rest = (int)blockIdx.x / a.n_kv;
+  const int h = rest % G, qh = kvh * G + h, d = (rest / G) * 64 + lane;
   // The step position is a vector load among the others (a scalar load's
   // wait would also cover the kernel arguments, putting its round trip ahead
   // of every load below); the loads of the first 64 splits clamp to the grid,
@@ -1647,11 +1652,11 @@ int hh_attn_launch(const AttnArgs& a, hipStream_t s) {
   if (a.hd == 128) {
     if (a.kv_q8) split(T128{}, std::true_type{});
     else split(T128{}, std::false_type{});
-    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_heads, 2), dim3(256), merge_lds, s, a);
+    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_heads * 2), dim3(256), merge_lds, s, a);
   } else {
     if (a.kv_q8) split(T256{}, std::true_type{});
     else split(T256{}, std::false_type{});
-    hipLaunchKernelGGL(k_attn_merge<256>, dim3(a.n_heads, 4), dim3(256), merge_lds, s, a);
+    hipLaunchKernelGGL(k_attn_merge<256>, dim3(a.n_heads * 4), dim3(256), merge_lds, s, a);
   }
   return ok();
 }
