@@ -285,27 +285,44 @@ template <int N> HH_DEV float pairwise_tree(float* t) {
 // its loads need no branch (never written).
 __device__ __align__(32) float attn_zero_row[8];   // also a zero StepState stand-in (state_lanes)
 
-// Q8_0 KV rows (KV8): the cache holds int8 values [n_kv][max_seq][hd] followed
-// by the f16 block scales [n_kv][max_seq][hd/32].  A lane's float4 slice of a
-// row is its 4 int8 times the block's f16 scale, exactly the f32 value
-// attention_q8_0 (ops.rs:946-1030) multiplies.
+// Q8_0 KV rows (KV8): the cache holds int8 values for [n_kv][max_seq] rows of
+// hd, then their f16 block scales (hd/32 per row); max_seq is a multiple of 64.
+// Rows are stored in 64-row blocks laid out for the attention split's lanes:
+// in a block, row j = i*RPI + sub (RPI = 512 / (hd/4) rows per pass of a
+// 512-lane workgroup) keeps its 4-byte slice c (elements 4c .. 4c+3) at
+// ((sub*(hd/4) + c)*NRB + i)*4, NRB = 64/RPI, and its scale of block cb at
+// (sub*(hd/32) + cb)*NRB + i.  A lane (sub, c) then finds the slices of its
+// rows i, i+1, .. side by side: 4 rows in one 16-byte load, their scales in
+// one 8-byte load.  A slice's value is its 4 int8 times the block's f16 scale,
+// exactly the f32 value attention_q8_0 (ops.rs:946-1030) multiplies.
+HH_DEV float4 kv_dequant4(uint32_t v, float s) {
+  return make_float4((float)(int8_t)(v & 0xff) * s, (float)(int8_t)((v >> 8) & 0xff) * s,
+                     (float)(int8_t)((v >> 16) & 0xff) * s, (float)(int8_t)(v >> 24) * s);
+}
 struct KvQ8 {
   int8_t* q;
   uint16_t* d;
   HH_DEV KvQ8(float* cache, int n_kv, int max_seq, int hd)
       : q((int8_t*)cache), d((uint16_t*)((int8_t*)cache + (size_t)n_kv * max_seq * hd)) {}
-  // the slice of row `row`, or zeros read from attn_zero_row when !held
-  HH_DEV float4 load_or_zero(size_t row, int hd, int c, bool held) const {
-    const uint32_t v = *(held ? (const uint32_t*)(q + row * hd + 4 * c) : (const uint32_t*)attn_zero_row);
-    const float s = h2f(*(held ? d + row * (hd / 32) + (c >> 3) : (const uint16_t*)attn_zero_row));
-    return make_float4((float)(int8_t)(v & 0xff) * s, (float)(int8_t)((v >> 8) & 0xff) * s,
-                       (float)(int8_t)((v >> 16) & 0xff) * s, (float)(int8_t)(v >> 24) * s);
+  // byte offset of row `row`'s slice c (row = kvh*max_seq + p)
+  static HH_DEV size_t qoff(size_t row, int hd, int c) {
+    const int R = 512 / (hd / 4), nrb = 64 / R, j = (int)(row & 63);
+    return (row >> 6) * 64 * (size_t)hd + ((size_t)((j % R) * (hd / 4) + c) * nrb + j / R) * 4;
   }
-  HH_DEV float4 load(size_t row, int hd, int c) const {   // row = kvh*max_seq + p, lane slice c
-    const uint32_t v = *(const uint32_t*)(q + row * hd + 4 * c);
-    const float s = h2f(d[row * (hd / 32) + (c >> 3)]);
-    return make_float4((float)(int8_t)(v & 0xff) * s, (float)(int8_t)((v >> 8) & 0xff) * s,
-                       (float)(int8_t)((v >> 16) & 0xff) * s, (float)(int8_t)(v >> 24) * s);
+  // index of row `row`'s scale of 32-block cb
+  static HH_DEV size_t doff(size_t row, int hd, int cb) {
+    const int R = 512 / (hd / 4), nrb = 64 / R, j = (int)(row & 63);
+    return (row >> 6) * 64 * (size_t)(hd / 32) + (size_t)((j % R) * (hd / 32) + cb) * nrb + j / R;
+  }
+  HH_DEV float4 load(size_t row, int hd, int c) const {   // lane slice c of one row
+    return kv_dequant4(*(const uint32_t*)(q + qoff(row, hd, c)), h2f(d[doff(row, hd, c >> 3)]));
+  }
+  // the slices c of rows row, row + RPI, row + 2 RPI, row + 3 RPI (row's block
+  // position a multiple of 4 passes): 16 bytes and four scales, or zeros
+  // from attn_zero_row when !ok
+  HH_DEV void load4(size_t row, int hd, int c, bool ok, uint4& v, uint2& sc) const {
+    v = *(ok ? (const uint4*)(q + qoff(row, hd, c)) : (const uint4*)attn_zero_row);
+    sc = *(ok ? (const uint2*)(d + doff(row, hd, c >> 3)) : (const uint2*)attn_zero_row);
   }
 };
 
@@ -329,8 +346,8 @@ HH_DEV float4 kv_q8_store(float4 x, const KvQ8& kv, size_t row, int hd, int c, b
     out[i] = (float)q * d;
   }
   if (write) {
-    *(uint32_t*)(kv.q + row * hd + 4 * c) = word;
-    if ((c & 7) == 0) kv.d[row * (hd / 32) + (c >> 3)] = (uint16_t)h;
+    *(uint32_t*)(kv.q + KvQ8::qoff(row, hd, c)) = word;
+    if ((c & 7) == 0) kv.d[KvQ8::doff(row, hd, c >> 3)] = (uint16_t)h;
   }
   return make_float4(out[0], out[1], out[2], out[3]);
 }
@@ -408,14 +425,35 @@ HH_DEV void attn_split_body(const AttnArgs& a, int G, int seq, int pos, bool pre
   // count of loads in flight, and its conservative wait would hold step 3's q
   // prep until every K/V row had landed.
   float4 kr[NR], vr[NR];
+  if constexpr (KV8) {
+    // four rows per 16-byte load (the blocked Q8_0 layout, KvQ8); a group's
+    // 64-row block lies in the cache when the group starts below max_seq
+    static_assert(NR % 4 == 0, "four rows per load");
+    uint4 kw[NR / 4], vw[NR / 4];
+    uint2 ks[NR / 4], vs[NR / 4];
 #pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    const int j = i * RPI + sub;
-    const bool held = j < np && p0 + j != pos;
-    if constexpr (KV8) {
-      kr[i] = kq.load_or_zero(row0 + p0 + j, HD, c, held);
-      vr[i] = vq.load_or_zero(row0 + p0 + j, HD, c, held);
-    } else {
+    for (int g = 0; g < NR / 4; ++g) {
+      const bool ok = p0 + 4 * g * RPI < a.max_seq;
+      kq.load4(row0 + p0 + 4 * g * RPI + sub, HD, c, ok, kw[g], ks[g]);
+      vq.load4(row0 + p0 + 4 * g * RPI + sub, HD, c, ok, vw[g], vs[g]);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int j = i * RPI + sub, g = i / 4, t = i % 4;
+      const bool held = j < np && p0 + j != pos;
+      const uint32_t kb = t == 0 ? kw[g].x : t == 1 ? kw[g].y : t == 2 ? kw[g].z : kw[g].w;
+      const uint32_t vb = t == 0 ? vw[g].x : t == 1 ? vw[g].y : t == 2 ? vw[g].z : vw[g].w;
+      const uint32_t kd = ((t < 2 ? ks[g].x : ks[g].y) >> (16 * (t & 1))) & 0xffffu;
+      const uint32_t vd = ((t < 2 ? vs[g].x : vs[g].y) >> (16 * (t & 1))) & 0xffffu;
+      const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+      kr[i] = held ? kv_dequant4(kb, h2f(kd)) : zero;
+      vr[i] = held ? kv_dequant4(vb, h2f(vd)) : zero;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int j = i * RPI + sub;
+      const bool held = j < np && p0 + j != pos;
       kr[i] = *(held ? (const float4*)(kg + (size_t)(p0 + j) * HD) : (const float4*)attn_zero_row);
       vr[i] = *(held ? (const float4*)(vg + (size_t)(p0 + j) * HD) : (const float4*)attn_zero_row);
     }
@@ -1581,10 +1619,11 @@ __global__ void k_kv_synth_q8(uint64_t key, int n_pos, int n_kv, int hd, int max
     am = fmaxf(am, fabsf(v[j]));
   }
   const float sc = q8_scale(am), rc = q8_rcp(sc);
-  int8_t* q = (int8_t*)cache + ((size_t)h * max_seq + p) * hd + blk * 32;
+  const size_t row = (size_t)h * max_seq + p;
+  int8_t* q = (int8_t*)cache;
   uint16_t* d = (uint16_t*)((int8_t*)cache + (size_t)n_kv * max_seq * hd);
-  for (int j = 0; j < 32; ++j) q[j] = (int8_t)q8_round_r(v[j], sc, rc);
-  d[((size_t)h * max_seq + p) * nb + blk] = (uint16_t)f2h(sc);
+  for (int j = 0; j < 32; ++j) q[KvQ8::qoff(row, hd, blk * 8 + j / 4) + j % 4] = (int8_t)q8_round_r(v[j], sc, rc);
+  d[KvQ8::doff(row, hd, blk)] = (uint16_t)f2h(sc);
 }
 
 inline int ok() { return hipGetLastError() == hipSuccess ? 0 : 1; }
