@@ -97,9 +97,9 @@ struct AttnArgs {
   float* out_f32;        // optional [n_heads*hd]
   uint8_t* act_out;      // optional packed activation (K = n_heads*hd)
   int act_fmt;
-  int kv_q8;             // caches hold Q8_0 rows in 64-row blocks (max_seq a multiple of 64): int8
-                         // [n_kv][max_seq][hd] then f16 scales [..][hd/32], each block interleaved so
-                         // one 16-byte load holds 4 bytes of 4 rows (KvQ8::qoff / doff)
+  int kv_q8;             // caches hold Q8_0 rows in 64-row blocks (max_seq a multiple of 64): each
+                         // block's 64*hd int8 values, then its f16 scales [64][hd/32], the values
+                         // interleaved so one 16-byte load holds 4 bytes of 4 rows (KvQ8::qoff / doff)
 };
 int hh_attn_launch(const AttnArgs& a, hipStream_t s);
 int hh_kv_synth_q8_launch(uint64_t key, int n_pos, int n_kv, int hd, int max_seq, float cs, float* cache,

@@ -302,17 +302,19 @@ HH_DEV float4 kv_dequant4(uint32_t v, float s) {
 struct KvQ8 {
   int8_t* q;
   uint16_t* d;
-  HH_DEV KvQ8(float* cache, int n_kv, int max_seq, int hd)
-      : q((int8_t*)cache), d((uint16_t*)((int8_t*)cache + (size_t)n_kv * max_seq * hd)) {}
-  // byte offset of row `row`'s slice c (row = kvh*max_seq + p)
+  HH_DEV KvQ8(float* cache, int /*n_kv*/, int /*max_seq*/, int hd) : q((int8_t*)cache), d((uint16_t*)cache) {}
+  // A 64-row block holds its 64*hd int8 values, then their 64*hd/32 f16 scales
+  // (68*hd bytes); inside a block the values of 4 rows that one lane reads
+  // together sit side by side.  Byte offset of row `row`'s slice c
+  // (row = kvh*max_seq + p):
   static HH_DEV size_t qoff(size_t row, int hd, int c) {
     const int R = 512 / (hd / 4), nrb = 64 / R, j = (int)(row & 63);
-    return (row >> 6) * 64 * (size_t)hd + ((size_t)((j % R) * (hd / 4) + c) * nrb + j / R) * 4;
+    return (row >> 6) * 68 * (size_t)hd + ((size_t)((j % R) * (hd / 4) + c) * nrb + j / R) * 4;
   }
-  // index of row `row`'s scale of 32-block cb
+  // f16 index (from the cache base) of row `row`'s scale of 32-block cb
   static HH_DEV size_t doff(size_t row, int hd, int cb) {
     const int R = 512 / (hd / 4), nrb = 64 / R, j = (int)(row & 63);
-    return (row >> 6) * 64 * (size_t)(hd / 32) + (size_t)((j % R) * (hd / 32) + cb) * nrb + j / R;
+    return (row >> 6) * 34 * (size_t)hd + 32 * (size_t)hd + (size_t)((j % R) * (hd / 32) + cb) * nrb + j / R;
   }
   HH_DEV float4 load(size_t row, int hd, int c) const {   // lane slice c of one row
     return kv_dequant4(*(const uint32_t*)(q + qoff(row, hd, c)), h2f(d[doff(row, hd, c >> 3)]));
@@ -1620,10 +1622,9 @@ __global__ void k_kv_synth_q8(uint64_t key, int n_pos, int n_kv, int hd, int max
   }
   const float sc = q8_scale(am), rc = q8_rcp(sc);
   const size_t row = (size_t)h * max_seq + p;
-  int8_t* q = (int8_t*)cache;
-  uint16_t* d = (uint16_t*)((int8_t*)cache + (size_t)n_kv * max_seq * hd);
-  for (int j = 0; j < 32; ++j) q[KvQ8::qoff(row, hd, blk * 8 + j / 4) + j % 4] = (int8_t)q8_round_r(v[j], sc, rc);
-  d[KvQ8::doff(row, hd, blk)] = (uint16_t)f2h(sc);
+  const KvQ8 kv(cache, n_kv, max_seq, hd);
+  for (int j = 0; j < 32; ++j) kv.q[KvQ8::qoff(row, hd, blk * 8 + j / 4) + j % 4] = (int8_t)q8_round_r(v[j], sc, rc);
+  kv.d[KvQ8::doff(row, hd, blk)] = (uint16_t)f2h(sc);
 }
 
 inline int ok() { return hipGetLastError() == hipSuccess ? 0 : 1; }
