@@ -1328,6 +1328,17 @@ size_t hh_gemv_lds(int fmt, int K, int rows_total_per_wg) {
   return (b + 15) & ~(size_t)15;
 }
 
+// EPI_SILU workgroups for nblk 32-row gate blocks.  Past two blocks per
+// workgroup every workgroup takes the same count: 27B (544 blocks) on 182
+// workgroups of 3 instead of 256 of 2 or 3, gate+up 17.01 -> 16.57 us, step
+// 3.331 -> 3.315 ms.  Two or fewer stay on up to 256 workgroups (8B and 9B,
+// 384 blocks: even shares measured the same).
+static int silu_grid(int nblk) {
+  if (nblk <= 512) return std::min(nblk, 256);
+  const int per = (nblk + 255) / 256;
+  return (nblk + per - 1) / per;
+}
+
 int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   int el = hh_unit_el(fmt);
   if (a.K % el != 0) return 1;
@@ -1359,7 +1370,7 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
   if (epi == EPI_SILU) {
     if (a.half_rows % 32 != 0) return 1;
     const int nblk = a.half_rows / 32;
-    n_wg = std::min(nblk, 256);
+    n_wg = silu_grid(nblk);
     rows_total = 64 * ((nblk + n_wg - 1) / n_wg);   // the largest share
   } else {
     n_wg = (a.n_rows + a.rows_per_wg - 1) / a.rows_per_wg;
@@ -1399,6 +1410,6 @@ int hh_gemv_launch(int fmt, int pro, int epi, GemvArgs a, hipStream_t s) {
 }
 
 int hh_gemv_grid(int epi, const GemvArgs& a) {
-  if (epi == EPI_SILU) return std::min(a.half_rows / 32, 256);
+  if (epi == EPI_SILU) return silu_grid(a.half_rows / 32);
   return (a.n_rows + a.rows_per_wg - 1) / a.rows_per_wg;
 }
