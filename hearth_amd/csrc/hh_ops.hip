@@ -427,30 +427,20 @@ HH_DEV void attn_split_body(const AttnArgs& a, int G, int seq, int pos, bool pre
   // count of loads in flight, and its conservative wait would hold step 3's q
   // prep until every K/V row had landed.
   float4 kr[NR], vr[NR];
+  // Q8_0 rows stay as loaded (four rows per 16-byte load, the blocked layout of
+  // KvQ8) until their first use: K before the scores, V before o.  Dequantizing
+  // here would wait for the whole stream before the q prep below.
+  uint4 kw[NR / 4], vw[NR / 4];
+  uint2 ks[NR / 4], vs[NR / 4];
+  static_assert(NR % 4 == 0, "four rows per load");
   if constexpr (KV8) {
-    // four rows per 16-byte load (the blocked Q8_0 layout, KvQ8); a group's
-    // 64-row block lies in the cache when the group starts below max_seq
-    static_assert(NR % 4 == 0, "four rows per load");
-    uint4 kw[NR / 4], vw[NR / 4];
-    uint2 ks[NR / 4], vs[NR / 4];
+    // a group's 64-row block lies in the cache when the group starts below max_seq
 #pragma unroll
-    for (int g = 0; g < NR / 4; ++g) {
-      const bool ok = p0 + 4 * g * RPI < a.max_seq;
-      kq.load4(row0 + p0 + 4 * g * RPI + sub, HD, c, ok, kw[g], ks[g]);
-      vq.load4(row0 + p0 + 4 * g * RPI + sub, HD, c, ok, vw[g], vs[g]);
-    }
+    for (int g = 0; g < NR / 4; ++g)
+      kq.load4(row0 + p0 + 4 * g * RPI + sub, HD, c, p0 + 4 * g * RPI < a.max_seq, kw[g], ks[g]);
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      const int j = i * RPI + sub, g = i / 4, t = i % 4;
-      const bool held = j < np && p0 + j != pos;
-      const uint32_t kb = t == 0 ? kw[g].x : t == 1 ? kw[g].y : t == 2 ? kw[g].z : kw[g].w;
-      const uint32_t vb = t == 0 ? vw[g].x : t == 1 ? vw[g].y : t == 2 ? vw[g].z : vw[g].w;
-      const uint32_t kd = ((t < 2 ? ks[g].x : ks[g].y) >> (16 * (t & 1))) & 0xffffu;
-      const uint32_t vd = ((t < 2 ? vs[g].x : vs[g].y) >> (16 * (t & 1))) & 0xffffu;
-      const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
-      kr[i] = held ? kv_dequant4(kb, h2f(kd)) : zero;
-      vr[i] = held ? kv_dequant4(vb, h2f(vd)) : zero;
-    }
+    for (int g = 0; g < NR / 4; ++g)
+      vq.load4(row0 + p0 + 4 * g * RPI + sub, HD, c, p0 + 4 * g * RPI < a.max_seq, vw[g], vs[g]);
   } else {
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
@@ -480,12 +470,28 @@ HH_DEV void attn_split_body(const AttnArgs& a, int G, int seq, int pos, bool pre
         *(float4*)(a.k_cache + (size_t)kvh * hstride + (size_t)pos * HD + 4 * c) = kn4;
         *(float4*)(a.v_cache + (size_t)kvh * hstride + (size_t)pos * HD + 4 * c) = vn4;
       }
+      if constexpr (!KV8) {
 #pragma unroll
-      for (int i = 0; i < NR; ++i) {
-        if (p0 + i * RPI + sub == pos) { kr[i] = kn4; vr[i] = vn4; }
+        for (int i = 0; i < NR; ++i) {
+          if (p0 + i * RPI + sub == pos) { kr[i] = kn4; vr[i] = vn4; }
+        }
       }
     }
   }
+  // row i of the lane from its load group (rows absent from the chunk, and the
+  // new position, are zero; the new row is then put in from registers)
+  auto unpack = [&](const uint4* w, const uint2* sc, float4* r, float4 nw) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int j = i * RPI + sub, g = i / 4, t = i % 4;
+      const bool held = j < np && p0 + j != pos;
+      const uint32_t b = t == 0 ? w[g].x : t == 1 ? w[g].y : t == 2 ? w[g].z : w[g].w;
+      const uint32_t d = ((t < 2 ? sc[g].x : sc[g].y) >> (16 * (t & 1))) & 0xffffu;
+      r[i] = held ? kv_dequant4(b, h2f(d)) : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (has_new && p0 + j == pos) r[i] = nw;
+    }
+  };
+  if constexpr (KV8) unpack(kw, ks, kr, kn4);
   // 4. scores (ops.rs:362-374), four heads per pass
   const float inv_sqrt = 1.0f / sqrtf((float)HD);
   constexpr int NV = 4 * NR;                          // values per lane per pass
@@ -534,6 +540,7 @@ HH_DEV void attn_split_body(const AttnArgs& a, int G, int seq, int pos, bool pre
     }
   }
   __syncthreads();
+  if constexpr (KV8) unpack(vw, vs, vr, vn4);
   // 6. o = sum_j e_j v_j
   const size_t pbase = ((size_t)kvh * a.max_splits + s) * G;
   for (int hg = 0; hg < G; hg += 4) {
