@@ -442,11 +442,18 @@ HH_DEV void attn_split_body(const AttnArgs& a, int G, int seq, int pos, bool pre
     for (int g = 0; g < NR / 4; ++g)
       vq.load4(row0 + p0 + 4 * g * RPI + sub, HD, c, p0 + 4 * g * RPI < a.max_seq, vw[g], vs[g]);
   } else {
+    // every K row before the V rows: loads return in issue order, so the scores
+    // need not wait for V
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       const int j = i * RPI + sub;
       const bool held = j < np && p0 + j != pos;
       kr[i] = *(held ? (const float4*)(kg + (size_t)(p0 + j) * HD) : (const float4*)attn_zero_row);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int j = i * RPI + sub;
+      const bool held = j < np && p0 + j != pos;
       vr[i] = *(held ? (const float4*)(vg + (size_t)(p0 + j) * HD) : (const float4*)attn_zero_row);
     }
   }
