@@ -987,17 +987,26 @@ __global__ __launch_bounds__(NTA) void k_attn_prefill_split(const float* __restr
   constexpr int NV = 4 * NR;
   const int rsp = rs_perm<NV, LPR / 2>(lane), pi = rsp % NR, ph = rsp / NR;
   float4 kr[NR], vr[NR];
+  // every K row before the V rows (the scores need only K)
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
-    const int j = i * RPI + sub, jk = (i ^ pi) * RPI + sub;
+    const int jk = (i ^ pi) * RPI + sub;
     kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    vr[i] = kr[i];
     if constexpr (KV8) {
       const size_t r = (size_t)kvh * max_seq + p0;
       if (jk < np_max) kr[i] = KvQ8(const_cast<float*>(k_cache), n_kv, max_seq, HD).load(r + jk, HD, cc);
-      if (j < np_max) vr[i] = KvQ8(const_cast<float*>(v_cache), n_kv, max_seq, HD).load(r + j, HD, cc);
     } else {
       if (jk < np_max) kr[i] = *(const float4*)(kg + (size_t)(p0 + jk) * HD);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int j = i * RPI + sub;
+    vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (KV8) {
+      const size_t r = (size_t)kvh * max_seq + p0;
+      if (j < np_max) vr[i] = KvQ8(const_cast<float*>(v_cache), n_kv, max_seq, HD).load(r + j, HD, cc);
+    } else {
       if (j < np_max) vr[i] = *(const float4*)(vg + (size_t)(p0 + j) * HD);
     }
   }
