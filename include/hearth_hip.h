@@ -175,7 +175,8 @@ typedef struct {
 enum { HH_HAD_LATENT_EMBD = 1, HH_HAD_TIED_OUTPUT = 2 };
 
 /* Allocates every weight (native GGUF block layout, uploaded once), the KV
- * cache (f32 or Q8_0 rows, [layer][kv_head][max_seq][hd], kvcache.rs:11-57), the recurrent state
+ * cache (f32 [layer][kv_head][max_seq][hd], or the same rows as Q8_0 blocks in a device-internal
+ * 64-row interleaved layout; kvcache.rs:11-57), the recurrent state
  * and the step buffers.  Replaces LlamaModel::load's GPU branch (mod.rs:238-282,
  * model/gpu.rs:8-50). */
 int hh_model_create(hh_ctx* ctx, const hh_model_config* cfg, hh_model** out);
