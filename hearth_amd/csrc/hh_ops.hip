@@ -285,13 +285,13 @@ template <int N> HH_DEV float pairwise_tree(float* t) {
 // its loads need no branch (never written).
 __device__ __align__(32) float attn_zero_row[8];   // also a zero StepState stand-in (state_lanes)
 
-// Q8_0 KV rows (KV8): the cache holds int8 values for [n_kv][max_seq] rows of
-// hd, then their f16 block scales (hd/32 per row); max_seq is a multiple of 64.
-// Rows are stored in 64-row blocks laid out for the attention split's lanes:
-// in a block, row j = i*RPI + sub (RPI = 512 / (hd/4) rows per pass of a
+// Q8_0 KV rows (KV8): the [n_kv][max_seq] rows of hd values (max_seq a
+// multiple of 64) are stored in 64-row blocks of 68*hd bytes, the block's int8
+// values then its f16 block scales (hd/32 per row), laid out for the attention
+// split's lanes: in a block, row j = i*RPI + sub (RPI = 512 / (hd/4) rows per pass of a
 // 512-lane workgroup) keeps its 4-byte slice c (elements 4c .. 4c+3) at
 // ((sub*(hd/4) + c)*NRB + i)*4, NRB = 64/RPI, and its scale of block cb at
-// (sub*(hd/32) + cb)*NRB + i.  A lane (sub, c) then finds the slices of its
+// f16 index (sub*(hd/32) + cb)*NRB + i after the block's values.  A lane (sub, c) then finds the slices of its
 // rows i, i+1, .. side by side: 4 rows in one 16-byte load, their scales in
 // one 8-byte load.  A slice's value is its 4 int8 times the block's f16 scale,
 // exactly the f32 value attention_q8_0 (ops.rs:946-1030) multiplies.
